@@ -1,0 +1,293 @@
+// qlin_api.cpp -- the C ABI (include/qlin.h): host-side argument validation and dispatch.
+//
+// Validation runs entirely on the host, before any HIP call, and returns a qlin_status where the
+// reference launchers (AI/codes/local-llm/src/backend/cuda/ops/launch.cu) return void.  The facade
+// entry points mirror TensorTool (src/tensor/TensorTool.cpp) including its rejection rules.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+
+#include "qlin.h"
+#include "qlin_internal.hpp"
+
+namespace qlin {
+
+const DeviceInfo &device_info() {
+    static DeviceInfo infos[64];
+    static std::atomic<bool> ready[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        static DeviceInfo fallback;
+        return fallback;
+    }
+    if (!ready[dev].load(std::memory_order_acquire)) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            infos[dev].cu_count = cus;
+        ready[dev].store(true, std::memory_order_release);
+    }
+    return infos[dev];
+}
+
+}  // namespace qlin
+
+namespace {
+
+std::atomic<hipStream_t> g_stream{nullptr};
+
+hipStream_t stream() { return g_stream.load(std::memory_order_relaxed); }
+
+bool known_weight_type(int t) {
+    return t == QLIN_TYPE_Q4_0 || t == QLIN_TYPE_Q5_0 || t == QLIN_TYPE_Q8_0 || t == QLIN_TYPE_Q4_K ||
+           t == QLIN_TYPE_Q6_K;
+}
+
+int elems_of(int t) {
+    switch (t) {
+        case QLIN_TYPE_Q4_0: case QLIN_TYPE_Q5_0: case QLIN_TYPE_Q8_0: case QLIN_TYPE_Q8_1: return 32;
+        case QLIN_TYPE_Q4_K: case QLIN_TYPE_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+int bytes_of(int t) {
+    switch (t) {
+        case QLIN_TYPE_Q4_0: return 18;
+        case QLIN_TYPE_Q5_0: return 22;
+        case QLIN_TYPE_Q8_0: return 34;
+        case QLIN_TYPE_Q8_1: return 36;
+        case QLIN_TYPE_Q4_K: return 144;
+        case QLIN_TYPE_Q6_K: return 210;
+        default: return 0;
+    }
+}
+
+size_t min_row_bytes(int t, int in_dim) {
+    const int be = elems_of(t);
+    if (be == 0 || in_dim < 0 || in_dim % be) return 0;
+    return static_cast<size_t>(in_dim / be) * static_cast<size_t>(bytes_of(t));
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int launched(hipError_t e) { return e == hipSuccess ? QLIN_OK : QLIN_ERR_LAUNCH; }
+
+// Shared checks of a [out_dim, in_dim] weight with the given row stride.
+int check_weight(int type, const uint8_t *w, size_t row_bytes, int out_dim, int in_dim) {
+    if (!known_weight_type(type)) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (out_dim < 0 || in_dim <= 0 || in_dim % elems_of(type)) return QLIN_ERR_SHAPE;
+    if (row_bytes < min_row_bytes(type, in_dim)) return QLIN_ERR_ROW_BYTES;
+    if (out_dim > 0 && !w) return QLIN_ERR_NULL;
+    if (!aligned(w, 2) || (out_dim > 1 && row_bytes % 2)) return QLIN_ERR_ALIGN;
+    return QLIN_OK;
+}
+
+int check_f32(const float *p, bool needed) {
+    if (needed && !p) return QLIN_ERR_NULL;
+    if (!aligned(p, 4)) return QLIN_ERR_ALIGN;
+    return QLIN_OK;
+}
+
+int gemv_common(int type, const uint8_t *w, size_t rb, const float *x, float *y, int out_dim, int in_dim, int m,
+                bool add) {
+    int rc = check_weight(type, w, rb, out_dim, in_dim);
+    if (rc) return rc;
+    if (m < 0) return QLIN_ERR_SHAPE;
+    const bool work = out_dim > 0 && m > 0;
+    if ((rc = check_f32(x, work)) || (rc = check_f32(y, work))) return rc;
+    if (!work) return QLIN_OK;
+    return launched(qlin::gemv(type, w, rb, x, y, out_dim, in_dim, m, add, stream()));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *qlin_status_string(int status) {
+    switch (status) {
+        case QLIN_OK: return "ok";
+        case QLIN_ERR_UNSUPPORTED_TYPE: return "unsupported weight type";
+        case QLIN_ERR_SHAPE: return "invalid shape (negative dimension or in_dim not a multiple of the block)";
+        case QLIN_ERR_NULL: return "null pointer";
+        case QLIN_ERR_ROW_BYTES: return "row or expert stride smaller than its packed data";
+        case QLIN_ERR_LIMIT: return "argument beyond a documented limit";
+        case QLIN_ERR_LAUNCH: return "HIP launch failed";
+        case QLIN_ERR_ALIGN: return "misaligned pointer";
+        default: return "unknown status";
+    }
+}
+
+const char *qlin_version(void) { return "qlin 0.1 gfx950"; }
+
+int qlin_set_stream(void *s) {
+    g_stream.store(static_cast<hipStream_t>(s), std::memory_order_relaxed);
+    return QLIN_OK;
+}
+
+void *qlin_get_stream(void) { return stream(); }
+
+int qlin_block_elems(int type) { return elems_of(type); }
+int qlin_block_bytes(int type) { return bytes_of(type); }
+size_t qlin_row_bytes(int type, int in_dim) { return min_row_bytes(type, in_dim); }
+
+int qlin_launch_quant_gemv(int type, const uint8_t *w, size_t rb, const float *x, float *y, int out_dim, int in_dim,
+                           int m) {
+    return gemv_common(type, w, rb, x, y, out_dim, in_dim, m, false);
+}
+
+int qlin_launch_quant_gemv_add(int type, const uint8_t *w, size_t rb, const float *x, float *y, int out_dim,
+                               int in_dim) {
+    return gemv_common(type, w, rb, x, y, out_dim, in_dim, 1, true);
+}
+
+int qlin_launch_quant_matmul(int type, const uint8_t *w, size_t rb, const float *x, float *y, int out_dim,
+                             int in_dim, int m) {
+    return gemv_common(type, w, rb, x, y, out_dim, in_dim, m, false);
+}
+
+size_t qlin_q8_1_row_bytes(int in_dim) {
+    return in_dim <= 0 ? 0 : static_cast<size_t>((in_dim + 31) / 32) * 36;
+}
+
+int qlin_launch_quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, int store_raw_sum) {
+    if (in_dim <= 0 || m < 0) return QLIN_ERR_SHAPE;
+    if (m == 0) return QLIN_OK;
+    int rc = check_f32(x, true);
+    if (rc) return rc;
+    if (!xq) return QLIN_ERR_NULL;
+    if (!aligned(xq, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::quantize_q8_1(x, xq, in_dim, m, store_raw_sum != 0, stream()));
+}
+
+int qlin_launch_quant_matmul_q8_1(int type, const uint8_t *w, size_t rb, const uint8_t *xq, float *y,
+                                  int out_dim, int in_dim, int m) {
+    int rc = check_weight(type, w, rb, out_dim, in_dim);
+    if (rc) return rc;
+    if (m < 0) return QLIN_ERR_SHAPE;
+    const bool work = out_dim > 0 && m > 0;
+    if (!work) return QLIN_OK;
+    if (!xq) return QLIN_ERR_NULL;
+    if (!aligned(xq, 2)) return QLIN_ERR_ALIGN;
+    if ((rc = check_f32(y, true))) return rc;
+    return launched(qlin::matmul_q8_1(type, w, rb, xq, y, out_dim, in_dim, m, stream()));
+}
+
+int qlin_launch_quant_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_rb, size_t u_rb,
+                             const float *x, float *act, int ffn_dim, int in_dim) {
+    int rc = check_weight(type, wg, g_rb, ffn_dim, in_dim);
+    if (rc || (rc = check_weight(type, wu, u_rb, ffn_dim, in_dim))) return rc;
+    const bool work = ffn_dim > 0;
+    if ((rc = check_f32(x, work)) || (rc = check_f32(act, work))) return rc;
+    if (!work) return QLIN_OK;
+    return launched(qlin::swiglu(type, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim, stream()));
+}
+
+int qlin_launch_quant_swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb,
+                                     size_t g_rb, size_t u_rb, const float *x, const int *ids, float *act, int k,
+                                     int ffn_dim, int in_dim) {
+    int rc = check_weight(type, wg, g_rb, ffn_dim, in_dim);
+    if (rc || (rc = check_weight(type, wu, u_rb, ffn_dim, in_dim))) return rc;
+    if (k < 0) return QLIN_ERR_SHAPE;
+    if (g_eb < g_rb * static_cast<size_t>(ffn_dim) || u_eb < u_rb * static_cast<size_t>(ffn_dim))
+        return QLIN_ERR_ROW_BYTES;
+    const bool work = ffn_dim > 0 && k > 0;
+    if ((rc = check_f32(x, work)) || (rc = check_f32(act, work))) return rc;
+    if (!work) return QLIN_OK;
+    if (!ids) return QLIN_ERR_NULL;
+    if (!aligned(ids, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::swiglu_indexed(type, wg, wu, g_eb, u_eb, g_rb, u_rb, x, ids, act, k, ffn_dim, in_dim,
+                                         stream()));
+}
+
+int qlin_launch_quant_down_f32_indexed_accum_ordered(int type, const uint8_t *wd, size_t d_eb, size_t d_rb,
+                                                     const float *act, const int *ids, const float *rw,
+                                                     float *out, int k, int hidden, int ffn_dim) {
+    int rc = check_weight(type, wd, d_rb, hidden, ffn_dim);
+    if (rc) return rc;
+    if (k < 0) return QLIN_ERR_SHAPE;
+    if (d_eb < d_rb * static_cast<size_t>(hidden)) return QLIN_ERR_ROW_BYTES;
+    const bool work = hidden > 0;
+    if ((rc = check_f32(out, work)) || (rc = check_f32(act, work && k > 0)) || (rc = check_f32(rw, work && k > 0)))
+        return rc;
+    if (!work) return QLIN_OK;
+    if (k > 0 && !ids) return QLIN_ERR_NULL;
+    if (!aligned(ids, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::down_indexed_ordered(type, wd, d_eb, d_rb, act, ids, rw, out, k, hidden, ffn_dim, stream()));
+}
+
+int qlin_launch_moe_router_topk(const float *logits, int *idx, float *w, int tokens, int n_experts, int k,
+                                float routed_scaling) {
+    if (tokens < 0 || k < 0 || n_experts <= 0) return QLIN_ERR_SHAPE;
+    if (n_experts > 256) return QLIN_ERR_LIMIT;
+    if (tokens == 0 || k == 0) return QLIN_OK;
+    int rc = check_f32(logits, true);
+    if (rc || (rc = check_f32(w, true))) return rc;
+    if (!idx) return QLIN_ERR_NULL;
+    if (!aligned(idx, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::router_topk(logits, idx, w, tokens, n_experts, k, routed_scaling, stream()));
+}
+
+static int dequant_common(int type, const uint8_t *src, void *out, int64_t n, bool f16) {
+    if (!known_weight_type(type)) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (n < 0 || n % elems_of(type)) return QLIN_ERR_SHAPE;
+    if (n == 0) return QLIN_OK;
+    if (!src || !out) return QLIN_ERR_NULL;
+    if (!aligned(src, 2) || !aligned(out, f16 ? 2 : 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::dequant(type, src, out, n, f16, stream()));
+}
+
+int qlin_launch_dequantize_to_f16(int type, const uint8_t *src, uint16_t *out, int64_t n) {
+    return dequant_common(type, src, out, n, true);
+}
+int qlin_launch_dequantize_q4k_to_f16(const uint8_t *src, uint16_t *out, int64_t n) {
+    return dequant_common(QLIN_TYPE_Q4_K, src, out, n, true);
+}
+int qlin_launch_dequantize_q80_to_f16(const uint8_t *src, uint16_t *out, int64_t n) {
+    return dequant_common(QLIN_TYPE_Q8_0, src, out, n, true);
+}
+int qlin_launch_dequantize_q50_to_f16(const uint8_t *src, uint16_t *out, int64_t n) {
+    return dequant_common(QLIN_TYPE_Q5_0, src, out, n, true);
+}
+int qlin_launch_dequantize_q6k_to_f16(const uint8_t *src, uint16_t *out, int64_t n) {
+    return dequant_common(QLIN_TYPE_Q6_K, src, out, n, true);
+}
+int qlin_launch_dequantize_to_f32(int type, const uint8_t *src, float *out, int64_t n) {
+    return dequant_common(type, src, out, n, false);
+}
+
+int qlin_gemm(int type, const uint8_t *w, size_t weight_bytes, const float *x, float *y, int out_dim, int in_dim,
+              int m) {
+    if (out_dim < 0) return QLIN_ERR_SHAPE;
+    const size_t rb = out_dim > 0 ? weight_bytes / static_cast<size_t>(out_dim) : min_row_bytes(type, in_dim);
+    return gemv_common(type, w, rb, x, y, out_dim, in_dim, m, false);
+}
+
+int qlin_moe_routed_decode_indexed(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                   int down_type, const uint8_t *down, size_t down_bytes, int n_experts, int ffn_dim,
+                                   int in_dim, int hidden, const float *x, const int *ids, const float *rw,
+                                   float *act, float *out, int k) {
+    // TensorTool.cpp:277-305, in the reference's order of checks.
+    if (!ids || !rw) return QLIN_ERR_NULL;
+    if (down_type != QLIN_TYPE_Q4_K && down_type != QLIN_TYPE_Q6_K && down_type != QLIN_TYPE_Q5_0 &&
+        down_type != QLIN_TYPE_Q8_0)
+        return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (gu_type != QLIN_TYPE_Q4_K && gu_type != QLIN_TYPE_Q6_K) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (n_experts <= 0 || ffn_dim <= 0 || in_dim <= 0 || hidden <= 0 || k < 0) return QLIN_ERR_SHAPE;
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const size_t d_rb = d_eb / static_cast<size_t>(hidden);
+    if (!act) return QLIN_ERR_NULL;
+    // the down projection is validated before anything is launched, so a rejection launches nothing
+    int rc = check_weight(down_type, down, d_rb, hidden, ffn_dim);
+    if (rc) return rc;
+    if ((rc = check_f32(out, true)) || (rc = check_f32(rw, k > 0))) return rc;
+    rc = qlin_launch_quant_swiglu_indexed(gu_type, gate, up, g_eb, g_eb, g_rb, g_rb, x, ids, act, k, ffn_dim,
+                                              in_dim);
+    if (rc) return rc;
+    return qlin_launch_quant_down_f32_indexed_accum_ordered(down_type, down, d_eb, d_rb, act, ids, rw, out, k,
+                                                            hidden, ffn_dim);
+}
+
+}  // extern "C"

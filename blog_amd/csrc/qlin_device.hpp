@@ -1,0 +1,142 @@
+// qlin_device.hpp -- device-side building blocks shared by the gfx950 kernels.
+//
+// GGUF block layouts (ggml type codes, little-endian fields), as the reference engine stores them
+// (AI/codes/local-llm/src/format/gguf/GgufFile.cpp:35-55, kernel.cu:1090-1185):
+//   Q4_0  32 elems / 18 B : d f16 | qs[16]            w = d*(q-8),  q = nibble (e<16 low, else high)
+//   Q5_0  32 elems / 22 B : d f16 | qh u32 | qs[16]   w = d*(q-16), q = nibble | bit e of qh << 4
+//   Q8_0  32 elems / 34 B : d f16 | int8 qs[32]       w = d*q
+//   Q4_K 256 elems / 144 B: d f16 | dmin f16 | scales[12] | qs[128]   w = d*sc*q - dmin*m
+//   Q6_K 256 elems / 210 B: ql[128] | qh[64] | int8 sc[16] | d f16    w = d*sc*q
+// Every per-element value below is computed with the canonical, non-contracted order
+// (no fused multiply-add), which is what makes the dequant kernels bit-exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qlin {
+
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8, T_Q8_1 = 9, T_Q4_K = 12, T_Q6_K = 14 };
+
+template <int T> struct Block;
+template <> struct Block<T_Q4_0> { static constexpr int elems = 32, bytes = 18; };
+template <> struct Block<T_Q5_0> { static constexpr int elems = 32, bytes = 22; };
+template <> struct Block<T_Q8_0> { static constexpr int elems = 32, bytes = 34; };
+template <> struct Block<T_Q4_K> { static constexpr int elems = 256, bytes = 144; };
+template <> struct Block<T_Q6_K> { static constexpr int elems = 256, bytes = 210; };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (nontemporal: the weight stream is read once).
+__device__ __forceinline__ u32x4 ld_stream16(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// f32 -> binary16 bits, round to nearest even, f16 subnormals kept (the kernels' FP16 denorm mode
+// is "preserve").  Pinned to the scalar v_cvt_f16_f32: the packed v_cvt_pk_f16_f32 that the
+// compiler forms from two adjacent conversions does not give the same bits for every input.
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+    uint32_t r;
+    asm volatile("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r & 0xffffu;
+}
+
+// Exact IEEE products / differences that the compiler may not fuse.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+    return *reinterpret_cast<const uint16_t *>(p);
+}
+
+// Q4_K 6-bit (scale, min) of sub-block j from the 12 scale bytes packed in three dwords
+// (kernel.cu:913-921).
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              int &sc, int &m) {
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63;
+        m = (s1 >> (8 * j)) & 63;
+    } else {
+        const int jj = 8 * (j - 4);
+        sc = ((s2 >> jj) & 0x0f) | (((s0 >> (jj + 6)) & 3) << 4);
+        m = ((s2 >> (jj + 4)) & 0x0f) | (((s1 >> (jj + 6)) & 3) << 4);
+    }
+}
+
+// ---- per-element decoders (canonical values; used by dequant and the generic paths) ----------
+
+// Q4_K element e (0..255) of the super-block at b.
+__device__ __forceinline__ float q4k_value(const uint8_t *b, int e) {
+    const float d = f16_bits_to_f32(ld_u16(b));
+    const float dmin = f16_bits_to_f32(ld_u16(b + 2));
+    const int j = e >> 5;
+    const uint32_t s0 = b[4] | (b[5] << 8) | (b[6] << 16) | (static_cast<uint32_t>(b[7]) << 24);
+    const uint32_t s1 = b[8] | (b[9] << 8) | (b[10] << 16) | (static_cast<uint32_t>(b[11]) << 24);
+    const uint32_t s2 = b[12] | (b[13] << 8) | (b[14] << 16) | (static_cast<uint32_t>(b[15]) << 24);
+    int sc, m;
+    q4k_scale_min(j, s0, s1, s2, sc, m);
+    const uint8_t byte = b[16 + (j >> 1) * 32 + (e & 31)];
+    const int q = (j & 1) ? (byte >> 4) : (byte & 0x0f);
+    return sub_rn(mul_rn(mul_rn(d, static_cast<float>(sc)), static_cast<float>(q)),
+                  mul_rn(dmin, static_cast<float>(m)));
+}
+
+// Q6_K element e (0..255): half h = e/128; group g = (e%128)/32, lane l = e%32.
+__device__ __forceinline__ float q6k_value(const uint8_t *b, int e) {
+    const int half = e >> 7, within = e & 127, g = within >> 5, l = within & 31;
+    const uint8_t lo_byte = b[half * 64 + l + 32 * (g & 1)];
+    const int lo = (g < 2) ? (lo_byte & 0x0f) : (lo_byte >> 4);
+    const int hi = (b[128 + half * 32 + l] >> (2 * g)) & 3;
+    const int q = (lo | (hi << 4)) - 32;
+    const int sc = static_cast<int8_t>(b[192 + half * 8 + l / 16 + 2 * g]);
+    const float d = f16_bits_to_f32(ld_u16(b + 208));
+    return mul_rn(mul_rn(d, static_cast<float>(sc)), static_cast<float>(q));
+}
+
+__device__ __forceinline__ float q50_value(const uint8_t *b, int e) {
+    const float d = f16_bits_to_f32(ld_u16(b));
+    const uint32_t qh = ld_u16(b + 2) | (ld_u16(b + 4) << 16);
+    const int lo = (e < 16) ? (b[6 + e] & 0x0f) : (b[6 + e - 16] >> 4);
+    const int q = lo | static_cast<int>(((qh >> e) & 1u) << 4);
+    return mul_rn(d, static_cast<float>(q - 16));
+}
+
+__device__ __forceinline__ float q80_value(const uint8_t *b, int e) {
+    const float d = f16_bits_to_f32(ld_u16(b));
+    return mul_rn(d, static_cast<float>(static_cast<int8_t>(b[2 + e])));
+}
+
+__device__ __forceinline__ float q40_value(const uint8_t *b, int e) {
+    const float d = f16_bits_to_f32(ld_u16(b));
+    const int q = (e < 16) ? (b[2 + e] & 0x0f) : (b[2 + e - 16] >> 4);
+    return mul_rn(d, static_cast<float>(q - 8));
+}
+
+template <int T>
+__device__ __forceinline__ float block_value(const uint8_t *b, int e) {
+    if constexpr (T == T_Q4_K) return q4k_value(b, e);
+    else if constexpr (T == T_Q6_K) return q6k_value(b, e);
+    else if constexpr (T == T_Q5_0) return q50_value(b, e);
+    else if constexpr (T == T_Q8_0) return q80_value(b, e);
+    else return q40_value(b, e);
+}
+
+// ---- wave64 reductions ------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace qlin

@@ -1,0 +1,48 @@
+// qlin_internal.hpp -- launchers shared between the kernel translation units and the C-ABI layer.
+// All launchers are asynchronous on the given stream, allocate nothing and never synchronise, so a
+// caller may capture them into a HIP graph.  Arguments are validated by the C-ABI layer first.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qlin {
+
+struct DeviceInfo {
+    int cu_count = 256;
+};
+const DeviceInfo &device_info();
+
+// y[r, o] (=|+=) sum_k W[o, k] x[r, k] for r < m.  add => y += (m must be 1 for add).
+hipError_t gemv(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y, int out_dim,
+                int in_dim, int m, bool add, hipStream_t s);
+
+// The per-element fallback used for any type / alignment (exposed for tests of the fast paths).
+hipError_t gemv_generic(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,
+                        int out_dim, int in_dim, int m, bool add, hipStream_t s);
+
+// Whole-stream dequantization: n elements to f32 or to f16 bit patterns (RNE of the f32 value).
+hipError_t dequant(int type, const uint8_t *src, void *out, int64_t n, bool to_f16, hipStream_t s);
+
+// Q8_1 activation quantizer (36 B per 32 values) and the weight x Q8_1 matmul.
+hipError_t quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, bool raw_sum, hipStream_t s);
+hipError_t matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y,
+                       int out_dim, int in_dim, int m, hipStream_t s);
+
+// MoE.
+hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts,
+                       int k, float routed_scaling, hipStream_t s);
+hipError_t swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_row_bytes,
+                  size_t u_row_bytes, const float *x, float *act, int ffn_dim, int in_dim,
+                  hipStream_t s);
+hipError_t swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t g_expert_bytes,
+                          size_t u_expert_bytes, size_t g_row_bytes, size_t u_row_bytes,
+                          const float *x, const int *expert_ids, float *act, int k, int ffn_dim,
+                          int in_dim, hipStream_t s);
+hipError_t down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_bytes,
+                                size_t d_row_bytes, const float *act, const int *expert_ids,
+                                const float *route_w, float *out, int k, int hidden, int ffn_dim,
+                                hipStream_t s);
+
+}  // namespace qlin

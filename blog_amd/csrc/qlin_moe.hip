@@ -1,0 +1,147 @@
+// qlin_moe.hip -- routed-expert decode pieces, gfx950.
+//
+// Semantics (AI/codes/local-llm/src/backend/cuda/ops/kernel.cu):
+//   router_topk            3463-3511  softmax over n_experts (non-finite -> -inf), k picks by strict
+//                                     '>' (lowest index wins ties), w = p * routed_scaling.
+//   swiglu                 1289-1328  act[o] = g / (1 + exp(-g)) * u, g = Wg[o].x, u = Wu[o].x
+//   swiglu_indexed         1340-1385  the same per route r on expert expert_ids[r]; id < 0 -> 0.
+//   down_indexed_ordered   2253-2287  out[h] += sum_r fmaf(Wd[e_r][h].act[r], w_r, .) in route order
+// One wave64 per output row; the dot products decode weights per element (any alignment).
+#include "qlin_device.hpp"
+#include "qlin_internal.hpp"
+
+namespace qlin {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int T>
+__device__ __forceinline__ float row_dot(const uint8_t *row, const float *x, int in_dim, int lane) {
+    constexpr int BE = Block<T>::elems, BB = Block<T>::bytes;
+    float acc = 0.0f;
+    for (int k = lane; k < in_dim; k += 64) acc = fmaf(block_value<T>(row + (k / BE) * BB, k % BE), x[k], acc);
+    return wave_sum(acc);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+__global__ __launch_bounds__(64) void router_kernel(const float *__restrict__ logits, int *__restrict__ idx,
+                                                    float *__restrict__ wout, int tokens, int ne, int k,
+                                                    float scaling) {
+    const int t = blockIdx.x * 64 + threadIdx.x;
+    if (t >= tokens) return;
+    const float *lg = logits + static_cast<size_t>(t) * ne;
+    float maxv = -INFINITY;
+    for (int e = 0; e < ne; ++e) {
+        const float v = isfinite(lg[e]) ? lg[e] : -INFINITY;
+        maxv = fmaxf(maxv, v);
+    }
+    float denom = 0.0f;
+    if (isfinite(maxv))
+        for (int e = 0; e < ne; ++e) {
+            const float v = isfinite(lg[e]) ? lg[e] : -INFINITY;
+            denom += expf(v - maxv);
+        }
+    uint64_t used[4] = {0, 0, 0, 0};  // n_experts <= 256, checked by the caller
+    for (int r = 0; r < k; ++r) {
+        float best = -INFINITY;
+        int best_e = -1;
+        for (int e = 0; e < ne; ++e) {
+            if ((used[e >> 6] >> (e & 63)) & 1u) continue;
+            const float v = isfinite(lg[e]) ? lg[e] : -INFINITY;
+            if (v > best) { best = v; best_e = e; }
+        }
+        if (best_e < 0) best_e = r < ne ? r : 0;
+        used[best_e >> 6] |= 1ull << (best_e & 63);
+        const float prob = (denom > 0.0f && isfinite(best)) ? expf(best - maxv) / denom : 0.0f;
+        idx[static_cast<size_t>(t) * k + r] = best_e;
+        wout[static_cast<size_t>(t) * k + r] = prob * scaling;
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu,
+                                                        size_t g_eb, size_t u_eb, size_t g_rb, size_t u_rb,
+                                                        const float *__restrict__ x, const int *__restrict__ ids,
+                                                        float *__restrict__ act, int k, int ffn, int in_dim) {
+    const int wave = static_cast<int>((blockIdx.x * kBlock + threadIdx.x) >> 6);
+    const int lane = threadIdx.x & 63;
+    if (wave >= k * ffn) return;
+    const int route = wave / ffn, row = wave - route * ffn;
+    const int e = ids ? ids[route] : 0;
+    float *dst = act + static_cast<size_t>(route) * ffn + row;
+    if (e < 0) {
+        if (lane == 0) *dst = 0.0f;
+        return;
+    }
+    const float g = row_dot<T>(wg + static_cast<size_t>(e) * g_eb + static_cast<size_t>(row) * g_rb, x, in_dim, lane);
+    const float u = row_dot<T>(wu + static_cast<size_t>(e) * u_eb + static_cast<size_t>(row) * u_rb, x, in_dim, lane);
+    if (lane == 0) *dst = silu_mul(g, u);
+}
+
+template <int T>
+__global__ __launch_bounds__(kBlock) void down_kernel(const uint8_t *__restrict__ wd, size_t d_eb, size_t d_rb,
+                                                      const float *__restrict__ act, const int *__restrict__ ids,
+                                                      const float *__restrict__ rw, float *__restrict__ out,
+                                                      int k, int hidden, int ffn) {
+    const int h = static_cast<int>((blockIdx.x * kBlock + threadIdx.x) >> 6);
+    const int lane = threadIdx.x & 63;
+    if (h >= hidden) return;
+    float total = 0.0f;
+    for (int r = 0; r < k; ++r) {
+        const int e = ids[r];
+        if (e < 0) continue;
+        const float a = row_dot<T>(wd + static_cast<size_t>(e) * d_eb + static_cast<size_t>(h) * d_rb,
+                                   act + static_cast<size_t>(r) * ffn, ffn, lane);
+        total = fmaf(a, rw[r], total);
+    }
+    if (lane == 0) out[h] += total;
+}
+
+}  // namespace
+
+hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts, int k,
+                       float routed_scaling, hipStream_t s) {
+    if (tokens == 0) return hipSuccess;
+    hipLaunchKernelGGL(router_kernel, dim3((tokens + 63) / 64), dim3(64), 0, s, logits, top_idx, top_w, tokens,
+                       n_experts, k, routed_scaling);
+    return hipGetLastError();
+}
+
+#define QLIN_TYPE_SWITCH(type, CALL)            \
+    switch (type) {                             \
+        case T_Q4_0: { constexpr int TT = T_Q4_0; CALL; break; } \
+        case T_Q5_0: { constexpr int TT = T_Q5_0; CALL; break; } \
+        case T_Q8_0: { constexpr int TT = T_Q8_0; CALL; break; } \
+        case T_Q4_K: { constexpr int TT = T_Q4_K; CALL; break; } \
+        case T_Q6_K: { constexpr int TT = T_Q6_K; CALL; break; } \
+        default: return hipErrorInvalidValue;   \
+    }
+
+hipError_t swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb,
+                          size_t g_rb, size_t u_rb, const float *x, const int *ids, float *act, int k,
+                          int ffn, int in_dim, hipStream_t s) {
+    const int64_t waves = static_cast<int64_t>(k) * ffn;
+    if (waves == 0) return hipSuccess;
+    const int blocks = static_cast<int>((waves + 3) / 4);
+    QLIN_TYPE_SWITCH(type, hipLaunchKernelGGL((swiglu_kernel<TT>), dim3(blocks), dim3(kBlock), 0, s, wg, wu,
+                                              g_eb, u_eb, g_rb, u_rb, x, ids, act, k, ffn, in_dim));
+    return hipGetLastError();
+}
+
+hipError_t swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_rb, size_t u_rb, const float *x,
+                  float *act, int ffn, int in_dim, hipStream_t s) {
+    return swiglu_indexed(type, wg, wu, 0, 0, g_rb, u_rb, x, nullptr, act, 1, ffn, in_dim, s);
+}
+
+hipError_t down_indexed_ordered(int type, const uint8_t *wd, size_t d_eb, size_t d_rb, const float *act,
+                                const int *ids, const float *rw, float *out, int k, int hidden, int ffn,
+                                hipStream_t s) {
+    if (hidden == 0) return hipSuccess;
+    const int blocks = (hidden + 3) / 4;
+    QLIN_TYPE_SWITCH(type, hipLaunchKernelGGL((down_kernel<TT>), dim3(blocks), dim3(kBlock), 0, s, wd, d_eb, d_rb,
+                                              act, ids, rw, out, k, hidden, ffn));
+    return hipGetLastError();
+}
+
+}  // namespace qlin

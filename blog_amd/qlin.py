@@ -1,0 +1,134 @@
+"""ctypes binding of ``blog_amd/libqlin.so`` (the C ABI declared in ``include/qlin.h``).
+
+Plumbing for the tests and the benchmark: device memory comes from torch tensors, every compute
+call goes through the C ABI into the HIP kernels.  There is no fallback of any kind: if the
+library is missing or a call is rejected, this module raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libqlin.so")
+
+Q4_0, Q5_0, Q8_0, Q8_1, Q4_K, Q6_K = 2, 6, 8, 9, 12, 14
+STATUS = {0: "QLIN_OK", 1: "QLIN_ERR_UNSUPPORTED_TYPE", 2: "QLIN_ERR_SHAPE", 3: "QLIN_ERR_NULL",
+          4: "QLIN_ERR_ROW_BYTES", 5: "QLIN_ERR_LIMIT", 6: "QLIN_ERR_LAUNCH", 7: "QLIN_ERR_ALIGN"}
+
+P, I, I64, SZ, F = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
+
+# name -> (restype, argtypes); every symbol of include/qlin.h
+SIGNATURES = {
+    "qlin_status_string": (C.c_char_p, [I]),
+    "qlin_version": (C.c_char_p, []),
+    "qlin_set_stream": (I, [P]),
+    "qlin_get_stream": (P, []),
+    "qlin_block_elems": (I, [I]),
+    "qlin_block_bytes": (I, [I]),
+    "qlin_row_bytes": (SZ, [I, I]),
+    "qlin_launch_quant_gemv": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_gemv_add": (I, [I, P, SZ, P, P, I, I]),
+    "qlin_launch_quant_matmul": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_q8_1_row_bytes": (SZ, [I]),
+    "qlin_launch_quantize_q8_1": (I, [P, P, I, I, I]),
+    "qlin_launch_quant_matmul_q8_1": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_swiglu": (I, [I, P, P, SZ, SZ, P, P, I, I]),
+    "qlin_launch_quant_swiglu_indexed": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
+    "qlin_launch_quant_down_f32_indexed_accum_ordered": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
+    "qlin_launch_moe_router_topk": (I, [P, P, P, I, I, I, F]),
+    "qlin_launch_dequantize_to_f16": (I, [I, P, P, I64]),
+    "qlin_launch_dequantize_q4k_to_f16": (I, [P, P, I64]),
+    "qlin_launch_dequantize_q80_to_f16": (I, [P, P, I64]),
+    "qlin_launch_dequantize_q50_to_f16": (I, [P, P, I64]),
+    "qlin_launch_dequantize_q6k_to_f16": (I, [P, P, I64]),
+    "qlin_launch_dequantize_to_f32": (I, [I, P, P, I64]),
+    "qlin_gemm": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_moe_routed_decode_indexed": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, P, I]),
+}
+
+
+class QlinError(RuntimeError):
+    def __init__(self, fn: str, rc: int):
+        super().__init__(f"{fn} returned {rc} ({STATUS.get(rc, '?')})")
+        self.rc = rc
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Loads the HIP library; raises if it has not been built (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python -m blog_amd.build` (HIP/gfx950 build)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ptr(t) -> int:
+    """Device address of a torch tensor (or an int address, or None -> 0)."""
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def call(name: str, *args) -> int:
+    """Calls an entry point with tensors converted to addresses; raises on a non-zero status."""
+    rc = getattr(lib(), name)(*[ptr(a) if not isinstance(a, (float, bool)) and hasattr(a, "data_ptr") else a
+                                for a in args])
+    if rc != 0:
+        raise QlinError(name, rc)
+    return rc
+
+
+def status(name: str, *args) -> int:
+    """Calls an entry point and returns its status without raising."""
+    return getattr(lib(), name)(*[ptr(a) if hasattr(a, "data_ptr") else a for a in args])
+
+
+def set_stream(stream) -> None:
+    """Launch on a torch.cuda.Stream (or a raw hipStream_t address, or None)."""
+    handle = 0 if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
+    lib().qlin_set_stream(handle or None)
+
+
+def row_bytes(qtype: int, in_dim: int) -> int:
+    return int(lib().qlin_row_bytes(qtype, in_dim))
+
+
+# ---- convenience wrappers (tensors in, launches on the current library stream) --------------
+
+def quant_gemv(qtype, w, rb, x, y, out_dim, in_dim, m=1):
+    call("qlin_launch_quant_gemv", qtype, w, rb, x, y, out_dim, in_dim, m)
+
+
+def quant_gemv_add(qtype, w, rb, x, y, out_dim, in_dim):
+    call("qlin_launch_quant_gemv_add", qtype, w, rb, x, y, out_dim, in_dim)
+
+
+def quant_matmul(qtype, w, rb, x, y, out_dim, in_dim, m):
+    call("qlin_launch_quant_matmul", qtype, w, rb, x, y, out_dim, in_dim, m)
+
+
+def quantize_q8_1(x, xq, in_dim, m, store_raw_sum=False):
+    call("qlin_launch_quantize_q8_1", x, xq, in_dim, m, int(store_raw_sum))
+
+
+def quant_matmul_q8_1(qtype, w, rb, xq, y, out_dim, in_dim, m):
+    call("qlin_launch_quant_matmul_q8_1", qtype, w, rb, xq, y, out_dim, in_dim, m)
+
+
+def dequantize(qtype, src, out, n, f16=True):
+    if f16:
+        call("qlin_launch_dequantize_to_f16", qtype, src, out, n)
+    else:
+        call("qlin_launch_dequantize_to_f32", qtype, src, out, n)

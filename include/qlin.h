@@ -1,0 +1,158 @@
+/*
+ * qlin.h -- C ABI of the MI355X (gfx950) GGUF quantized-linear library (libqlin.so).
+ *
+ * Drop-in boundary for the quantized-linear launchers of the reference engine
+ * (AI/codes/local-llm/src/backend/cuda/ops/kernel.cuh).  Each entry point keeps the reference
+ * launcher's argument list and meaning, with three deliberate differences:
+ *   - the weight format is an int ggml type code instead of the C++ DType enum (same values,
+ *     src/tensor/TensorCommon.h:15-33);
+ *   - every call returns a qlin_status (0 = launched) where the reference returns void and silently
+ *     does nothing for an unsupported type (src/backend/cuda/ops/launch.cu:57);
+ *   - the stream is the library's current stream, set with qlin_set_stream (the reference's
+ *     set_current_cuda_stream, src/backend/cuda/common.cpp:13-17).
+ *
+ * Conventions (as the reference's):
+ *   - all data pointers are device pointers owned by the caller; weights are resident packed GGUF
+ *     bytes, row-major [out_dim, in_dim], row r at weight + r * row_bytes; activations and outputs
+ *     are f32 row-major [m, in_dim] / [m, out_dim];
+ *   - launches are asynchronous on the current stream; no entry point allocates device memory,
+ *     synchronises or reads device data back, so all of them may be captured into a HIP graph;
+ *   - validation happens on the host before any launch and needs no GPU.
+ *
+ * Supported weight types: Q4_0 (2), Q5_0 (6), Q8_0 (8), Q4_K (12), Q6_K (14).
+ */
+#ifndef QLIN_H
+#define QLIN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QLIN_TYPE_Q4_0 2
+#define QLIN_TYPE_Q5_0 6
+#define QLIN_TYPE_Q8_0 8
+#define QLIN_TYPE_Q8_1 9
+#define QLIN_TYPE_Q4_K 12
+#define QLIN_TYPE_Q6_K 14
+
+typedef enum qlin_status {
+    QLIN_OK = 0,
+    QLIN_ERR_UNSUPPORTED_TYPE = 1, /* weight type not supported by this entry point */
+    QLIN_ERR_SHAPE = 2,            /* negative dimension, or in_dim not a multiple of the block */
+    QLIN_ERR_NULL = 3,             /* required pointer is NULL while there is work to do */
+    QLIN_ERR_ROW_BYTES = 4,        /* row / expert stride smaller than the packed data it holds */
+    QLIN_ERR_LIMIT = 5,            /* argument beyond a documented limit (e.g. n_experts > 256) */
+    QLIN_ERR_LAUNCH = 6,           /* the HIP runtime rejected the launch */
+    QLIN_ERR_ALIGN = 7             /* pointer misaligned for its element type */
+} qlin_status;
+
+/* Human-readable name of a status code. */
+const char *qlin_status_string(int status);
+
+/* Library version, and the gfx target it was built for ("gfx950"). */
+const char *qlin_version(void);
+
+/* Stream used by every launch (a hipStream_t; NULL = the default stream).
+ * Mirrors set_current_cuda_stream / get_current_cuda_stream (common.cpp:13-17). */
+int qlin_set_stream(void *stream);
+void *qlin_get_stream(void);
+
+/* Block geometry of a ggml type (GgufFile.cpp:35-55); 0 for an unknown type. */
+int qlin_block_elems(int type);
+int qlin_block_bytes(int type);
+/* Packed bytes of one row of in_dim elements; 0 if the type is unknown or in_dim is indivisible. */
+size_t qlin_row_bytes(int type, int in_dim);
+
+/* ---- decode / prefill linear (kernel.cuh:33-42) ------------------------------------------------ */
+
+/* y[r, o] = sum_k W[o, k] x[r, k], r < m.  Replaces launch_quant_gemv (launch.cu:42-60). */
+int qlin_launch_quant_gemv(int type, const uint8_t *weight, size_t row_bytes, const float *x, float *y,
+                           int out_dim, int in_dim, int m);
+
+/* y[o] += sum_k W[o, k] x[k].  Replaces launch_quant_gemv_add (launch.cu:71-89). */
+int qlin_launch_quant_gemv_add(int type, const uint8_t *weight, size_t row_bytes, const float *x,
+                               float *y, int out_dim, int in_dim);
+
+/* Same contraction as qlin_launch_quant_gemv, for m > 1 (prefill with f32 activations).
+ * Replaces launch_quant_matmul (launch.cu:101-119). */
+int qlin_launch_quant_matmul(int type, const uint8_t *weight, size_t row_bytes, const float *x, float *y,
+                             int out_dim, int in_dim, int m);
+
+/* ---- Q8_1 activations (kernel.cuh:46-54) ------------------------------------------------------ */
+
+/* Bytes of one Q8_1 activation row: ceil(in_dim / 32) * 36.  Replaces q8_1_row_bytes. */
+size_t qlin_q8_1_row_bytes(int in_dim);
+
+/* Quantize m rows of in_dim f32 values to Q8_1 blocks (d f16, s f16, int8 q[32]); s = d * sum(q),
+ * or the raw f32 sum when store_raw_sum != 0.  Replaces launch_quantize_q8_1 (launch.cu:201-207). */
+int qlin_launch_quantize_q8_1(const float *x, uint8_t *x_q8_1, int in_dim, int m, int store_raw_sum);
+
+/* y[r, o] = W[o] . x_q8_1[r] with block-dot semantics (kernel.cu:2305-2402).
+ * Replaces launch_quant_matmul_q8_1 (launch.cu:500-531). */
+int qlin_launch_quant_matmul_q8_1(int type, const uint8_t *weight, size_t row_bytes, const uint8_t *x_q8_1,
+                                  float *y, int out_dim, int in_dim, int m);
+
+/* ---- MoE decode (kernel.cuh:62-129, 335-336) --------------------------------------------------- */
+
+/* act[o] = silu(Wg[o].x) * (Wu[o].x).  Replaces launch_quant_swiglu (launch.cu:132-154). */
+int qlin_launch_quant_swiglu(int type, const uint8_t *gate_weight, const uint8_t *up_weight,
+                             size_t gate_row_bytes, size_t up_row_bytes, const float *x, float *act,
+                             int ffn_dim, int in_dim);
+
+/* act[r, o] for route r on expert expert_ids[r] (device array; id < 0 writes 0).
+ * Replaces launch_quant_swiglu_indexed (launch.cu:170-189). */
+int qlin_launch_quant_swiglu_indexed(int type, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                     size_t gate_expert_bytes, size_t up_expert_bytes,
+                                     size_t gate_row_bytes, size_t up_row_bytes, const float *x,
+                                     const int *expert_ids, float *act, int k, int ffn_dim, int in_dim);
+
+/* out[h] += sum_r route_weights[r] * (Wd[e_r][h] . act[r]), routes in order, negative ids skipped.
+ * Replaces launch_quant_down_f32_indexed_accum_ordered (launch.cu:469-498). */
+int qlin_launch_quant_down_f32_indexed_accum_ordered(int type, const uint8_t *down_weight,
+                                                     size_t down_expert_bytes, size_t down_row_bytes,
+                                                     const float *act, const int *expert_ids,
+                                                     const float *route_weights, float *out, int k,
+                                                     int hidden_size, int ffn_dim);
+
+/* Softmax top-k router: top_idx[t, r], top_w[t, r] = p * routed_scaling (n_experts <= 256).
+ * Replaces launch_moe_router_topk (kernel.cu:3463-3511). */
+int qlin_launch_moe_router_topk(const float *router_logits, int *top_idx, float *top_w, int tokens,
+                                int n_experts, int k, float routed_scaling);
+
+/* ---- dequantization (kernel.cuh:237-252) -------------------------------------------------------- */
+
+/* num_elements values of a contiguous block stream to f16 bit patterns (RNE of the exact f32 value).
+ * Generic form of launch_dequantize_{q4k,q80,q50,q6k}_to_f16 (launch.cu:803-828). */
+int qlin_launch_dequantize_to_f16(int type, const uint8_t *src, uint16_t *out, int64_t num_elements);
+/* The reference's per-type names. */
+int qlin_launch_dequantize_q4k_to_f16(const uint8_t *src, uint16_t *out, int64_t num_elements);
+int qlin_launch_dequantize_q80_to_f16(const uint8_t *src, uint16_t *out, int64_t num_elements);
+int qlin_launch_dequantize_q50_to_f16(const uint8_t *src, uint16_t *out, int64_t num_elements);
+int qlin_launch_dequantize_q6k_to_f16(const uint8_t *src, uint16_t *out, int64_t num_elements);
+/* Same values as f32 (no reference counterpart; the exact values the GEMV consumes). */
+int qlin_launch_dequantize_to_f32(int type, const uint8_t *src, float *out, int64_t num_elements);
+
+/* ---- op facade (TensorTool, src/tensor/TensorTool.cpp) ----------------------------------------- */
+
+/* TensorTool::gemm for a quantized weight (TensorTool.cpp:87-98, 146-173): row_bytes is derived as
+ * weight_bytes / out_dim, m == 1 runs the decode GEMV, m > 1 the f32-activation matmul. */
+int qlin_gemm(int type, const uint8_t *weight, size_t weight_bytes, const float *x, float *y, int out_dim,
+              int in_dim, int m);
+
+/* TensorTool::moe_routed_decode_indexed (TensorTool.cpp:271-336) for one token: expert tensors are
+ * packed [n_experts, rows, cols] with strides derived from their byte sizes; act_scratch holds
+ * k * ffn_dim floats.  Returns QLIN_OK when launched and a QLIN_ERR_* code where the reference
+ * returns false (caller falls back). */
+int qlin_moe_routed_decode_indexed(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                   size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                   size_t down_bytes, int n_experts, int ffn_dim, int in_dim,
+                                   int hidden_size, const float *x, const int *expert_ids,
+                                   const float *route_weights, float *act_scratch, float *out, int k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QLIN_H */

@@ -1,0 +1,222 @@
+"""ctypes front end of the CPU oracle (``oracle/liboracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg, always as the checker.  The product (``blog_amd``) never imports it.
+
+Every function restates reference arithmetic; the C source cites the reference lines
+(``AI/codes/local-llm/src/backend/cuda/ops/kernel.cu``).  Arrays are numpy, C-contiguous.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_0, Q5_0, Q8_0, Q8_1, Q4_K, Q6_K = 0, 1, 2, 6, 8, 9, 12, 14
+BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q6_K: (256, 210)}
+NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+I = C.c_int
+I64 = C.c_int64
+SZ = C.c_size_t
+
+
+def _declare(L: C.CDLL) -> None:
+    sig = {
+        "orc_block_elems": (I, [I]),
+        "orc_block_bytes": (I, [I]),
+        "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+        "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+        "orc_f16_to_f32_array": (None, [P, P, I64]),
+        "orc_f32_to_f16_array": (None, [P, P, I64]),
+        "orc_q4k_scale_min": (None, [I, P, P, P]),
+        "orc_dequant_f32": (I, [I, P, I64, P]),
+        "orc_dequant_f16": (I, [I, P, I64, P]),
+        "orc_matmul_f64": (I, [I, P, SZ, P, P, I, I, I]),
+        "orc_matmul_f32": (I, [I, P, SZ, P, P, I, I, I, I]),
+        "orc_matmul_lane32": (I, [I, P, SZ, P, P, I, I, I]),
+        "orc_gemv_add": (I, [I, P, SZ, P, P, I, I]),
+        "orc_q8_1_row_bytes": (SZ, [I]),
+        "orc_quantize_q8_1": (None, [P, P, I, I, I]),
+        "orc_matmul_q8_1": (I, [I, P, SZ, P, P, I, I, I]),
+        "orc_router_topk": (None, [P, P, P, I, I, I, C.c_float]),
+        "orc_swiglu": (I, [I, P, P, SZ, SZ, P, P, I, I]),
+        "orc_swiglu_indexed": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
+        "orc_down_indexed_ordered": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
+        "orc_argmax": (I, [P, I]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _ok(rc: int, what: str) -> None:
+    if rc != 0:
+        raise ValueError(f"oracle {what}: unsupported type or shape")
+
+
+def row_bytes(qtype: int, in_dim: int) -> int:
+    be, bb = BLOCK[qtype]
+    assert in_dim % be == 0
+    return in_dim // be * bb
+
+
+# ---- f16 ----------------------------------------------------------------------------------
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32_array(_p(h), _p(out), h.size)
+    return out
+
+
+def f32_to_f16(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().orc_f32_to_f16_array(_p(f), _p(out), f.size)
+    return out
+
+
+def q4k_scale_min(j: int, scales: bytes) -> tuple[int, int]:
+    s = np.frombuffer(bytes(scales), np.uint8).copy()
+    sc, m = C.c_int(), C.c_int()
+    lib().orc_q4k_scale_min(j, _p(s), C.addressof(sc), C.addressof(m))
+    return sc.value, m.value
+
+
+# ---- dequant -------------------------------------------------------------------------------
+def dequant_f32(qtype: int, src: np.ndarray, n: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    _ok(lib().orc_dequant_f32(qtype, _p(src), n, _p(out)), "dequant_f32")
+    return out
+
+
+def dequant_f16(qtype: int, src: np.ndarray, n: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(n, np.uint16)
+    _ok(lib().orc_dequant_f16(qtype, _p(src), n, _p(out)), "dequant_f16")
+    return out
+
+
+# ---- GEMV / matmul -------------------------------------------------------------------------
+def matmul_f64(qtype: int, w: np.ndarray, rb: int, x: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    m = x.shape[0]
+    y = np.empty((m, out_dim), np.float64)
+    _ok(lib().orc_matmul_f64(qtype, _p(w), rb, _p(x), _p(y), out_dim, in_dim, m), "matmul_f64")
+    return y
+
+
+def matmul_f32(qtype: int, w: np.ndarray, rb: int, x: np.ndarray, out_dim: int, in_dim: int,
+               nthreads: int = 0) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    m = x.shape[0]
+    y = np.empty((m, out_dim), np.float32)
+    _ok(lib().orc_matmul_f32(qtype, _p(w), rb, _p(x), _p(y), out_dim, in_dim, m, nthreads), "matmul_f32")
+    return y
+
+
+def matmul_lane32(qtype: int, w: np.ndarray, rb: int, x: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    m = x.shape[0]
+    y = np.empty((m, out_dim), np.float32)
+    _ok(lib().orc_matmul_lane32(qtype, _p(w), rb, _p(x), _p(y), out_dim, in_dim, m), "matmul_lane32")
+    return y
+
+
+def gemv_add(qtype: int, w: np.ndarray, rb: int, x: np.ndarray, y: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.array(y, dtype=np.float32, copy=True)
+    _ok(lib().orc_gemv_add(qtype, _p(w), rb, _p(x), _p(y), out_dim, in_dim), "gemv_add")
+    return y
+
+
+# ---- Q8_1 ----------------------------------------------------------------------------------
+def q8_1_row_bytes(in_dim: int) -> int:
+    return int(lib().orc_q8_1_row_bytes(in_dim))
+
+
+def quantize_q8_1(x: np.ndarray, in_dim: int, store_raw_sum: bool = False) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    m = x.shape[0]
+    out = np.zeros(m * q8_1_row_bytes(in_dim), np.uint8)
+    lib().orc_quantize_q8_1(_p(x), _p(out), in_dim, m, int(store_raw_sum))
+    return out
+
+
+def matmul_q8_1(qtype: int, w: np.ndarray, rb: int, xq: np.ndarray, out_dim: int, in_dim: int, m: int) -> np.ndarray:
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    y = np.empty((m, out_dim), np.float64)
+    _ok(lib().orc_matmul_q8_1(qtype, _p(w), rb, _p(xq), _p(y), out_dim, in_dim, m), "matmul_q8_1")
+    return y
+
+
+# ---- MoE -----------------------------------------------------------------------------------
+def router_topk(logits: np.ndarray, k: int, routed_scaling: float = 1.0):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    tokens, n_experts = logits.shape
+    idx = np.empty((tokens, k), np.int32)
+    w = np.empty((tokens, k), np.float32)
+    lib().orc_router_topk(_p(logits), _p(idx), _p(w), tokens, n_experts, k, routed_scaling)
+    return idx, w
+
+
+def swiglu(qtype, wg, wu, g_rb, u_rb, x, ffn_dim, in_dim) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    act = np.empty(ffn_dim, np.float32)
+    _ok(lib().orc_swiglu(qtype, _p(wg), _p(wu), g_rb, u_rb, _p(x), _p(act), ffn_dim, in_dim), "swiglu")
+    return act
+
+
+def swiglu_indexed(qtype, wg, wu, g_eb, u_eb, g_rb, u_rb, x, expert_ids, ffn_dim, in_dim) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(expert_ids, dtype=np.int32)
+    k = ids.size
+    act = np.empty((k, ffn_dim), np.float32)
+    _ok(lib().orc_swiglu_indexed(qtype, _p(wg), _p(wu), g_eb, u_eb, g_rb, u_rb, _p(x), _p(ids), _p(act),
+                                 k, ffn_dim, in_dim), "swiglu_indexed")
+    return act
+
+
+def down_indexed_ordered(qtype, wd, d_eb, d_rb, act, expert_ids, route_w, out, hidden, ffn_dim) -> np.ndarray:
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    ids = np.ascontiguousarray(expert_ids, dtype=np.int32)
+    rw = np.ascontiguousarray(route_w, dtype=np.float32)
+    out = np.array(out, dtype=np.float32, copy=True)
+    _ok(lib().orc_down_indexed_ordered(qtype, _p(wd), d_eb, d_rb, _p(act), _p(ids), _p(rw), _p(out),
+                                       ids.size, hidden, ffn_dim), "down_indexed_ordered")
+    return out
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return int(lib().orc_argmax(_p(v), v.size))

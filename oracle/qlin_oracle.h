@@ -1,0 +1,120 @@
+/*
+ * qlin_oracle.h -- CPU restatement of the reference's GGUF quantized-linear arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (blog_amd/, include/) may link, load or
+ * call this code; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
+ * and only as the checker.  It is plain C99, compiled with -ffp-contract=off so every
+ * floating-point expression is evaluated exactly as written (no fused multiply-add).
+ *
+ * Reference being restated (paths relative to AI/codes/local-llm/ in the reference repo):
+ *   block codecs   src/backend/cuda/ops/kernel.cu:913-921 (q4k_scale_min), 1090-1119 (q4k_at),
+ *                  1122-1156 (q6k_at), 1159-1175 (q50_at), 1178-1185 (q80_at)
+ *   dequant->f16   kernel.cu:954-1063 (dequantize_{q4k,q80,q50,q6k}_to_f16_kernel)
+ *   GEMV / matmul  kernel.cu:1192-1279 (quant_gemv_kernel, quant_gemv_add_kernel, quant_matmul_kernel)
+ *   Q8_1           kernel.cu:1679-1720 (quantize_q8_1_kernel), 2305-2402 (quant_matmul_q8_1_kernel)
+ *   MoE            kernel.cu:1289-1385 (quant_swiglu[_indexed]_kernel),
+ *                  2253-2287 (quant_down_f32_indexed_accum_ordered_kernel),
+ *                  3463-3511 (moe_router_topk_kernel), 3531-3592 (argmax, lowest index on ties)
+ *   block traits   src/format/gguf/GgufFile.cpp:35-55; dtype codes src/tensor/TensorCommon.h:15-33
+ *   Q4_0           not implemented by the reference (trait only, GgufFile.cpp:40); restated from
+ *                  the published ggml block_q4_0 format (d f16, 16 bytes of split-half nibbles,
+ *                  w = d * (q - 8)).
+ */
+#ifndef QLIN_ORACLE_H
+#define QLIN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type codes (TensorCommon.h:15-33). */
+enum {
+    ORC_F32 = 0,
+    ORC_F16 = 1,
+    ORC_Q4_0 = 2,
+    ORC_Q5_0 = 6,
+    ORC_Q8_0 = 8,
+    ORC_Q8_1 = 9,
+    ORC_Q4_K = 12,
+    ORC_Q6_K = 14,
+};
+
+/* Elements and bytes per block; 0 for an unknown type (GgufFile.cpp:35-55). */
+int orc_block_elems(int type);
+int orc_block_bytes(int type);
+
+/* IEEE-754 binary16 <-> binary32.  f16->f32 is exact; f32->f16 rounds to nearest, ties to even. */
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+void orc_f16_to_f32_array(const uint16_t *h, float *out, int64_t n);
+void orc_f32_to_f16_array(const float *f, uint16_t *out, int64_t n);
+
+/* Q4_K 6-bit (scale, min) of sub-block j in [0,8) (kernel.cu:913-921). */
+void orc_q4k_scale_min(int j, const uint8_t *scales, int *sc, int *m);
+
+/* Dequantize n elements (n a multiple of the block size) of one contiguous block stream.
+ * f32 values use the canonical non-contracted formulas; the f16 variant is RNE of the f32 value.
+ * Returns 0, or -1 for an unsupported type / indivisible n. */
+int orc_dequant_f32(int type, const uint8_t *src, int64_t n, float *out);
+int orc_dequant_f16(int type, const uint8_t *src, int64_t n, uint16_t *out);
+
+/* y[r, o] = sum_k w(o, k) * x[r, k] over m activation rows, double accumulation (the truth).
+ * W is [out_dim, in_dim] in row_bytes-strided rows.  Returns 0 or -1. */
+int orc_matmul_f64(int type, const uint8_t *w, size_t row_bytes, const float *x, double *y,
+                   int out_dim, int in_dim, int m);
+
+/* Same contraction with f32 accumulation, parallel over output rows with nthreads OpenMP
+ * threads (<= 0 means the OpenMP default).  This is the timed CPU path. */
+int orc_matmul_f32(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,
+                   int out_dim, int in_dim, int m, int nthreads);
+
+/* The reference kernel's own f32 order: 32 lanes, lane-strided fmaf, then a shuffle-down tree
+ * (kernel.cu:1192-1215).  Used to bound the fp32 deviation expected of any GPU order. */
+int orc_matmul_lane32(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,
+                      int out_dim, int in_dim, int m);
+
+/* y[o] += sum_k w(o,k) x[k]  (kernel.cu:1223-1244), double accumulation then one f32 add. */
+int orc_gemv_add(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,
+                 int out_dim, int in_dim);
+
+/* Q8_1 activation blocks: per 32 values, 36 bytes = d f16 | s f16 | q int8[32]
+ * (kernel.cu:1679-1720).  A trailing partial block is zero padded.  Bit-exact target. */
+size_t orc_q8_1_row_bytes(int in_dim);
+void orc_quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, int store_raw_sum);
+
+/* Quantized weight x Q8_1 activation, block-dot semantics of kernel.cu:2305-2402, computed in
+ * double (the truth for the int8 prefill path).  Returns 0 or -1. */
+int orc_matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y,
+                    int out_dim, int in_dim, int m);
+
+/* MoE router: softmax over n_experts (non-finite -> -inf), k picks with strict '>' (lowest index
+ * wins ties), w = p * routed_scaling, no renormalisation (kernel.cu:3463-3511). */
+void orc_router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts,
+                     int k, float routed_scaling);
+
+/* act[o] = silu(Wg[o].x) * (Wu[o].x)  (kernel.cu:1289-1328). */
+int orc_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_row_bytes,
+               size_t u_row_bytes, const float *x, float *act, int ffn_dim, int in_dim);
+
+/* act[r, o] for route r with expert_ids[r] (< 0 -> 0)  (kernel.cu:1340-1385). */
+int orc_swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t g_expert_bytes,
+                       size_t u_expert_bytes, size_t g_row_bytes, size_t u_row_bytes,
+                       const float *x, const int *expert_ids, float *act, int k, int ffn_dim,
+                       int in_dim);
+
+/* out[h] += sum_r w_r * (Wd[e_r][h] . act[r]), routes in order, negative ids skipped
+ * (kernel.cu:2253-2287). */
+int orc_down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_bytes,
+                             size_t d_row_bytes, const float *act, const int *expert_ids,
+                             const float *route_w, float *out, int k, int hidden, int ffn_dim);
+
+/* Index of the maximum, lowest index on ties (kernel.cu:3531-3592). */
+int orc_argmax(const float *v, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QLIN_ORACLE_H */

@@ -1,0 +1,142 @@
+"""CPU-side checks of the C ABI: the library loads, exports every declared symbol, and rejects bad
+arguments on the host with the documented status codes (no GPU is touched: every call here fails
+validation, or has no work, before any HIP call)."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from blog_amd import qlin
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qlin.h")
+
+OK, UNSUP, SHAPE, NULL, ROWB, LIMIT, LAUNCH, ALIGN = range(8)
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qlin_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    L = qlin.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 25
+    for s in syms:
+        assert hasattr(L, s), s
+        assert s in qlin.SIGNATURES, f"{s} missing from the ctypes binding"
+    assert set(qlin.SIGNATURES) == set(syms)
+
+
+def test_nm_exports_match_header():
+    if not shutil.which("nm"):
+        pytest.skip("nm not available")
+    out = subprocess.run(["nm", "-D", "--defined-only", qlin.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\b(qlin_\w+)$", out, flags=re.M))
+    assert exported == set(declared_symbols())
+
+
+def test_block_geometry():
+    geo = {2: (32, 18), 6: (32, 22), 8: (32, 34), 9: (32, 36), 12: (256, 144), 14: (256, 210)}
+    for t, (e, b) in geo.items():
+        assert qlin.lib().qlin_block_elems(t) == e
+        assert qlin.lib().qlin_block_bytes(t) == b
+    assert qlin.lib().qlin_block_elems(3) == 0
+    assert qlin.row_bytes(12, 3584) == 2016 and qlin.row_bytes(12, 18944) == 10656
+    assert qlin.row_bytes(8, 4096) == 4352 and qlin.row_bytes(2, 3584) == 2016
+    assert qlin.row_bytes(12, 100) == 0
+    assert qlin.lib().qlin_q8_1_row_bytes(4096) == 128 * 36 and qlin.lib().qlin_q8_1_row_bytes(40) == 72
+
+
+def test_status_strings():
+    for rc in range(8):
+        assert qlin.lib().qlin_status_string(rc)
+    assert qlin.lib().qlin_status_string(99) == b"unknown status"
+
+
+FAKE = 0x10000  # a 64 KiB-aligned non-null address; never dereferenced (validation fails first)
+
+
+@pytest.mark.parametrize("args,expected", [
+    ((3, FAKE, 18, FAKE, FAKE, 4, 32, 1), UNSUP),       # Q4_1: not supported (the reference no-ops)
+    ((12, FAKE, 144, FAKE, FAKE, 4, 255, 1), SHAPE),    # K not a multiple of 256
+    ((12, FAKE, 144, FAKE, FAKE, -1, 256, 1), SHAPE),
+    ((12, FAKE, 144, FAKE, FAKE, 4, 256, -1), SHAPE),
+    ((12, FAKE, 144, FAKE, FAKE, 4, 0, 1), SHAPE),
+    ((12, FAKE, 143, FAKE, FAKE, 4, 256, 1), ROWB),     # stride shorter than one row
+    ((12, 0, 144, FAKE, FAKE, 4, 256, 1), NULL),
+    ((12, FAKE, 144, 0, FAKE, 4, 256, 1), NULL),
+    ((12, FAKE, 144, FAKE, 0, 4, 256, 1), NULL),
+    ((12, FAKE + 1, 144, FAKE, FAKE, 4, 256, 1), ALIGN),
+    ((12, FAKE, 144, FAKE + 2, FAKE, 4, 256, 1), ALIGN),
+    ((8, FAKE, 35, FAKE, FAKE, 4, 32, 1), ALIGN),        # odd row stride: f16 fields misaligned
+])
+def test_gemv_validation(args, expected):
+    assert qlin.status("qlin_launch_quant_gemv", *args) == expected
+    assert qlin.status("qlin_launch_quant_matmul", *args) == expected
+
+
+def test_empty_work_is_a_noop():
+    # out_dim == 0 or m == 0: nothing to do, no launch, status OK even with null buffers
+    assert qlin.status("qlin_launch_quant_gemv", 12, 0, 144, 0, 0, 0, 256, 1) == OK
+    assert qlin.status("qlin_launch_quant_gemv", 12, FAKE, 144, 0, 0, 4, 256, 0) == OK
+    assert qlin.status("qlin_launch_dequantize_to_f16", 12, 0, 0, 0) == OK
+    assert qlin.status("qlin_launch_quantize_q8_1", 0, 0, 32, 0, 0) == OK
+    assert qlin.status("qlin_launch_moe_router_topk", 0, 0, 0, 0, 64, 6, 1.0) == OK
+
+
+def test_dequant_validation():
+    assert qlin.status("qlin_launch_dequantize_to_f16", 12, FAKE, FAKE, 255) == SHAPE
+    assert qlin.status("qlin_launch_dequantize_to_f16", 9, FAKE, FAKE, 32) == UNSUP
+    assert qlin.status("qlin_launch_dequantize_to_f32", 8, FAKE, FAKE + 2, 32) == ALIGN
+    assert qlin.status("qlin_launch_dequantize_q4k_to_f16", 0, FAKE, 256) == NULL
+    assert qlin.status("qlin_launch_dequantize_q80_to_f16", FAKE, FAKE, 33) == SHAPE
+
+
+def test_router_validation():
+    assert qlin.status("qlin_launch_moe_router_topk", FAKE, FAKE, FAKE, 16, 257, 6, 1.0) == LIMIT
+    assert qlin.status("qlin_launch_moe_router_topk", FAKE, FAKE, FAKE, 16, 0, 6, 1.0) == SHAPE
+    assert qlin.status("qlin_launch_moe_router_topk", FAKE, 0, FAKE, 16, 64, 6, 1.0) == NULL
+
+
+def test_moe_facade_rejections_follow_tensortool():
+    # TensorTool.cpp:277-305: null route pointers, unsupported down / gate-up dtypes, bad shapes
+    a = dict(gate=FAKE, up=FAKE, gub=64 * 1408 * 1152, down=FAKE, db=64 * 2048 * 968, ne=64, ffn=1408,
+             ind=2048, hid=2048, x=FAKE, ids=FAKE, rw=FAKE, act=FAKE, out=FAKE, k=6)
+
+    def run(gu=12, dt=6, **kw):
+        v = {**a, **kw}
+        return qlin.status("qlin_moe_routed_decode_indexed", gu, v["gate"], v["up"], v["gub"], dt, v["down"],
+                           v["db"], v["ne"], v["ffn"], v["ind"], v["hid"], v["x"], v["ids"], v["rw"], v["act"],
+                           v["out"], v["k"])
+    assert run(ids=0) == NULL
+    assert run(rw=0) == NULL
+    assert run(dt=2) == UNSUP          # Q4_0 down is not accepted by the reference's rule
+    assert run(gu=8) == UNSUP          # gate/up must be Q4_K or Q6_K
+    assert run(dt=12) == SHAPE         # Q4_K down with ffn 1408 (not a multiple of 256): rejected
+    assert run(gub=64 * 1408 * 1152 - 64) == ROWB
+    assert run(ne=0) == SHAPE
+
+
+def test_swiglu_and_down_validation():
+    assert qlin.status("qlin_launch_quant_swiglu_indexed", 12, FAKE, FAKE, 100, 100, 144, 144, FAKE, FAKE, FAKE,
+                       2, 1, 256) == ROWB
+    assert qlin.status("qlin_launch_quant_swiglu_indexed", 12, FAKE, FAKE, 144, 144, 144, 144, FAKE, 0, FAKE,
+                       2, 1, 256) == NULL
+    assert qlin.status("qlin_launch_quant_down_f32_indexed_accum_ordered", 6, FAKE, 22, 22, FAKE, FAKE, FAKE,
+                       FAKE, 2, 1, 33) == SHAPE
+
+
+def test_cpp_shim_compiles():
+    """The C++ shim with the reference's launcher names builds against the C ABI."""
+    gxx = shutil.which("g++")
+    if not gxx:
+        pytest.skip("g++ not available")
+    src = os.path.join(ROOT, "include", "qlin_launch.hpp")
+    r = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-x", "c++", "-I", os.path.join(ROOT, "include"), src],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

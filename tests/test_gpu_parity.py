@@ -1,0 +1,321 @@
+"""Parity of the HIP kernels (through the C ABI) with the CPU oracle on the same seeded inputs.
+
+Bars: dequantized values bit-exact (f32 and f16); Q8_1 bytes bit-exact; router indices exact;
+linear outputs within max|y - ref| / max|ref| <= 1e-3 (the gate), and also within 1e-5, the fp32
+deviation the oracle's own fp32 orders show against the double-precision truth.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+import qgen
+from blog_amd import qlin
+from gpu_util import banner, bind_stream, dev, empty_f32, host
+from qgen import Q4_0, Q5_0, Q8_0, Q4_K, Q6_K, f16_bits, normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+GATE = 1e-3
+FP32 = 1e-5      # expected fp32 accumulation deviation
+
+
+@pytest.fixture(autouse=True)
+def _stream():
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    bind_stream()
+    yield
+    torch.cuda.synchronize()
+
+
+def gpu_gemv(qtype, w, rb, x, out_dim, in_dim, m=1, w_offset=0):
+    wd = dev(np.concatenate([np.zeros(w_offset, np.uint8), w])) if w_offset else dev(w)
+    xd = dev(np.ascontiguousarray(x, np.float32).reshape(m, in_dim))
+    yd = empty_f32(m, out_dim)
+    qlin.quant_gemv(qtype, wd.data_ptr() + w_offset, rb, xd, yd, out_dim, in_dim, m)
+    return host(yd)
+
+
+# ---- dequant -----------------------------------------------------------------------------------
+
+def edge_blocks(qtype):
+    """Blocks with extreme f16 scales: subnormal, max finite, negative, zero."""
+    rng = np.random.default_rng(5)
+    w, _ = qgen.random_blocks(qtype, 8, rng)
+    bb = qgen.BLOCK[qtype][1]
+    w = w.reshape(8, bb).copy()
+    scales = [0x0001, 0x03FF, 0x7BFF, 0xBC00, 0x0000, 0x8001, 0x3555, 0xFBFF]
+    for i, s in enumerate(scales):
+        off = 208 if qtype == Q6_K else 0
+        w[i, off:off + 2] = np.array([s & 0xFF, s >> 8], np.uint8)
+        if qtype == Q4_K:
+            w[i, 2:4] = np.array([scales[-1 - i] & 0xFF, scales[-1 - i] >> 8], np.uint8)
+    return w.reshape(-1)
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
+def test_dequant_bit_exact(qtype):
+    rng = np.random.default_rng(200 + qtype)
+    nb = 6000 if qgen.BLOCK[qtype][0] == 32 else 1500
+    w, _ = qgen.random_blocks(qtype, nb, rng)
+    w = np.concatenate([w, edge_blocks(qtype)])
+    n = (w.size // qgen.BLOCK[qtype][1]) * qgen.BLOCK[qtype][0]
+    banner(f"dequant type={qtype} n={n}")
+    wd = dev(w)
+    o16 = torch.zeros(n, dtype=torch.int16, device="cuda")
+    o32 = empty_f32(n)
+    qlin.dequantize(qtype, wd, o16, n, f16=True)
+    qlin.dequantize(qtype, wd, o32, n, f16=False)
+    _same_bits(host(o32).view(np.uint32), orc.dequant_f32(qtype, w, n).view(np.uint32), "f32")
+    _same_bits(host(o16).view(np.uint16), orc.dequant_f16(qtype, w, n), "f16")
+
+
+def _same_bits(got, ref, what):
+    bad = np.nonzero(got != ref)[0]
+    if bad.size:
+        i = bad[:8]
+        pytest.fail(f"{what}: {bad.size} mismatches, first at {i.tolist()}: got {got[i].tolist()} "
+                    f"expected {ref[i].tolist()}")
+
+
+def test_dequant_reference_names():
+    w = qgen.random_matrix(Q4_K, 4, 512, seed=3)[0]
+    n = 4 * 512
+    o = torch.zeros(n, dtype=torch.int16, device="cuda")
+    qlin.call("qlin_launch_dequantize_q4k_to_f16", dev(w), o, n)
+    assert np.array_equal(host(o).view(np.uint16), orc.dequant_f16(Q4_K, w, n))
+
+
+# ---- GEMV --------------------------------------------------------------------------------------
+
+GEMV_CASES = [
+    (Q4_K, 1, 256), (Q4_K, 3, 512), (Q4_K, 17, 3584), (Q4_K, 4097, 8448),
+    (Q4_K, 512, 3584), (Q4_K, 3584, 3584), (Q4_K, 18944, 3584), (Q4_K, 3584, 18944),
+    (Q8_0, 4096, 4096), (Q8_0, 7, 96), (Q8_0, 4864, 896),
+    (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64),
+    (Q5_0, 2048, 1408), (Q5_0, 5, 64),
+    (Q6_K, 64, 512), (Q6_K, 257, 2048),
+]
+
+
+@pytest.mark.parametrize("qtype,out_dim,in_dim", GEMV_CASES)
+def test_gemv_parity(qtype, out_dim, in_dim):
+    w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=out_dim * 7 + in_dim + qtype)
+    x = qgen.random_x(1, in_dim, seed=in_dim + 1)
+    banner(f"gemv type={qtype} N={out_dim} K={in_dim}")
+    y = gpu_gemv(qtype, w, rb, x, out_dim, in_dim)
+    ref = orc.matmul_f64(qtype, w, rb, x, out_dim, in_dim)
+    err = normwise_rel_err(y, ref)
+    assert err <= GATE and err <= FP32, err
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(300, 3584), (1000, 8448)])
+def test_gemv_q4k_generic_path_agrees(out_dim, in_dim):
+    """A weight pointer that is not 16-byte aligned takes the generic kernel: same results."""
+    w, rb, _ = qgen.random_matrix(Q4_K, out_dim, in_dim, seed=11)
+    x = qgen.random_x(1, in_dim, seed=12)
+    banner(f"gemv generic Q4_K N={out_dim} K={in_dim}")
+    y_fast = gpu_gemv(Q4_K, w, rb, x, out_dim, in_dim)
+    y_gen = gpu_gemv(Q4_K, w, rb, x, out_dim, in_dim, w_offset=2)
+    ref = orc.matmul_f64(Q4_K, w, rb, x, out_dim, in_dim)
+    assert normwise_rel_err(y_fast, ref) <= FP32
+    assert normwise_rel_err(y_gen, ref) <= FP32
+
+
+@pytest.mark.parametrize("qtype,m", [(Q4_K, 2), (Q4_K, 5), (Q8_0, 3), (Q4_0, 9)])
+def test_gemv_several_rows(qtype, m):
+    in_dim = 1024
+    w, rb, _ = qgen.random_matrix(qtype, 200, in_dim, seed=m)
+    x = qgen.random_x(m, in_dim, seed=m + 1)
+    banner(f"gemv m={m} type={qtype}")
+    y = gpu_gemv(qtype, w, rb, x, 200, in_dim, m=m)
+    ref = orc.matmul_f64(qtype, w, rb, x, 200, in_dim)
+    assert normwise_rel_err(y, ref) <= FP32
+    # the matmul entry point computes the same contraction
+    yd = empty_f32(m, 200)
+    qlin.quant_matmul(qtype, dev(w), rb, dev(x), yd, 200, in_dim, m)
+    assert normwise_rel_err(host(yd), ref) <= FP32
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q8_0, Q5_0])
+def test_gemv_add(qtype):
+    in_dim = 512
+    w, rb, _ = qgen.random_matrix(qtype, 333, in_dim, seed=21)
+    x = qgen.random_x(1, in_dim, seed=22)[0]
+    y0 = np.random.default_rng(23).standard_normal(333).astype(np.float32) * 100
+    yd = dev(y0)
+    banner(f"gemv_add type={qtype}")
+    qlin.quant_gemv_add(qtype, dev(w), rb, dev(x), yd, 333, in_dim)
+    ref = orc.gemv_add(qtype, w, rb, x, y0, 333, in_dim)
+    assert normwise_rel_err(host(yd), ref) <= FP32
+
+
+def test_gemm_facade_derives_row_bytes():
+    w, rb, _ = qgen.random_matrix(Q4_K, 96, 768, seed=31)
+    x = qgen.random_x(1, 768, seed=32)
+    yd = empty_f32(1, 96)
+    qlin.call("qlin_gemm", Q4_K, dev(w), w.size, dev(x), yd, 96, 768, 1)
+    assert normwise_rel_err(host(yd), orc.matmul_f64(Q4_K, w, rb, x, 96, 768)) <= FP32
+
+
+def test_gemv_linearity_full_size():
+    """Size-independent property at the metric's gate shape: y(a x1 + b x2) = a y(x1) + b y(x2)."""
+    w, rb, _ = qgen.random_matrix(Q4_K, 18944, 3584, seed=41)
+    x = qgen.random_x(2, 3584, seed=42)
+    banner("gemv linearity 18944x3584")
+    y = gpu_gemv(Q4_K, w, rb, x[0], 18944, 3584)[0], gpu_gemv(Q4_K, w, rb, x[1], 18944, 3584)[0]
+    yc = gpu_gemv(Q4_K, w, rb, 2.0 * x[0] - 0.5 * x[1], 18944, 3584)[0]
+    assert normwise_rel_err(yc, 2.0 * y[0].astype(np.float64) - 0.5 * y[1]) <= FP32
+
+
+def test_empty_calls_are_noops():
+    w, rb, _ = qgen.random_matrix(Q4_K, 4, 256, seed=1)
+    yd = dev(np.full(4, 7.0, np.float32))
+    qlin.quant_gemv(Q4_K, dev(w), rb, dev(np.zeros(256, np.float32)), yd, 0, 256, 1)
+    qlin.quant_gemv(Q4_K, dev(w), rb, dev(np.zeros(256, np.float32)), yd, 4, 256, 0)
+    assert np.all(host(yd) == 7.0)
+
+
+# ---- reference known-answer tests on the GPU (LaunchAddTest.cpp) --------------------------------
+
+def _kat_blocks():
+    from test_oracle import kat_x, q4k_kat_block, q6k_kat_block
+    return kat_x(), q4k_kat_block(), q6k_kat_block()
+
+
+@pytest.mark.parametrize("which", ["q4k", "q6k"])
+def test_kats(which):
+    x, q4k, q6k = _kat_blocks()
+    qtype, w, expected = (Q4_K, q4k, 2212.0) if which == "q4k" else (Q6_K, q6k, 948.0)
+    y = gpu_gemv(qtype, w, w.size, x, 1, 256)
+    assert abs(y[0, 0] - expected) <= 1e-3
+    xq = torch.zeros(qlin.lib().qlin_q8_1_row_bytes(256), dtype=torch.uint8, device="cuda")
+    qlin.quantize_q8_1(dev(x), xq, 256, 1)
+    yd = empty_f32(1, 1)
+    qlin.quant_matmul_q8_1(qtype, dev(w), w.size, xq, yd, 1, 256, 1)
+    assert abs(host(yd)[0, 0] - expected) <= 1e-3
+
+
+def test_kat_q8_0_rows_and_q8_1_sums():
+    w = np.zeros(68, np.uint8)
+    for row in range(2):
+        w[row * 34:row * 34 + 2] = [0x00, 0x3C]
+        for k in range(32):
+            w[row * 34 + 2 + k] = (1 if row == 0 else (2 if k % 2 == 0 else -1)) & 0xFF
+    x = np.array(list(range(1, 33)) + [-v for v in range(1, 33)] + [1, -1] * 16, np.float32).reshape(3, 32)
+    yd = empty_f32(3, 2)
+    qlin.quant_matmul(Q8_0, dev(w), 34, dev(x), yd, 2, 32, 3)
+    y = host(yd)
+    for r in range(3):
+        assert abs(y[r, 0] - x[r].sum()) <= 1e-5
+        assert abs(y[r, 1] - sum(x[r, k] * (2 if k % 2 == 0 else -1) for k in range(32))) <= 1e-5
+    xs = np.full(32, 0.01, np.float32)
+    xs[0] = 1.0
+    for raw, expected in ((False, 158.0 / 127.0), (True, 1.31)):
+        xq = torch.zeros(36, dtype=torch.uint8, device="cuda")
+        qlin.quantize_q8_1(dev(xs), xq, 32, 1, store_raw_sum=raw)
+        s = qgen.f16_val(host(xq)[2:4].view("<u2"))[0]
+        assert abs(s - expected) <= 1e-3
+
+
+# ---- Q8_1 ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("raw", [False, True])
+def test_quantize_q8_1_bit_exact(raw):
+    in_dim, m = 4096 + 40, 5
+    x = qgen.random_x(m, in_dim, seed=51) * np.float32(3.0)
+    x[1, 64:96] = 0.0
+    x[2, 5] = 1e-30
+    rb = qlin.lib().qlin_q8_1_row_bytes(in_dim)
+    xq = torch.zeros(m * rb, dtype=torch.uint8, device="cuda")
+    qlin.quantize_q8_1(dev(x), xq, in_dim, m, store_raw_sum=raw)
+    assert np.array_equal(host(xq), orc.quantize_q8_1(x, in_dim, raw))
+
+
+@pytest.mark.parametrize("qtype,out_dim,in_dim,m", [(Q4_K, 96, 1024, 7), (Q6_K, 40, 512, 3), (Q8_0, 50, 256, 4),
+                                                    (Q5_0, 33, 128, 2), (Q4_0, 17, 64, 3), (Q4_K, 512, 4096, 64)])
+def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
+    w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=61 + out_dim)
+    x = qgen.random_x(m, in_dim, seed=62)
+    xq_h = orc.quantize_q8_1(x, in_dim)
+    banner(f"matmul_q8_1 type={qtype} N={out_dim} K={in_dim} m={m}")
+    yd = empty_f32(m, out_dim)
+    qlin.quant_matmul_q8_1(qtype, dev(w), rb, dev(xq_h), yd, out_dim, in_dim, m)
+    ref = orc.matmul_q8_1(qtype, w, rb, xq_h, out_dim, in_dim, m)
+    assert normwise_rel_err(host(yd), ref) <= FP32
+
+
+# ---- MoE ----------------------------------------------------------------------------------------
+
+def test_router_topk():
+    rng = np.random.default_rng(71)
+    logits = rng.standard_normal((16, 64)).astype(np.float32)
+    logits[3, :] = 0.5                 # all tied: 0..5 in order
+    logits[4, 7] = np.nan
+    logits[5, :] = np.nan              # nothing finite
+    logits[6, [9, 4, 60]] = 9.0        # tie at the top
+    idx_d = torch.zeros((16, 6), dtype=torch.int32, device="cuda")
+    w_d = empty_f32(16, 6)
+    qlin.call("qlin_launch_moe_router_topk", dev(logits), idx_d, w_d, 16, 64, 6, 1.0)
+    idx_r, w_r = orc.router_topk(logits, 6, 1.0)
+    assert np.array_equal(host(idx_d), idx_r)
+    assert np.allclose(host(w_d), w_r, rtol=1e-5, atol=1e-7)
+
+
+def _experts(qtype, E, rows, cols, seed):
+    w, rb, vals = qgen.random_matrix(qtype, E * rows, cols, seed=seed)
+    return w, rb, rows * rb
+
+
+def test_swiglu_indexed_and_down_ordered():
+    E, ffn, hid, k = 8, 96, 512, 4
+    wg, grb, geb = _experts(Q4_K, E, ffn, hid, 81)
+    wu, _, _ = _experts(Q4_K, E, ffn, hid, 82)
+    wdn, drb, deb = _experts(Q5_0, E, hid, ffn, 83)
+    x = qgen.random_x(1, hid, seed=84)[0]
+    ids = np.array([5, -1, 0, 7], np.int32)
+    rw = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    act_d = empty_f32(k, ffn)
+    qlin.call("qlin_launch_quant_swiglu_indexed", Q4_K, dev(wg), dev(wu), geb, geb, grb, grb, dev(x), dev(ids),
+              act_d, k, ffn, hid)
+    act_ref = orc.swiglu_indexed(Q4_K, wg, wu, geb, geb, grb, grb, x, ids, ffn, hid)
+    act = host(act_d)
+    assert np.all(act[1] == 0.0)
+    assert normwise_rel_err(act, act_ref) <= 1e-4
+    out0 = np.random.default_rng(85).standard_normal(hid).astype(np.float32)
+    out_d = dev(out0)
+    qlin.call("qlin_launch_quant_down_f32_indexed_accum_ordered", Q5_0, dev(wdn), deb, drb, dev(act_ref), dev(ids),
+              dev(rw), out_d, k, hid, ffn)
+    ref = orc.down_indexed_ordered(Q5_0, wdn, deb, drb, act_ref, ids, rw, out0, hid, ffn)
+    assert normwise_rel_err(host(out_d), ref) <= FP32
+
+
+def test_shared_swiglu():
+    ffn, hid = 200, 768
+    wg, rb, _ = qgen.random_matrix(Q4_K, ffn, hid, seed=91)
+    wu, _, _ = qgen.random_matrix(Q4_K, ffn, hid, seed=92)
+    x = qgen.random_x(1, hid, seed=93)[0]
+    act_d = empty_f32(ffn)
+    qlin.call("qlin_launch_quant_swiglu", Q4_K, dev(wg), dev(wu), rb, rb, dev(x), act_d, ffn, hid)
+    assert normwise_rel_err(host(act_d), orc.swiglu(Q4_K, wg, wu, rb, rb, x, ffn, hid)) <= 1e-4
+
+
+def test_moe_facade_deepseek_shape():
+    """DeepSeek-V2-Lite routed experts (64 x [1408, 2048] Q4_K gate/up, [2048, 1408] Q5_0 down), k = 6."""
+    E, ffn, hid, k = 64, 1408, 2048, 6
+    wg, grb, geb = _experts(Q4_K, E, ffn, hid, 101)
+    wu, _, _ = _experts(Q4_K, E, ffn, hid, 102)
+    wdn, drb, deb = _experts(Q5_0, E, hid, ffn, 103)
+    x = qgen.random_x(1, hid, seed=104)[0]
+    logits = np.random.default_rng(105).standard_normal((1, E)).astype(np.float32)
+    ids, rw = orc.router_topk(logits, k, 1.0)
+    ids, rw = ids[0], rw[0]
+    out0 = np.zeros(hid, np.float32)
+    out_d = dev(out0)
+    act_d = empty_f32(k, ffn)
+    banner("moe facade deepseek shape")
+    qlin.call("qlin_moe_routed_decode_indexed", Q4_K, dev(wg), dev(wu), wg.size, Q5_0, dev(wdn), wdn.size, E, ffn,
+              hid, hid, dev(x), dev(ids), dev(rw), act_d, out_d, k)
+    act_ref = orc.swiglu_indexed(Q4_K, wg, wu, geb, geb, grb, grb, x, ids, ffn, hid)
+    ref = orc.down_indexed_ordered(Q5_0, wdn, deb, drb, act_ref, ids, rw, out0, hid, ffn)
+    assert normwise_rel_err(host(out_d), ref) <= 1e-4
