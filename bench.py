@@ -3,9 +3,11 @@
 One step = one decode token's worth of quantized-linear work: for each of 28 layers the q, k, v, o,
 gate, up and down projections ([3584,3584], [512,3584] x2, [3584,3584], [18944,3584] x2,
 [3584,18944]) plus the lm_head [152064, 3584], all Q4_K with f32 activations (3.98 GB of distinct
-packed weights per token, so the 256 MB Infinity Cache cannot hold them).  The step is captured once
-into a HIP graph (torch.cuda.CUDAGraph) and replayed.  Weights and activations are synthetic and
-resident in HBM before the timed region.
+packed weights per token, so the 256 MB Infinity Cache cannot hold them).  Per layer this is four
+dependent launches, as a decoder issues them: q/k/v together (one launch, they read the same x), o,
+gate/up fused with SiLU (the reference's launch_quant_swiglu), and down reading that activation;
+then the lm_head.  The step is captured once into a HIP graph (torch.cuda.CUDAGraph) and replayed.
+Weights and activations are synthetic and resident in HBM before the timed region.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
@@ -50,6 +52,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--probe-only", action="store_true",
+                    help="only the gate/up SwiGLU kernel, eagerly, plus a 1 GiB copy (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -65,6 +69,9 @@ def main() -> int:
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
 
+    if args.probe_only:
+        return probe_only(torch, qlin, gen, rb_h)
+
     log("generating synthetic Q4_K weights (28 layers + lm_head)")
     shapes = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
               ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN)]
@@ -74,22 +81,29 @@ def main() -> int:
     x_a = torch.randn(HIDDEN, device="cuda", generator=gen)
     x_f = torch.randn(FFN, device="cuda", generator=gen)
     outs = {name: torch.empty(n, device="cuda") for name, n, _ in shapes}
+    act = torch.empty(FFN, device="cuda")
     logits = torch.empty(VOCAB, device="cuda")
     xin = {"q": x_h, "k": x_h, "v": x_h, "o": x_a, "gate": x_h, "up": x_h, "down": x_f}
 
-    launches = []
-    for L in layers:
-        for name, n, k in shapes:
-            launches.append((L[name], rb_f if k == FFN else rb_h, xin[name], outs[name], n, k))
-    launches.append((lm_head, rb_h, x_h, logits, VOCAB, HIDDEN))
-    bytes_per_step = sum(w.numel() + 4 * k + 4 * n for w, _, _, _, n, k in launches)
-    weight_bytes = sum(w.numel() for w, *_ in launches)
-    log(f"{len(launches)} GEMVs per step, {weight_bytes / 1e9:.3f} GB packed weights")
+    # algorithmic bytes: packed weights + f32 inputs read + f32 outputs written, per launch
+    per_layer = (sum(layers[0][n].numel() for n in ("q", "k", "v")) + 4 * HIDDEN + 4 * (HIDDEN + 2 * KV)
+                 + layers[0]["o"].numel() + 4 * HIDDEN + 4 * HIDDEN
+                 + layers[0]["gate"].numel() + layers[0]["up"].numel() + 4 * HIDDEN + 4 * FFN
+                 + layers[0]["down"].numel() + 4 * FFN + 4 * HIDDEN)
+    bytes_per_step = LAYERS * per_layer + lm_head.numel() + 4 * HIDDEN + 4 * VOCAB
+    weight_bytes = sum(t.numel() for L in layers for t in L.values()) + lm_head.numel()
+    n_launches = 4 * LAYERS + 1
+    log(f"{n_launches} launches per step, {weight_bytes / 1e9:.3f} GB packed weights")
 
     def step():
         qlin.set_stream(torch.cuda.current_stream())
-        for w, rb, x, y, n, k in launches:
-            qlin.quant_gemv(Q4_K, w, rb, x, y, n, k, 1)
+        for L in layers:
+            qlin.quant_gemv_multi(Q4_K, [L["q"], L["k"], L["v"]], rb_h, x_h, [outs["q"], outs["k"], outs["v"]],
+                                  [HIDDEN, KV, KV], HIDDEN)
+            qlin.quant_gemv(Q4_K, L["o"], rb_h, x_a, outs["o"], HIDDEN, HIDDEN, 1)
+            qlin.quant_swiglu(Q4_K, L["gate"], L["up"], rb_h, rb_h, x_h, act, FFN, HIDDEN)
+            qlin.quant_gemv(Q4_K, L["down"], rb_f, act, outs["down"], HIDDEN, FFN, 1)
+        qlin.quant_gemv(Q4_K, lm_head, rb_h, x_h, logits, VOCAB, HIDDEN, 1)
 
     # eager warm-up (also initialises the library's per-device state outside capture)
     step()
@@ -118,28 +132,11 @@ def main() -> int:
     gbs = bytes_per_step * args.steps / wall / 1e9
     log(f"{ms_per_step:.4f} ms/step (events {gpu_s / args.steps * 1e3:.4f}), {gbs:.1f} GB/s")
 
-    # ---- roofline probe: the dominant kernel (Q4_K GEMV at the gate/up shape), on its own --------
-    # 56 distinct [18944, 3584] matrices (2.14 GB) per replay; events on the launch stream.
-    probe = torch.cuda.CUDAGraph()
-    probe_mats = [L[n] for L in layers for n in ("gate", "up")]
-    with torch.cuda.graph(probe):
-        qlin.set_stream(torch.cuda.current_stream())
-        for w in probe_mats:
-            qlin.quant_gemv(Q4_K, w, rb_h, x_h, outs["gate"], FFN, HIDDEN, 1)
-    for _ in range(3):
-        probe.replay()
-    torch.cuda.synchronize()
-    reps = 20
-    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    pe0.record()
-    for _ in range(reps):
-        probe.replay()
-    pe1.record()
-    torch.cuda.synchronize()
-    launch_us = pe0.elapsed_time(pe1) * 1e3 / (reps * len(probe_mats))
-    gate_bytes = FFN * rb_h + 4 * HIDDEN + 4 * FFN
-    achieved = gate_bytes / (launch_us * 1e-6) / 1e9
-    log(f"gate GEMV: {launch_us:.2f} us/launch, {achieved:.1f} GB/s")
+    # ---- roofline probe: the dominant kernel (Q4_K gate/up + SiLU), on its own -------------------
+    launch_us, achieved, gate_bytes = roofline_probe(torch, qlin, [(L["gate"], L["up"]) for L in layers], x_h, act,
+                                                     rb_h, reps=20, graph=True)
+    log(f"gate/up SwiGLU: {launch_us:.2f} us/launch, {achieved:.1f} GB/s")
+    traffic = read_traffic()
 
     result = {
         "metric": "decode GEMV HBM GB/s (% of peak) + tokens/s, Qwen2-7B-shape Q4_K, 1 GPU",
@@ -158,11 +155,12 @@ def main() -> int:
         "data": "synthetic (random Q4_K blocks, f32 N(0,1) activations)",
         "config": {"workload": "qwen2-7b-q4k-decode-token", "layers": LAYERS, "hidden": HIDDEN, "ffn": FFN,
                    "kv_dim": KV, "vocab": VOCAB, "weight_format": "Q4_K", "batch": 1,
-                   "gemvs_per_step": len(launches), "algorithmic_bytes_per_step": bytes_per_step,
+                   "launches_per_step": n_launches, "algorithmic_bytes_per_step": bytes_per_step,
                    "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "gemv_q4k_kernel<4> [18944 x 3584]", "avg_launch_us": round(launch_us, 3),
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "kernel": "q4k_mfma_kernel<true, 1, 1> (gate/up SwiGLU, 2 x [18944, 3584])",
+                     "avg_launch_us": round(launch_us, 3),
                      "algorithmic_bytes_per_launch": gate_bytes},
     }
 
@@ -171,6 +169,70 @@ def main() -> int:
                                               bytes_per_step)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def roofline_probe(torch, qlin, pairs, x, act, rb, reps, graph):
+    """Times launch_quant_swiglu over distinct (gate, up) pairs; returns (us/launch, GB/s, bytes/launch).
+
+    Events are recorded on the stream the kernels run on (the graph's replay stream, or the
+    current stream when eager), so the figure is the kernel's own average launch duration."""
+    run = lambda: [qlin.quant_swiglu(Q4_K, wg, wu, rb, rb, x, act, FFN, HIDDEN) for wg, wu in pairs]
+    qlin.set_stream(torch.cuda.current_stream())
+    run()
+    torch.cuda.synchronize()
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            qlin.set_stream(torch.cuda.current_stream())
+            run()
+        qlin.set_stream(torch.cuda.current_stream())
+        body = g.replay
+    else:
+        body = run
+    for _ in range(3):
+        body()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        body()
+    e1.record()
+    torch.cuda.synchronize()
+    launch_us = e0.elapsed_time(e1) * 1e3 / (reps * len(pairs))
+    nbytes = 2 * FFN * qlin.row_bytes(Q4_K, HIDDEN) + 4 * HIDDEN + 4 * FFN
+    return launch_us, nbytes / (launch_us * 1e-6) / 1e9, nbytes
+
+
+def probe_only(torch, qlin, gen, rb_h) -> int:
+    """Workload of the --pmc passes: 28 gate/up pairs run eagerly, then a 1 GiB device copy whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters (known 1 GiB read + 1 GiB written)."""
+    pairs = [(synth_q4k(torch, FFN, HIDDEN, gen), synth_q4k(torch, FFN, HIDDEN, gen)) for _ in range(LAYERS)]
+    x = torch.randn(HIDDEN, device="cuda", generator=gen)
+    act = torch.empty(FFN, device="cuda")
+    launch_us, gbs, nbytes = roofline_probe(torch, qlin, pairs, x, act, rb_h, reps=2, graph=False)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"probe: {launch_us:.2f} us/launch (eager, profiled), {nbytes} algorithmic bytes/launch; copy 1 GiB x 2")
+    return 0
+
+
+def read_traffic():
+    """HBM bytes per launch of the probe kernel, from the committed rocprofv3 --pmc summary, or None.
+
+    The summary's 'traffic_bytes_per_launch:' line is FETCH_SIZE + WRITE_SIZE of the kernel,
+    each divided by what the same counter reads per byte for the 1 GiB copy."""
+    path = os.path.join(ROOT, "profiles", "q4k_swiglu_pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(torch, layer, shapes, xin, outs, seconds, bytes_per_step):

@@ -146,6 +146,24 @@ int qlin_launch_quant_matmul(int type, const uint8_t *w, size_t rb, const float 
     return gemv_common(type, w, rb, x, y, out_dim, in_dim, m, false);
 }
 
+int qlin_launch_quant_gemv_multi(int type, int n_mats, const uint8_t *const *weights, size_t rb, const float *x,
+                                 float *const *ys, const int *out_dims, int in_dim) {
+    if (n_mats < 0) return QLIN_ERR_SHAPE;
+    if (n_mats > qlin::kMaxStreamMats) return QLIN_ERR_LIMIT;
+    if (n_mats == 0) return QLIN_OK;
+    if (!weights || !ys || !out_dims) return QLIN_ERR_NULL;
+    bool work = false;
+    for (int i = 0; i < n_mats; ++i) {
+        int rc = check_weight(type, weights[i], rb, out_dims[i], in_dim);
+        if (rc) return rc;
+        if ((rc = check_f32(ys[i], out_dims[i] > 0))) return rc;
+        work = work || out_dims[i] > 0;
+    }
+    int rc = check_f32(x, work);
+    if (rc || !work) return rc;
+    return launched(qlin::gemv_multi(type, weights, ys, out_dims, n_mats, rb, x, in_dim, stream()));
+}
+
 size_t qlin_q8_1_row_bytes(int in_dim) {
     return in_dim <= 0 ? 0 : static_cast<size_t>((in_dim + 31) / 32) * 36;
 }

@@ -18,6 +18,27 @@ const DeviceInfo &device_info();
 hipError_t gemv(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y, int out_dim,
                 int in_dim, int m, bool add, hipStream_t s);
 
+// Several GEMVs that share x (same type, in_dim and row_bytes), as one launch when possible.
+constexpr int kMaxStreamMats = 4;
+hipError_t gemv_multi(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat,
+                      size_t row_bytes, const float *x, int in_dim, hipStream_t s);
+
+// Streaming Q4_K kernels (m == 1): preconditions, several matrices sharing x, fused SwiGLU.
+bool q4k_stream_ok(const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
+                   bool swiglu);
+hipError_t q4k_stream_gemv(const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t row_bytes,
+                           const float *x, int in_dim, bool add, hipStream_t s);
+hipError_t q4k_stream_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
+                             int ffn_dim, int in_dim, hipStream_t s);
+
+// Matrix-core Q4_K kernels (m == 1), same contracts as the streaming ones.
+bool q4k_mfma_ok(const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
+                 bool swiglu);
+hipError_t q4k_mfma_gemv(const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t row_bytes,
+                         const float *x, int in_dim, bool add, hipStream_t s);
+hipError_t q4k_mfma_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
+                           int ffn_dim, int in_dim, hipStream_t s);
+
 // The per-element fallback used for any type / alignment (exposed for tests of the fast paths).
 hipError_t gemv_generic(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,
                         int out_dim, int in_dim, int m, bool add, hipStream_t s);

@@ -1,0 +1,469 @@
+// qlin_q4k_mfma.hip -- Q4_K decode GEMV (m == 1) on the matrix cores, gfx950.
+//
+// Computes y[o] = sum_k w(o, k) x[k] (reference quant_gemv_kernel / quant_gemv_add_kernel,
+// AI/codes/local-llm/src/backend/cuda/ops/kernel.cu:1192-1244) for up to four matrices sharing x
+// (their rows form one concatenated index space), or the fused SwiGLU act[o] = g/(1+exp(-g))*u of a
+// gate/up pair (quant_swiglu_kernel, kernel.cu:1289-1328).
+//
+// Why matrix cores for a GEMV.  Without packed FP32 a CU retires about one wave64 VALU instruction
+// per clock, and decoding a Q4_K weight plus an f32 multiply-add costs about three of them per
+// weight: the VALU would need as long as HBM takes to deliver the bytes.  Here the multiply-adds
+// run on v_mfma_f32_16x16x32_bf16 and the VALU only builds operands (about one instruction per
+// weight) and applies the per-sub-block scales.
+//
+// Exactness.  A nibble q becomes the bf16 value 128 + q, exactly, with one v_perm_b32 and one
+// v_and_or_b32 per two weights.  x is split as hi = bf16(x), lo = bf16(x - hi), so hi + lo equals x
+// to within 2^-18 |x|; products are exact and accumulate in f32.  The 128 offset is removed in the
+// epilogue with the sub-block sums X = sum(hi + lo).
+//
+// Operands of one MFMA (16 weight rows n, K = 32; lane l supplies row or column l % 16 and the
+// eight k-slots 8*(l/16) .. 8*(l/16)+7, the same slots in A and B):
+//   B (weights): lane (n, g = l/16) takes dword t of sub-block pair g of its row -- 4 low nibbles
+//     (sub-block 2g, elements 4t..4t+3) and the 4 high nibbles of the same bytes (sub-block 2g+1).
+//   A (x): row i = 2*j + part holds part (hi or lo) of sub-block j, non-zero only in the slots that
+//     carry sub-block j -- a block-diagonal operand, so that after the 8 MFMAs of a super-block
+//     (t = 0..7) D[2j + part][n] is the complete dot of sub-block j for row n.
+//   D: lane (g, n) holds rows 4g..4g+3 = both parts of sub-blocks 2g and 2g+1 of row n, which is
+//     exactly the pair whose 6-bit scale and min the lane decodes for the epilogue
+//       acc += d*sc*(D_j - 128 X_j) - dmin*m*X_j.
+//
+// Work decomposition.  One workgroup per CU owns a contiguous slice of the rows.  Its work is the
+// flat sequence of steps (16-row tile, matrix, super-block); each wave takes an equal contiguous
+// range of it, keeps D steps of weight loads in flight ahead of the step it computes, and parks one
+// sum per run along a row in LDS; the runs are added in super-block order at the end
+// (deterministic) and only then is y written.
+#include "qlin_device.hpp"
+#include "qlin_internal.hpp"
+
+namespace qlin {
+namespace {
+
+#ifndef QLIN_MFMA_WAVES
+#define QLIN_MFMA_WAVES 16
+#endif
+constexpr int kWaves = QLIN_MFMA_WAVES;
+constexpr int kThreads = kWaves * 64;
+#ifndef QLIN_MFMA_DEPTH
+#define QLIN_MFMA_DEPTH 1
+#endif
+#ifndef QLIN_MFMA_XFIRST
+#define QLIN_MFMA_XFIRST 1  // 1: stage x completely before the first weight load
+#endif
+constexpr size_t kMaxLds = 160 * 1024;
+constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * kThreads
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct MfmaArgs {
+    const uint8_t *w[kMaxStreamMats];
+    float *y[kMaxStreamMats];
+    int row_end[kMaxStreamMats];
+    int nmat;
+    size_t row_bytes;
+    const float *x;
+    int nsb;      // super-blocks per row
+    int total;    // concatenated rows (SwiGLU: rows of each of gate and up)
+    int add;
+};
+
+// The argument arrays, copied into registers once: indexing the kernel-argument struct with a
+// per-lane value would compile to vector loads of the argument segment, whose completion shares the
+// vmcnt counter with the weight stream and forces a full drain of the prefetched loads.
+struct Mats {
+    const uint8_t *w[kMaxStreamMats];
+    float *y[kMaxStreamMats];
+    int end[kMaxStreamMats];
+    int nmat;
+    __device__ explicit Mats(const MfmaArgs &a) : nmat(a.nmat) {
+#pragma unroll
+        for (int i = 0; i < kMaxStreamMats; ++i) {
+            w[i] = a.w[i];
+            y[i] = a.y[i];
+            end[i] = a.row_end[i];
+        }
+    }
+    // matrix of concatenated row gr and the row within it, by compare-and-select
+    __device__ __forceinline__ void locate(int gr, const uint8_t *&wp, float *&yp, int &local) const {
+        wp = w[0];
+        yp = y[0];
+        local = gr;
+#pragma unroll
+        for (int i = 1; i < kMaxStreamMats; ++i) {
+            const bool past = i < nmat && gr >= end[i - 1];
+            wp = past ? w[i] : wp;
+            yp = past ? y[i] : yp;
+            local = past ? gr - end[i - 1] : local;
+        }
+    }
+};
+
+// bf16 bits of f (round to nearest even; finite inputs).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_val(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
+// Lane-constant (scale, min) decode of sub-blocks 2p and 2p+1 (kernel.cu:913-921), packed in bytes
+// 0 and 1 of the results.
+struct ScaleDecoder {
+    bool upper;
+    int sh, m_shift;
+    uint32_t lo_mask, hi_mask;
+    __device__ explicit ScaleDecoder(int p)
+        : upper(p >= 2), sh(p >= 2 ? 16 * (p - 2) : 16 * p), m_shift(p >= 2 ? 4 : 0),
+          lo_mask(p >= 2 ? 0x0f0fu : 0x3f3fu), hi_mask(p >= 2 ? 0x0303u : 0u) {}
+    __device__ __forceinline__ void operator()(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &scp,
+                                               uint32_t &mp) const {
+        const uint32_t a_sc = upper ? s2 : s0;
+        const uint32_t a_m = upper ? s2 : s1;
+        scp = ((a_sc >> sh) & lo_mask) | (((s0 >> (sh + 6)) & hi_mask) << 4);
+        mp = ((a_m >> (sh + m_shift)) & lo_mask) | (((s1 >> (sh + 6)) & hi_mask) << 4);
+    }
+};
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+template <int T>
+struct Step {
+    u32x4 hdr[T], qa[T], qb[T];
+};
+
+// B operand of MFMA t from qs dword v: bf16(128 + q) for the 4 low nibbles, then the 4 high ones.
+// bf16 128 + q has bytes (q, 0x43); v_perm_b32 interleaves the nibble bytes with 0x43 bytes taken
+// from a constant register.
+__device__ __forceinline__ u32x4 weights_operand(uint32_t v) {
+    const uint32_t lo = v & 0x0f0f0f0fu;
+    const uint32_t hi = (v >> 4) & 0x0f0f0f0fu;
+    const uint32_t k43 = 0x43434343u;
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(k43, lo, 0x04010400u);  // (q0, 43, q1, 43)
+    r.y = __builtin_amdgcn_perm(k43, lo, 0x04030402u);  // (q2, 43, q3, 43)
+    r.z = __builtin_amdgcn_perm(k43, hi, 0x04010400u);
+    r.w = __builtin_amdgcn_perm(k43, hi, 0x04030402u);
+    return r;
+}
+
+__device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  D: steps of weights in flight ahead of
+// the one being computed.
+template <bool SWIGLU, int XR, int D>
+__global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
+    constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nsb = a.nsb, K = nsb * 256;
+    uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
+    float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/32] sum(hi + lo) per sub-block
+    float *partial = xsum + K / 32;                                // [rows][NW][nsb]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rb = static_cast<int>(static_cast<int64_t>(a.total) * blockIdx.x / gridDim.x);
+    const int re = static_cast<int>(static_cast<int64_t>(a.total) * (blockIdx.x + 1) / gridDim.x);
+    const int nrows = re - rb;
+    // The workgroup's work is the flat sequence of steps (16-row tile, matrix, super-block); wave w
+    // takes the contiguous range [w * nsteps / W, (w + 1) * nsteps / W), so waves differ by at most
+    // one step and walk along their rows.
+    const int nsteps = (nrows + 15) / 16 * NW * nsb;
+    const int s_begin = wave * nsteps / kWaves, s_end = (wave + 1) * nsteps / kWaves;
+    const int n = lane & 15, g = lane >> 4;
+    const ScaleDecoder dec(g);
+    const Mats mats(a);
+
+    // A-operand role of this lane: row i = n holds part (i & 1) of sub-block i >> 1, which is
+    // carried by the slots of lane-group g only when (i >> 2) == g.
+    const bool a_active = (n >> 2) == g;
+    const bool a_high = (n >> 1) & 1;        // sub-block 2g+1: slots 4..7
+    const int a_part = n & 1;
+
+    // A step of this wave.  Past the wave's last step the position stays on that step (valid
+    // addresses, loads never consumed), so that no load needs a branch.
+    struct Pos {
+        int s, tile, which, sb;
+        const uint8_t *rp;  // this lane's weight row
+    };
+    auto row_ptr = [&](int tile, int which) -> const uint8_t * {
+        const int gr = min(rb + tile * 16 + n, re - 1);
+        if constexpr (SWIGLU) {
+            return (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes;
+        } else {
+            const uint8_t *wp;
+            float *yp;
+            int local;
+            mats.locate(gr, wp, yp, local);
+            return wp + static_cast<size_t>(local) * a.row_bytes;
+        }
+    };
+    auto advance = [&](const Pos &p) {
+        Pos q = p;
+        q.s = p.s + 1;
+        if (q.s >= s_end) return q;  // stays on the last step
+        if (++q.sb == nsb) {
+            q.sb = 0;
+            if (++q.which == NW) {
+                q.which = 0;
+                ++q.tile;
+            }
+            q.rp = row_ptr(q.tile, q.which);
+        }
+        return q;
+    };
+    auto load = [&](Step<1> &st, const Pos &p) {
+        const uint8_t *q = p.rp + static_cast<size_t>(p.sb) * 144;
+        st.hdr[0] = ld16(q);
+        st.qa[0] = ld16(q + 16 + 32 * g);
+        st.qb[0] = ld16(q + 32 + 32 * g);
+    };
+
+    if (nsteps == 0) return;  // uniform per workgroup
+
+    // x first: requested before any weight load of the workgroup (the barrier orders them in the
+    // CU's memory queue), so that its staging is not held up behind the HBM weight stream.  Every
+    // load is branch-free, which lets the compiler wait for exactly the loads a step consumes and
+    // keep the younger ones in flight.
+    float4 xv[XR];
+#pragma unroll
+    for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
+    for (int i = tid; i < nrows * NW * nsb; i += kThreads) partial[i] = 0.0f;
+
+    auto stage_x = [&]() {
+        // bf16 hi / lo parts and the per-sub-block sums of hi + lo
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int i = tid + r * kThreads;
+            const float xe[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+            uint32_t hb[4], lb[4];
+            float sm = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hb[e] = bf16_rne(xe[e]);
+                lb[e] = bf16_rne(xe[e] - bf16_val(hb[e]));
+                sm += bf16_val(hb[e]) + bf16_val(lb[e]);
+            }
+            // the 8 threads of a 32-element sub-block are 8 consecutive lanes (K/4 is a multiple of
+            // 64, so every wave is entirely below K/4 or entirely above it)
+            sm += __shfl_xor(sm, 1, 64);
+            sm += __shfl_xor(sm, 2, 64);
+            sm += __shfl_xor(sm, 4, 64);
+            if (i < K / 4) {
+                reinterpret_cast<uint2 *>(xpart)[i] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+                reinterpret_cast<uint2 *>(xpart + K)[i] = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+                if ((i & 7) == 0) xsum[i >> 3] = sm;
+            }
+        }
+    };
+
+    Pos pos[D + 1];
+    {
+        const int per_tile = NW * nsb;
+        const int s0 = min(s_begin, nsteps - 1);
+        pos[0].s = s_begin;
+        pos[0].tile = s0 / per_tile;
+        pos[0].which = (s0 % per_tile) / nsb;
+        pos[0].sb = s0 % nsb;
+        pos[0].rp = row_ptr(pos[0].tile, pos[0].which);
+    }
+#pragma unroll
+    for (int d = 1; d <= D; ++d) pos[d] = advance(pos[d - 1]);
+    Step<1> buf[D + 1];
+#if QLIN_MFMA_XFIRST
+    stage_x();
+    __syncthreads();
+#pragma unroll
+    for (int d = 0; d <= D; ++d) load(buf[d], pos[d]);
+#else
+    __syncthreads();
+#pragma unroll
+    for (int d = 0; d <= D; ++d) load(buf[d], pos[d]);
+    stage_x();
+    __syncthreads();
+#endif
+
+    float acc = 0.0f;
+    int seg_sb = 0;
+    u32x4 aop[8];
+
+    auto process = [&](const Step<1> &cur, const Pos &p) {
+        if (p.s == s_begin || p.sb == 0) {
+            acc = 0.0f;
+            seg_sb = p.sb;
+        }
+        // A operands of this super-block (x only): the lane's 32 values of its part/sub-block.
+        {
+            uint32_t dw[16];
+            if (a_active) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * K + p.sb * 256 + (n >> 1) * 32);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 v = src[q];
+                    dw[4 * q] = v.x; dw[4 * q + 1] = v.y; dw[4 * q + 2] = v.z; dw[4 * q + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) dw[q] = 0u;
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                aop[t].x = a_high ? 0u : dw[2 * t];
+                aop[t].y = a_high ? 0u : dw[2 * t + 1];
+                aop[t].z = a_high ? dw[2 * t] : 0u;
+                aop[t].w = a_high ? dw[2 * t + 1] : 0u;
+            }
+        }
+        const float2 xs = *reinterpret_cast<const float2 *>(xsum + p.sb * 8 + 2 * g);
+        const uint32_t qv[8] = {cur.qa[0].x, cur.qa[0].y, cur.qa[0].z, cur.qa[0].w,
+                                cur.qb[0].x, cur.qb[0].y, cur.qb[0].z, cur.qb[0].w};
+        f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) d = mfma(aop[t], weights_operand(qv[t]), d);
+        uint32_t scp, mp;
+        dec(cur.hdr[0].y, cur.hdr[0].z, cur.hdr[0].w, scp, mp);
+        const float dd = f16_bits_to_f32(cur.hdr[0].x & 0xffffu);
+        const float dmin = f16_bits_to_f32(cur.hdr[0].x >> 16);
+        const float dsc0 = dd * static_cast<float>(scp & 0xffu);
+        const float dsc1 = dd * static_cast<float>((scp >> 8) & 0xffu);
+        const float dm0 = dmin * static_cast<float>(mp & 0xffu);
+        const float dm1 = dmin * static_cast<float>((mp >> 8) & 0xffu);
+        acc = fmaf(dsc0, (d[0] + d[1]) - 128.0f * xs.x, acc);
+        acc = fmaf(dsc1, (d[2] + d[3]) - 128.0f * xs.y, acc);
+        acc = fmaf(-dm0, xs.x, acc);
+        acc = fmaf(-dm1, xs.y, acc);
+        if (p.s + 1 >= s_end || p.sb + 1 == nsb) {
+            // end of this wave's run along the row: add the four lane-groups (sub-block pairs) and
+            // park the sum in LDS (a global store here would share vmcnt with the weight stream)
+            float r = acc;
+            r += __shfl_xor(r, 16, 64);
+            r += __shfl_xor(r, 32, 64);
+            const int gr = rb + p.tile * 16 + n;
+            if (g == 0 && gr < re) partial[((gr - rb) * NW + p.which) * nsb + seg_sb] = r;
+        }
+    };
+
+    // Steady state: step i computes buffer i % (D+1) while step i + D's loads are issued into the
+    // buffer step i - 1 just released.
+    for (;;) {
+        bool done = false;
+#pragma unroll
+        for (int d = 0; d <= D; ++d) {
+            if (pos[d].s >= s_end) {
+                done = true;
+                break;
+            }
+            const Pos nxt = advance(pos[(d + D) % (D + 1)]);
+            process(buf[d], pos[d]);
+            pos[d] = nxt;
+            load(buf[d], nxt);
+        }
+        if (done) break;
+    }
+
+    __syncthreads();
+    for (int r = tid; r < nrows; r += kThreads) {
+        float tot[NW];
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+            tot[q] = 0.0f;
+            for (int sb = 0; sb < nsb; ++sb) tot[q] += partial[(r * NW + q) * nsb + sb];
+        }
+        const int gr = rb + r;
+        if constexpr (SWIGLU) {
+            mats.y[0][gr] = tot[0] / (1.0f + expf(-tot[0])) * tot[1];
+        } else {
+            const uint8_t *wp;
+            float *yp;
+            int local;
+            mats.locate(gr, wp, yp, local);
+            yp[local] = a.add ? yp[local] + tot[0] : tot[0];
+        }
+    }
+}
+
+struct Plan {
+    int grid;
+    size_t lds;
+};
+
+Plan plan(int total, int nsb, bool swiglu) {
+    Plan p;
+    p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
+    const int rows = (total + p.grid - 1) / p.grid;
+    const size_t K = static_cast<size_t>(nsb) * 256;
+    p.lds = 4 * K + (K / 32) * sizeof(float) + static_cast<size_t>(rows) * (swiglu ? 2 : 1) * nsb * sizeof(float);
+    return p;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <bool SWIGLU, int XR>
+void launch_xr(const Plan &p, const MfmaArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((q4k_mfma_kernel<SWIGLU, XR, QLIN_MFMA_DEPTH>), dim3(p.grid), dim3(kThreads), p.lds, s, a);
+}
+
+template <bool SWIGLU>
+void launch_sw(const Plan &p, const MfmaArgs &a, hipStream_t s) {
+    const int need = (a.nsb * 64 + kThreads - 1) / kThreads;  // float4 loads of x per thread
+    if (need <= 1) launch_xr<SWIGLU, 1>(p, a, s);
+    else if (need <= 2) launch_xr<SWIGLU, 2>(p, a, s);
+    else if (need <= 4) launch_xr<SWIGLU, 4>(p, a, s);
+    else if (need <= 6) launch_xr<SWIGLU, 6>(p, a, s);
+    else launch_xr<SWIGLU, kMaxXr>(p, a, s);
+}
+
+hipError_t launch(MfmaArgs &a, bool swiglu, hipStream_t s) {
+    const Plan p = plan(a.total, a.nsb, swiglu);
+    if (swiglu) launch_sw<true>(p, a, s);
+    else launch_sw<false>(p, a, s);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool q4k_mfma_ok(const uint8_t *const *w, int nmat, size_t rb, const float *x, int total, int k, bool swiglu) {
+    if (nmat < 1 || nmat > kMaxStreamMats || k % 256 || rb % 16 || !aligned16(x) || total <= 0) return false;
+    if (k / 4 > kMaxXr * kThreads) return false;
+    for (int i = 0; i < nmat; ++i)
+        if (!aligned16(w[i])) return false;
+    return plan(total, k / 256, swiglu).lds <= kMaxLds;
+}
+
+hipError_t q4k_mfma_gemv(const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,
+                         const float *x, int k, bool add, hipStream_t s) {
+    MfmaArgs a{};
+    int total = 0;
+    for (int i = 0; i < nmat; ++i) {
+        a.w[i] = w[i];
+        a.y[i] = y[i];
+        total += rows[i];
+        a.row_end[i] = total;
+    }
+    if (total == 0) return hipSuccess;
+    a.nmat = nmat;
+    a.row_bytes = rb;
+    a.x = x;
+    a.nsb = k / 256;
+    a.total = total;
+    a.add = add ? 1 : 0;
+    return launch(a, false, s);
+}
+
+hipError_t q4k_mfma_swiglu(const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x, float *act, int ffn,
+                           int k, hipStream_t s) {
+    if (ffn == 0) return hipSuccess;
+    MfmaArgs a{};
+    a.w[0] = wg;
+    a.w[1] = wu;
+    a.y[0] = act;
+    a.row_end[0] = ffn;
+    a.nmat = 1;
+    a.row_bytes = rb;
+    a.x = x;
+    a.nsb = k / 256;
+    a.total = ffn;
+    return launch(a, true, s);
+}
+
+}  // namespace qlin

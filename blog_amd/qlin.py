@@ -30,6 +30,7 @@ SIGNATURES = {
     "qlin_launch_quant_gemv": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_launch_quant_gemv_add": (I, [I, P, SZ, P, P, I, I]),
     "qlin_launch_quant_matmul": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_gemv_multi": (I, [I, I, P, SZ, P, P, P, I]),
     "qlin_q8_1_row_bytes": (SZ, [I]),
     "qlin_launch_quantize_q8_1": (I, [P, P, I, I, I]),
     "qlin_launch_quant_matmul_q8_1": (I, [I, P, SZ, P, P, I, I, I]),
@@ -113,6 +114,19 @@ def quant_gemv(qtype, w, rb, x, y, out_dim, in_dim, m=1):
 
 def quant_gemv_add(qtype, w, rb, x, y, out_dim, in_dim):
     call("qlin_launch_quant_gemv_add", qtype, w, rb, x, y, out_dim, in_dim)
+
+
+def quant_gemv_multi(qtype, ws, rb, x, ys, out_dims, in_dim):
+    """Several GEMVs sharing x in one launch (lists of tensors / device addresses)."""
+    n = len(ws)
+    wa = (C.c_void_p * n)(*[ptr(w) for w in ws])
+    ya = (C.c_void_p * n)(*[ptr(y) for y in ys])
+    da = (C.c_int * n)(*out_dims)
+    call("qlin_launch_quant_gemv_multi", qtype, n, C.addressof(wa), rb, x, C.addressof(ya), C.addressof(da), in_dim)
+
+
+def quant_swiglu(qtype, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim):
+    call("qlin_launch_quant_swiglu", qtype, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim)
 
 
 def quant_matmul(qtype, w, rb, x, y, out_dim, in_dim, m):

@@ -81,6 +81,14 @@ int qlin_launch_quant_gemv_add(int type, const uint8_t *weight, size_t row_bytes
 int qlin_launch_quant_matmul(int type, const uint8_t *weight, size_t row_bytes, const float *x, float *y,
                              int out_dim, int in_dim, int m);
 
+/* n_mats (1..4) GEMVs that share x, as one launch: ys[i][o] = W_i[o] . x for o < out_dims[i].
+ * weights, ys and out_dims are host arrays of n_mats entries (the pointers they hold are device
+ * pointers); all weights have the same type, in_dim and row_bytes.  No reference counterpart: the
+ * reference issues one launch_quant_gemv per matrix (e.g. q, k and v of a layer); on MI355X a
+ * launch costs about 2 us even when empty, so matrices that read the same x are batched. */
+int qlin_launch_quant_gemv_multi(int type, int n_mats, const uint8_t *const *weights, size_t row_bytes,
+                                 const float *x, float *const *ys, const int *out_dims, int in_dim);
+
 /* ---- Q8_1 activations (kernel.cuh:46-54) ------------------------------------------------------ */
 
 /* Bytes of one Q8_1 activation row: ceil(in_dim / 32) * 36.  Replaces q8_1_row_bytes. */

@@ -57,6 +57,13 @@ inline void launch_quant_matmul(DType t, const uint8_t *weight, size_t row_bytes
           "launch_quant_matmul");
 }
 
+// No reference counterpart: q, k and v (or any matrices reading the same x) in one launch.
+inline void launch_quant_gemv_multi(DType t, int n_mats, const uint8_t *const *weights, size_t row_bytes,
+                                    const float *x, float *const *ys, const int *out_dims, int in_dim) {
+    check(qlin_launch_quant_gemv_multi(static_cast<int>(t), n_mats, weights, row_bytes, x, ys, out_dims, in_dim),
+          "launch_quant_gemv_multi");
+}
+
 // kernel.cuh:46-54
 inline size_t q8_1_row_bytes(int in_dim) { return qlin_q8_1_row_bytes(in_dim); }
 inline void launch_quantize_q8_1(const float *x, uint8_t *x_q8_1, int in_dim, int m, bool store_raw_sum = false) {

@@ -89,6 +89,22 @@ def test_empty_work_is_a_noop():
     assert qlin.status("qlin_launch_moe_router_topk", 0, 0, 0, 0, 64, 6, 1.0) == OK
 
 
+def test_gemv_multi_validation():
+    import ctypes as C
+    w = (C.c_void_p * 5)(*([FAKE] * 5))
+    y = (C.c_void_p * 5)(*([FAKE] * 5))
+    d = (C.c_int * 5)(*([4] * 5))
+    addr = C.addressof
+    assert qlin.status("qlin_launch_quant_gemv_multi", 12, 5, addr(w), 144, FAKE, addr(y), addr(d), 256) == LIMIT
+    assert qlin.status("qlin_launch_quant_gemv_multi", 12, -1, addr(w), 144, FAKE, addr(y), addr(d), 256) == SHAPE
+    assert qlin.status("qlin_launch_quant_gemv_multi", 12, 3, 0, 144, FAKE, addr(y), addr(d), 256) == NULL
+    assert qlin.status("qlin_launch_quant_gemv_multi", 3, 3, addr(w), 144, FAKE, addr(y), addr(d), 256) == UNSUP
+    assert qlin.status("qlin_launch_quant_gemv_multi", 12, 3, addr(w), 100, FAKE, addr(y), addr(d), 256) == ROWB
+    assert qlin.status("qlin_launch_quant_gemv_multi", 12, 0, 0, 144, 0, 0, 0, 256) == OK
+    w[1] = 0
+    assert qlin.status("qlin_launch_quant_gemv_multi", 12, 3, addr(w), 144, FAKE, addr(y), addr(d), 256) == NULL
+
+
 def test_dequant_validation():
     assert qlin.status("qlin_launch_dequantize_to_f16", 12, FAKE, FAKE, 255) == SHAPE
     assert qlin.status("qlin_launch_dequantize_to_f16", 9, FAKE, FAKE, 32) == UNSUP
