@@ -28,10 +28,13 @@
 //       acc += d*sc*(D_j - 128 X_j) - dmin*m*X_j.
 //
 // Work decomposition.  One workgroup per CU owns a contiguous slice of the rows.  Its work is the
-// flat sequence of steps (16-row tile, matrix, super-block); each wave takes an equal contiguous
-// range of it, keeps D steps of weight loads in flight ahead of the step it computes, and parks one
-// sum per run along a row in LDS; the runs are added in super-block order at the end
-// (deterministic) and only then is y written.
+// flat sequence of steps (16-row tile, matrix, super-block), in memory order; the waves claim the
+// steps one at a time from an LDS counter, so the workgroup reads one compact window that slides
+// along its slice (waves with separate contiguous ranges each open their own window, and HBM
+// serves many scattered windows measurably slower), and no wave is left with a backlog at the end.
+// A wave loads the step it will compute next while it computes the current one, and parks each
+// step's 16 row sums in LDS; they are added in super-block order at the end (deterministic) and
+// only then is y written.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 
@@ -43,11 +46,8 @@ namespace {
 #endif
 constexpr int kWaves = QLIN_MFMA_WAVES;
 constexpr int kThreads = kWaves * 64;
-#ifndef QLIN_MFMA_DEPTH
-#define QLIN_MFMA_DEPTH 1
-#endif
-#ifndef QLIN_MFMA_XFIRST
-#define QLIN_MFMA_XFIRST 1  // 1: stage x completely before the first weight load
+#ifndef QLIN_MFMA_MATMAJOR
+#define QLIN_MFMA_MATMAJOR 1  // SwiGLU steps: 1 = all gate tiles, then all up tiles; 0 = tile-major
 #endif
 constexpr size_t kMaxLds = 160 * 1024;
 constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * kThreads
@@ -150,9 +150,8 @@ __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x
                                                    0, 0, 0);
 }
 
-// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  D: steps of weights in flight ahead of
-// the one being computed.
-template <bool SWIGLU, int XR, int D>
+// XR: float4 loads of x per thread (K/4 <= XR * kThreads).
+template <bool SWIGLU, int XR>
 __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
     constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -165,11 +164,10 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
     const int rb = static_cast<int>(static_cast<int64_t>(a.total) * blockIdx.x / gridDim.x);
     const int re = static_cast<int>(static_cast<int64_t>(a.total) * (blockIdx.x + 1) / gridDim.x);
     const int nrows = re - rb;
-    // The workgroup's work is the flat sequence of steps (16-row tile, matrix, super-block); wave w
-    // takes the contiguous range [w * nsteps / W, (w + 1) * nsteps / W), so waves differ by at most
-    // one step and walk along their rows.
+    // The workgroup's work is the flat sequence of steps (16-row tile, matrix, super-block), which
+    // is also the order of the bytes in memory; the waves claim them in that order, so that at any
+    // time the workgroup reads one compact window of its rows.
     const int nsteps = (nrows + 15) / 16 * NW * nsb;
-    const int s_begin = wave * nsteps / kWaves, s_end = (wave + 1) * nsteps / kWaves;
     const int n = lane & 15, g = lane >> 4;
     const ScaleDecoder dec(g);
     const Mats mats(a);
@@ -180,37 +178,45 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
     const bool a_high = (n >> 1) & 1;        // sub-block 2g+1: slots 4..7
     const int a_part = n & 1;
 
-    // A step of this wave.  Past the wave's last step the position stays on that step (valid
-    // addresses, loads never consumed), so that no load needs a branch.
+    // A step: tw = tile * NW + matrix, sb = super-block; s = its index in the flat sequence.
     struct Pos {
-        int s, tile, which, sb;
+        int s, tw, sb;
         const uint8_t *rp;  // this lane's weight row
     };
-    auto row_ptr = [&](int tile, int which) -> const uint8_t * {
+    const int ntiles = (nrows + 15) / 16;
+    auto split_tw = [&](int tw, int &tile, int &which) {
+        if constexpr (NW == 1) {
+            tile = tw;
+            which = 0;
+        } else if (QLIN_MFMA_MATMAJOR) {
+            which = tw >= ntiles;
+            tile = tw - which * ntiles;
+        } else {
+            tile = tw >> 1;
+            which = tw & 1;
+        }
+    };
+    // Position of step s (wave-uniform).  Past the last step the position is the last step (valid
+    // addresses, loads never consumed), so that no load needs a branch.
+    auto at = [&](int s) {
+        Pos p;
+        p.s = s;
+        const int c = min(s, nsteps - 1);
+        p.tw = c / nsb;
+        p.sb = c - p.tw * nsb;
+        int tile, which;
+        split_tw(p.tw, tile, which);
         const int gr = min(rb + tile * 16 + n, re - 1);
         if constexpr (SWIGLU) {
-            return (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes;
+            p.rp = (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes;
         } else {
             const uint8_t *wp;
             float *yp;
             int local;
             mats.locate(gr, wp, yp, local);
-            return wp + static_cast<size_t>(local) * a.row_bytes;
+            p.rp = wp + static_cast<size_t>(local) * a.row_bytes;
         }
-    };
-    auto advance = [&](const Pos &p) {
-        Pos q = p;
-        q.s = p.s + 1;
-        if (q.s >= s_end) return q;  // stays on the last step
-        if (++q.sb == nsb) {
-            q.sb = 0;
-            if (++q.which == NW) {
-                q.which = 0;
-                ++q.tile;
-            }
-            q.rp = row_ptr(q.tile, q.which);
-        }
-        return q;
+        return p;
     };
     auto load = [&](Step<1> &st, const Pos &p) {
         const uint8_t *q = p.rp + static_cast<size_t>(p.sb) * 144;
@@ -221,14 +227,12 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
 
     if (nsteps == 0) return;  // uniform per workgroup
 
-    // x first: requested before any weight load of the workgroup (the barrier orders them in the
-    // CU's memory queue), so that its staging is not held up behind the HBM weight stream.  Every
-    // load is branch-free, which lets the compiler wait for exactly the loads a step consumes and
-    // keep the younger ones in flight.
+    // x first: requested before any weight load of the workgroup.  Every load is branch-free, which
+    // lets the compiler wait for exactly the loads a step consumes and keep the younger ones in
+    // flight.
     float4 xv[XR];
 #pragma unroll
     for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
-    for (int i = tid; i < nrows * NW * nsb; i += kThreads) partial[i] = 0.0f;
 
     auto stage_x = [&]() {
         // bf16 hi / lo parts and the per-sub-block sums of hi + lo
@@ -257,41 +261,24 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
         }
     };
 
-    Pos pos[D + 1];
-    {
-        const int per_tile = NW * nsb;
-        const int s0 = min(s_begin, nsteps - 1);
-        pos[0].s = s_begin;
-        pos[0].tile = s0 / per_tile;
-        pos[0].which = (s0 % per_tile) / nsb;
-        pos[0].sb = s0 % nsb;
-        pos[0].rp = row_ptr(pos[0].tile, pos[0].which);
-    }
-#pragma unroll
-    for (int d = 1; d <= D; ++d) pos[d] = advance(pos[d - 1]);
-    Step<1> buf[D + 1];
-#if QLIN_MFMA_XFIRST
+    // Steps are handed out dynamically, in memory order: wave w starts with step w, then takes the
+    // next unclaimed one from an LDS counter each time it prefetches.  The waves of a CU are not
+    // served equally (a wave that starts late stays behind), so a fixed share per wave leaves the
+    // workgroup waiting for its slowest wave; claiming on demand ends all waves within about one step
+    // of each other.
+    __shared__ int next_step;
+    if (tid == 0) next_step = kWaves;
+    Pos cur = at(wave);
+    Step<1> buf;
+    load(buf, cur);
     stage_x();
     __syncthreads();
-#pragma unroll
-    for (int d = 0; d <= D; ++d) load(buf[d], pos[d]);
-#else
-    __syncthreads();
-#pragma unroll
-    for (int d = 0; d <= D; ++d) load(buf[d], pos[d]);
-    stage_x();
-    __syncthreads();
-#endif
 
-    float acc = 0.0f;
-    int seg_sb = 0;
     u32x4 aop[8];
 
+    // One step: the 16 rows' dots with super-block sb, parked in LDS (each (row, matrix, sb) slot is
+    // written by exactly one step; a global store here would share vmcnt with the weight stream).
     auto process = [&](const Step<1> &cur, const Pos &p) {
-        if (p.s == s_begin || p.sb == 0) {
-            acc = 0.0f;
-            seg_sb = p.sb;
-        }
         // A operands of this super-block (x only): the lane's 32 values of its part/sub-block.
         {
             uint32_t dw[16];
@@ -328,37 +315,28 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
         const float dsc1 = dd * static_cast<float>((scp >> 8) & 0xffu);
         const float dm0 = dmin * static_cast<float>(mp & 0xffu);
         const float dm1 = dmin * static_cast<float>((mp >> 8) & 0xffu);
-        acc = fmaf(dsc0, (d[0] + d[1]) - 128.0f * xs.x, acc);
-        acc = fmaf(dsc1, (d[2] + d[3]) - 128.0f * xs.y, acc);
-        acc = fmaf(-dm0, xs.x, acc);
-        acc = fmaf(-dm1, xs.y, acc);
-        if (p.s + 1 >= s_end || p.sb + 1 == nsb) {
-            // end of this wave's run along the row: add the four lane-groups (sub-block pairs) and
-            // park the sum in LDS (a global store here would share vmcnt with the weight stream)
-            float r = acc;
-            r += __shfl_xor(r, 16, 64);
-            r += __shfl_xor(r, 32, 64);
-            const int gr = rb + p.tile * 16 + n;
-            if (g == 0 && gr < re) partial[((gr - rb) * NW + p.which) * nsb + seg_sb] = r;
-        }
+        float r = dsc0 * ((d[0] + d[1]) - 128.0f * xs.x);
+        r = fmaf(dsc1, (d[2] + d[3]) - 128.0f * xs.y, r);
+        r = fmaf(-dm0, xs.x, r);
+        r = fmaf(-dm1, xs.y, r);
+        // add the four lane-groups (sub-block pairs)
+        r += __shfl_xor(r, 16, 64);
+        r += __shfl_xor(r, 32, 64);
+        int tile, which;
+        split_tw(p.tw, tile, which);
+        const int lr = tile * 16 + n;
+        if (g == 0 && lr < nrows) partial[(lr * NW + which) * nsb + p.sb] = r;
     };
 
-    // Steady state: step i computes buffer i % (D+1) while step i + D's loads are issued into the
-    // buffer step i - 1 just released.
-    for (;;) {
-        bool done = false;
-#pragma unroll
-        for (int d = 0; d <= D; ++d) {
-            if (pos[d].s >= s_end) {
-                done = true;
-                break;
-            }
-            const Pos nxt = advance(pos[(d + D) % (D + 1)]);
-            process(buf[d], pos[d]);
-            pos[d] = nxt;
-            load(buf[d], nxt);
-        }
-        if (done) break;
+    while (cur.s < nsteps) {
+        int claimed = 0;
+        if (lane == 0) claimed = atomicAdd(&next_step, 1);
+        const Pos nxt = at(__builtin_amdgcn_readfirstlane(claimed));
+        Step<1> nb;
+        load(nb, nxt);
+        process(buf, cur);
+        buf = nb;
+        cur = nxt;
     }
 
     __syncthreads();
@@ -400,7 +378,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 template <bool SWIGLU, int XR>
 void launch_xr(const Plan &p, const MfmaArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((q4k_mfma_kernel<SWIGLU, XR, QLIN_MFMA_DEPTH>), dim3(p.grid), dim3(kThreads), p.lds, s, a);
+    hipLaunchKernelGGL((q4k_mfma_kernel<SWIGLU, XR>), dim3(p.grid), dim3(kThreads), p.lds, s, a);
 }
 
 template <bool SWIGLU>
