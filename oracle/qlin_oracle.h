@@ -19,6 +19,24 @@
  *   Q4_0           not implemented by the reference (trait only, GgufFile.cpp:40); restated from
  *                  the published ggml block_q4_0 format (d f16, 16 bytes of split-half nibbles,
  *                  w = d * (q - 8)).
+ *
+ * How each part is pinned (tests/test_oracle.py):
+ *   f16 <-> f32     exhaustive over all 65536 halves and RNE-encoded against numpy's float16.
+ *   Q4_K, Q6_K      the reference's own known-answer blocks (LaunchAddTest.cpp:711-756 -> 2212,
+ *                   758-803 -> 948) plus every scale/min field and bit position against an
+ *                   independent encoder (tests/qgen.py).
+ *   Q8_0            the reference's two-row closed form (LaunchAddTest.cpp:186-240).
+ *   Q8_1            the reference's sums (LaunchAddTest.cpp:679-709: 158/127 and raw 1.31) and
+ *                   the quantizer's invariants (|q| <= 127, RNE, d = amax/127).
+ *   GEMV / matmul   double-precision truth against closed forms, linearity, and f32 orders.
+ *   router, SwiGLU, brute force on tiny inputs, the tie (lowest index) and NaN rules, numpy.
+ *   down-accumulate
+ *   Q5_0            parity unpinned: the reference has the codec (kernel.cu:1159-1175) but no test;
+ *                   checked only against that formula as read and an independent encoder.
+ *   Q4_0            parity unpinned: the reference has no implementation; checked only against the
+ *                   ggml closed form and an independent encoder.
+ *   The last ulp of the reference's f32 summation order and of its expf/__expf cannot be pinned
+ *   without running its CUDA code; those are bounded by tolerance, not bits.
  */
 #ifndef QLIN_ORACLE_H
 #define QLIN_ORACLE_H
