@@ -244,7 +244,9 @@ def test_quantize_q8_1_bit_exact(raw):
 
 
 @pytest.mark.parametrize("qtype,out_dim,in_dim,m", [(Q4_K, 96, 1024, 7), (Q6_K, 40, 512, 3), (Q8_0, 50, 256, 4),
-                                                    (Q5_0, 33, 128, 2), (Q4_0, 17, 64, 3), (Q4_K, 512, 4096, 64)])
+                                                    (Q5_0, 33, 128, 2), (Q4_0, 17, 64, 3), (Q4_K, 512, 4096, 64),
+                                                    (Q4_K, 300, 768, 70), (Q4_K, 257, 256, 1),
+                                                    (Q4_K, 16, 512, 129)])
 def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
     w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=61 + out_dim)
     x = qgen.random_x(m, in_dim, seed=62)
@@ -254,6 +256,24 @@ def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
     qlin.quant_matmul_q8_1(qtype, dev(w), rb, dev(xq_h), yd, out_dim, in_dim, m)
     ref = orc.matmul_q8_1(qtype, w, rb, xq_h, out_dim, in_dim, m)
     assert normwise_rel_err(host(yd), ref) <= FP32
+
+
+def test_q4k_gemm_c4_shape_sampled():
+    """C4: Q4_K [14336, 4096] x Q8_1 activations [512, 4096] (f16 N(0,1) values) -> [512, 14336], checked
+    against the oracle on 72 weight rows (random ones plus both ends of the matrix)."""
+    N, K, M = 14336, 4096, 512
+    rng = np.random.default_rng(81)
+    rb = K // 256 * 144
+    w = rng.integers(0, 256, size=(N, K // 256, 144), dtype=np.uint8)
+    w[:, :, 0:4] = f16_bits(np.abs(rng.standard_normal((N, K // 256, 2))) * 0.01).view(np.uint8).reshape(N, K // 256, 4)
+    x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+    xq = orc.quantize_q8_1(x, K)
+    banner("q4k gemm C4 shape 512x4096x14336")
+    yd = empty_f32(M, N)
+    qlin.quant_matmul_q8_1(Q4_K, dev(w.reshape(-1)), rb, dev(xq), yd, N, K, M)
+    rows = np.unique(np.concatenate([rng.choice(N, 64, replace=False), [0, 1, 255, 256, N - 2, N - 1]]))
+    ref = orc.matmul_q8_1(Q4_K, np.ascontiguousarray(w[rows]).reshape(-1), rb, xq, len(rows), K, M)
+    assert normwise_rel_err(host(yd)[:, rows], ref) <= FP32
 
 
 # ---- MoE ----------------------------------------------------------------------------------------
