@@ -5,9 +5,10 @@
 // reference quant_matmul_q8_1_kernel for Q4_K, AI/codes/local-llm/src/backend/cuda/ops/kernel.cu:
 // 2305-2345), for m tokens of Q8_1 activations (d8 f16 | s8 f16 | int8 q[32] per 32 values).
 //
-// Every product is exact on v_mfma_f32_16x16x32_f16:
+// The products are exact on v_mfma_f32_16x16x32_f16 (up to the 2^-22 rounding of lo):
 //   A (activations): d8*qx needs at most 18 significant bits (11 of d8, 7 of q), so it is split
-//     exactly into two fp16 halves, hi = f16(d8*qx) and lo = d8*qx - hi, and both are multiplied.
+//     into two fp16 halves, hi (its top 11 bits) and lo (the rest, rounded to fp16: 2^-22 of the
+//     value), and both are multiplied.
 //   B (weights): sc_j*qw is an integer <= 63*15 = 945, exact in fp16.  A nibble becomes fp16 1024+q
 //     by one v_perm_b32 per two weights (bytes (q, 0x64)); one v_pk_fma_f16 per two weights then
 //     gives (1024+q)*sc - 1024*sc = q*sc, exact because the result is representable.
@@ -35,7 +36,9 @@ constexpr int kNT = 2;                    // 16-row weight tiles per wave
 constexpr int kBN = kWaves * kNT * 16;    // weight rows per workgroup (256)
 constexpr int kMT = 4;                    // 16-token tiles per workgroup
 constexpr int kBM = kMT * 16;             // tokens per workgroup (64)
-constexpr size_t kLds = (2 * kMT * 8 * 64 + kMT * 16) * sizeof(uint4);  // A planes + s8 operands
+constexpr int kPlane = 2 * kMT * 8 * 64;  // uint4s of one buffer's A planes (hi, lo): 64 KB
+constexpr int kBuf = kPlane + kMT * 16;   // plus the s8 operands
+constexpr size_t kLds = 2 * kBuf * sizeof(uint4);  // two buffers
 
 struct GemmArgs {
     const uint8_t *w;
@@ -89,8 +92,9 @@ __device__ __forceinline__ f16x2 splat(float v) {
 
 __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
     extern __shared__ uint4 lds[];
-    uint4 *aplane = lds;                          // [part][mt][j][lane]
-    uint4 *s8op = lds + 2 * kMT * 8 * 64;         // [mt][token]: s8 of sub-blocks 0..7
+    // two buffers, each: A planes [part][mt][j][lane] then s8 operands [mt][token]
+    auto plane = [&](int buf) { return lds + buf * kBuf; };
+    auto s8ops = [&](int buf) { return lds + buf * kBuf + kPlane; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -113,65 +117,78 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 #pragma unroll
         for (int t = 0; t < kNT; ++t) acc[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int sb = 0; sb < a.nsb; ++sb) {
-        // this wave's weights for the super-block (issued before the staging so they are in flight)
+    // Raw operands of a super-block: this wave's weight bytes and this thread's activation slots.
+    struct WRaw {
         uint4 hdr[kNT];
         uint2 qs[kNT][4];
+    };
+    struct XRaw {
+        uint32_t bh[4], q0[4], q1[4];
+    };
+    // past the end a fetch reloads the last super-block (valid addresses, never used)
+    auto fetch_w = [&](WRaw &w, int sb) {
+        sb = min(sb, a.nsb - 1);
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
             const uint8_t *p = wrow[t] + static_cast<size_t>(sb) * 144;
-            hdr[t] = *reinterpret_cast<const uint4 *>(p);
+            w.hdr[t] = *reinterpret_cast<const uint4 *>(p);
 #pragma unroll
-            for (int pr = 0; pr < 4; ++pr) qs[t][pr] = *reinterpret_cast<const uint2 *>(p + 16 + 32 * pr + 8 * g);
+            for (int pr = 0; pr < 4; ++pr) w.qs[t][pr] = *reinterpret_cast<const uint2 *>(p + 16 + 32 * pr + 8 * g);
         }
+    };
+    auto fetch_x = [&](XRaw &x, int sb) {
+        sb = min(sb, a.nsb - 1);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const uint8_t *blk = xrow + static_cast<size_t>(sb * 8 + 4 * sjh + jj) * 36;
+            x.bh[jj] = *reinterpret_cast<const uint32_t *>(blk);
+            x.q0[jj] = *reinterpret_cast<const uint32_t *>(blk + 4 + 8 * sg);
+            x.q1[jj] = *reinterpret_cast<const uint32_t *>(blk + 8 + 8 * sg);
+        }
+    };
 
-        // activations: Q8_1 blocks -> exact fp16 hi / lo A operands in LDS
-        __syncthreads();  // the previous super-block's operands are no longer read
+    // Activations of a super-block into buffer buf: q becomes fp16 exactly (bytes (q ^ 0x80, 0x64)
+    // = 1152 + q, minus 1152), hi = f16(d8*q) and lo = fma(d8, q, -hi) = the exact residual of hi
+    // (d8*q has at most 18 significant bits, hi keeps 11, so the residual fits an fp16).
+    auto stage = [&](const XRaw &x, int buf) {
+        uint4 *pl = plane(buf);
+        const f16x2 off = splat(-1152.0f);
         uint32_t s8h[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int j = 4 * sjh + jj;
-            const uint8_t *blk = xrow + static_cast<size_t>(sb * 8 + j) * 36;
-            const uint32_t bh = *reinterpret_cast<const uint32_t *>(blk);
-            const uint32_t q0 = *reinterpret_cast<const uint32_t *>(blk + 4 + 8 * sg);
-            const uint32_t q1 = *reinterpret_cast<const uint32_t *>(blk + 8 + 8 * sg);
-            const float d8 = f16_bits_to_f32(bh & 0xffffu);
+            const f16x2 d2 = u2h((x.bh[jj] & 0xffffu) * 0x10001u);
+            const uint32_t u[2] = {x.q0[jj] ^ 0x80808080u, x.q1[jj] ^ 0x80808080u};
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t w = e < 2 ? q0 : q1;
-                const int sh = 16 * (e & 1);
-                const float v0 = d8 * static_cast<float>(static_cast<int8_t>((w >> sh) & 0xffu));
-                const float v1 = d8 * static_cast<float>(static_cast<int8_t>((w >> (sh + 8)) & 0xffu));
-                const _Float16 h0 = static_cast<_Float16>(v0), h1 = static_cast<_Float16>(v1);
-                const _Float16 l0 = static_cast<_Float16>(v0 - static_cast<float>(h0));
-                const _Float16 l1 = static_cast<_Float16>(v1 - static_cast<float>(h1));
-                hi[e] = h2u(f16x2{h0, h1});
-                lo[e] = h2u(f16x2{l0, l1});
+                const uint32_t sel = (e & 1) ? 0x04030402u : 0x04010400u;
+                const f16x2 q2 = u2h(__builtin_amdgcn_perm(0x64646464u, u[e >> 1], sel)) + off;
+                const f16x2 h2 = d2 * q2;
+                hi[e] = h2u(h2);
+                lo[e] = h2u(__builtin_elementwise_fma(d2, q2, -h2));
             }
             uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]), L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
             if (!tok_ok) H = L = make_uint4(0u, 0u, 0u, 0u);
-            aplane[((0 * kMT + smt) * 8 + j) * 64 + sl] = H;
-            aplane[((1 * kMT + smt) * 8 + j) * 64 + sl] = L;
-            s8h[jj] = tok_ok ? bh >> 16 : 0u;
+            pl[((0 * kMT + smt) * 8 + j) * 64 + sl] = H;
+            pl[((1 * kMT + smt) * 8 + j) * 64 + sl] = L;
+            s8h[jj] = tok_ok ? x.bh[jj] >> 16 : 0u;
         }
         // the s8 operand row of token si: halves s8_0 .. s8_7 (written by the two threads of sg == 0)
         if (sg == 0) {
-            uint2 *dst = reinterpret_cast<uint2 *>(&s8op[smt * 16 + si]) + sjh;
+            uint2 *dst = reinterpret_cast<uint2 *>(&s8ops(buf)[smt * 16 + si]) + sjh;
             *dst = make_uint2(s8h[0] | (s8h[1] << 16), s8h[2] | (s8h[3] << 16));
         }
-        __syncthreads();
+    };
 
-        // weights: per tile the super-block scales, then the 8 sub-blocks' MFMAs
+    // One super-block: per 16-row tile the scales, then the 8 sub-blocks' MFMAs, then the min term.
+    auto compute = [&](const WRaw &w, int buf) {
+        const uint4 *pl = plane(buf);
         float dd[kNT], dmin[kNT];
-        uint32_t s0[kNT], s1[kNT], s2[kNT];
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
-            dd[t] = f16_bits_to_f32(hdr[t].x & 0xffffu);
-            dmin[t] = f16_bits_to_f32(hdr[t].x >> 16);
-            s0[t] = hdr[t].y;
-            s1[t] = hdr[t].z;
-            s2[t] = hdr[t].w;
+            dd[t] = f16_bits_to_f32(w.hdr[t].x & 0xffffu);
+            dmin[t] = f16_bits_to_f32(w.hdr[t].x >> 16);
         }
         f32x4 D[kMT][kNT];
 #pragma unroll
@@ -185,21 +202,20 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 #pragma unroll
             for (int t = 0; t < kNT; ++t) {
                 uint32_t sc, mn;
-                scale_min<J>(s0[t], s1[t], s2[t], sc, mn);
+                scale_min<J>(w.hdr[t].y, w.hdr[t].z, w.hdr[t].w, sc, mn);
                 mins[t][J] = mn;
-                const float scf = static_cast<float>(sc);
-                B[t] = weights_b<J>(qs[t][J >> 1], splat(scf), splat(-1024.0f * scf));
+                const f16x2 sc2 = splat(static_cast<float>(sc));
+                B[t] = weights_b<J>(w.qs[t][J >> 1], sc2, sc2 * splat(-1024.0f));
             }
+            // hi for every (token tile, row tile), then lo: consecutive MFMAs never feed each other
 #pragma unroll
-            for (int i = 0; i < kMT; ++i) {
-                const uint4 ah = aplane[((0 * kMT + i) * 8 + J) * 64 + lane];
-                const uint4 al = aplane[((1 * kMT + i) * 8 + J) * 64 + lane];
+            for (int part = 0; part < 2; ++part)
 #pragma unroll
-                for (int t = 0; t < kNT; ++t) {
-                    D[i][t] = mfma(ah, B[t], D[i][t]);
-                    D[i][t] = mfma(al, B[t], D[i][t]);
+                for (int i = 0; i < kMT; ++i) {
+                    const uint4 av = pl[((part * kMT + i) * 8 + J) * 64 + lane];
+#pragma unroll
+                    for (int t = 0; t < kNT; ++t) D[i][t] = mfma(av, B[t], D[i][t]);
                 }
-            }
         };
         sub_block(std::integral_constant<int, 0>{});
         sub_block(std::integral_constant<int, 1>{});
@@ -211,6 +227,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
         sub_block(std::integral_constant<int, 7>{});
 
         // min term: sum_j s8_j * m_j on one more MFMA (k-slots 0..7 carried by lane-group 0)
+        const uint4 *s8 = s8ops(buf);
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
             uint4 b2 = make_uint4(0u, 0u, 0u, 0u);
@@ -221,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < kMT; ++i) {
-                const uint4 a2 = g == 0 ? s8op[i * 16 + n] : make_uint4(0u, 0u, 0u, 0u);
+                const uint4 a2 = g == 0 ? s8[i * 16 + n] : make_uint4(0u, 0u, 0u, 0u);
                 const f32x4 d2 = mfma(a2, b2, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -230,7 +247,36 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
                 }
             }
         }
+    };
+
+    // Pipeline: the operands of super-block sb + 2 are requested while sb is computed and sb + 1 is
+    // staged into the other LDS buffer; one barrier per super-block.  Two register sets in turn (a
+    // single set copied forward would make the copy wait for the loads just issued).
+    WRaw w0, w1;
+    XRaw x0, x1;
+    fetch_w(w0, 0);
+    fetch_x(x0, 0);
+    fetch_w(w1, 1);
+    fetch_x(x1, 1);
+    stage(x0, 0);
+    __syncthreads();
+    // At the top of an iteration: buffer 0 holds sb's activations, w0 = sb's weights, w1 / x1 =
+    // sb + 1's raw operands (buffer 1 was last read before the previous barrier).
+    const int pairs = a.nsb >> 1;  // branch-free body, so the compiler waits for exactly what is used
+    for (int pi = 0; pi < pairs; ++pi) {
+        const int sb = 2 * pi;
+        fetch_x(x0, sb + 2);
+        compute(w0, 0);
+        stage(x1, 1);
+        fetch_w(w0, sb + 2);
+        __syncthreads();
+        fetch_x(x1, sb + 3);
+        compute(w1, 1);
+        stage(x0, 0);
+        fetch_w(w1, sb + 3);
+        __syncthreads();
     }
+    if (a.nsb & 1) compute(w0, 0);  // odd count: the last super-block is staged in buffer 0
 
     // lane (g, n) holds tokens 4g .. 4g+3 of each 16-token tile, weight row n of each 16-row tile
 #pragma unroll
