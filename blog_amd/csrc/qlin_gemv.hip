@@ -81,10 +81,8 @@ hipError_t gemv_generic(int type, const uint8_t *w, size_t rb, const float *x, f
 hipError_t gemv(int type, const uint8_t *w, size_t rb, const float *x, float *y, int n, int k, int m,
                 bool add, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
-#if QLIN_Q4K_MFMA
-    if (type == T_Q4_K && m == 1 && q4k_mfma_ok(&w, 1, rb, x, n, k, false))
-        return q4k_mfma_gemv(&w, &y, &n, 1, rb, x, k, add, s);
-#endif
+    if (m == 1 && (QLIN_Q4K_MFMA || type != T_Q4_K) && mfma_ok(type, &w, 1, rb, x, n, k, false))
+        return mfma_gemv(type, &w, &y, &n, 1, rb, x, k, add, s);
     if (type == T_Q4_K && m == 1 && q4k_stream_ok(&w, 1, rb, x, n, k, false))
         return q4k_stream_gemv(&w, &y, &n, 1, rb, x, k, add, s);
     return gemv_generic(type, w, rb, x, y, n, k, m, add, s);
@@ -95,10 +93,8 @@ hipError_t gemv_multi(int type, const uint8_t *const *w, float *const *y, const 
     int total = 0;
     for (int i = 0; i < nmat; ++i) total += rows[i];
     if (total == 0) return hipSuccess;
-#if QLIN_Q4K_MFMA
-    if (type == T_Q4_K && q4k_mfma_ok(w, nmat, rb, x, total, k, false))
-        return q4k_mfma_gemv(w, y, rows, nmat, rb, x, k, false, s);
-#endif
+    if ((QLIN_Q4K_MFMA || type != T_Q4_K) && mfma_ok(type, w, nmat, rb, x, total, k, false))
+        return mfma_gemv(type, w, y, rows, nmat, rb, x, k, false, s);
     if (type == T_Q4_K && q4k_stream_ok(w, nmat, rb, x, total, k, false))
         return q4k_stream_gemv(w, y, rows, nmat, rb, x, k, false, s);
     for (int i = 0; i < nmat; ++i) {

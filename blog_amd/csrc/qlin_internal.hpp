@@ -31,13 +31,13 @@ hipError_t q4k_stream_gemv(const uint8_t *const *w, float *const *y, const int *
 hipError_t q4k_stream_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
                              int ffn_dim, int in_dim, hipStream_t s);
 
-// Matrix-core Q4_K kernels (m == 1), same contracts as the streaming ones.
-bool q4k_mfma_ok(const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
-                 bool swiglu);
-hipError_t q4k_mfma_gemv(const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t row_bytes,
-                         const float *x, int in_dim, bool add, hipStream_t s);
-hipError_t q4k_mfma_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
-                           int ffn_dim, int in_dim, hipStream_t s);
+// Matrix-core decode kernels (m == 1) for Q4_K, Q4_0 and Q8_0, same contracts as the streaming ones.
+bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
+             bool swiglu);
+hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat,
+                     size_t row_bytes, const float *x, int in_dim, bool add, hipStream_t s);
+hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
+                       int ffn_dim, int in_dim, hipStream_t s);
 
 // The per-element fallback used for any type / alignment (exposed for tests of the fast paths).
 hipError_t gemv_generic(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,

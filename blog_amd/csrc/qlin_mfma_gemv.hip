@@ -1,4 +1,4 @@
-// qlin_q4k_mfma.hip -- Q4_K decode GEMV (m == 1) on the matrix cores, gfx950.
+// qlin_mfma_gemv.hip -- decode GEMV (m == 1) of Q4_K, Q4_0 and Q8_0 weights on the matrix cores, gfx950.
 //
 // Computes y[o] = sum_k w(o, k) x[k] (reference quant_gemv_kernel / quant_gemv_add_kernel,
 // AI/codes/local-llm/src/backend/cuda/ops/kernel.cu:1192-1244) for up to four matrices sharing x
@@ -27,6 +27,18 @@
 //     exactly the pair whose 6-bit scale and min the lane decodes for the epilogue
 //       acc += d*sc*(D_j - 128 X_j) - dmin*m*X_j.
 //
+// Other formats on the same machinery (a step covers 16 rows x one chunk; "sub-block" j below is
+// the D-row pair of 32 weights that share one x slice and one scale):
+//   Q4_0 (chunk = 8 blocks of 18 B, kernel.cu-free ggml layout): lane group g holds blocks 2g and
+//     2g+1; MFMA t carries bytes 4(t%4).. of block 2g + t/4, whose low nibbles are elements 4(t%4)+e
+//     and high nibbles elements 16+4(t%4)+e, so the x operand of a block fills both halves of its
+//     4 MFMAs.  y += d (D - 136 X)  (q - 8, and the 128 offset).
+//   Q8_0 (chunk = 4 blocks of 34 B, kernel.cu:1178-1185): q + 128 = 16 h + l splits each int8
+//     weight into two nibbles, so block g becomes the nibble pair of a Q4_K sub-block pair with the
+//     same x slice in both; y += d (D_l + 16 D_h - 2304 X).
+//   Their blocks are only 2-byte aligned, so each lane loads 9 aligned dwords and realigns them
+//     with v_alignbyte_b32.
+//
 // Work decomposition.  One workgroup per CU owns a contiguous slice of the rows.  Its work is the
 // flat sequence of steps (16-row tile, matrix, super-block), in memory order; the waves claim the
 // steps one at a time from an LDS counter, so the workgroup reads one compact window that slides
@@ -52,6 +64,12 @@ constexpr int kThreads = kWaves * 64;
 constexpr size_t kMaxLds = 160 * 1024;
 constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * kThreads
 
+// Weights per step chunk of one row, and its bytes.
+template <int FMT> struct Chunk;
+template <> struct Chunk<T_Q4_K> { static constexpr int elems = 256, bytes = 144; };
+template <> struct Chunk<T_Q4_0> { static constexpr int elems = 256, bytes = 144; };
+template <> struct Chunk<T_Q8_0> { static constexpr int elems = 128, bytes = 136; };
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -62,7 +80,7 @@ struct MfmaArgs {
     int nmat;
     size_t row_bytes;
     const float *x;
-    int nsb;      // super-blocks per row
+    int nsb;      // chunks per row
     int total;    // concatenated rows (SwiGLU: rows of each of gate and up)
     int add;
 };
@@ -125,10 +143,12 @@ struct ScaleDecoder {
 
 __device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
-template <int T>
-struct Step {
-    u32x4 hdr[T], qa[T], qb[T];
+// A lane's raw bytes of one step: Q4_K the 16-byte header and 32 bytes of nibbles; the 32-weight
+// formats 9 aligned dwords covering the lane's blocks.
+struct Raw {
+    uint32_t w[12];
 };
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
 // B operand of MFMA t from qs dword v: bf16(128 + q) for the 4 low nibbles, then the 4 high ones.
 // bf16 128 + q has bytes (q, 0x43); v_perm_b32 interleaves the nibble bytes with 0x43 bytes taken
@@ -151,11 +171,12 @@ __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x
 }
 
 // XR: float4 loads of x per thread (K/4 <= XR * kThreads).
-template <bool SWIGLU, int XR>
-__global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
+template <int FMT, bool SWIGLU, int XR>
+__global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
     constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
+    constexpr int CE = Chunk<FMT>::elems, CB = Chunk<FMT>::bytes;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nsb = a.nsb, K = nsb * 256;
+    const int nsb = a.nsb, K = nsb * CE;
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
     float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/32] sum(hi + lo) per sub-block
     float *partial = xsum + K / 32;                                // [rows][NW][nsb]
@@ -218,11 +239,20 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
         }
         return p;
     };
-    auto load = [&](Step<1> &st, const Pos &p) {
-        const uint8_t *q = p.rp + static_cast<size_t>(p.sb) * 144;
-        st.hdr[0] = ld16(q);
-        st.qa[0] = ld16(q + 16 + 32 * g);
-        st.qb[0] = ld16(q + 32 + 32 * g);
+    auto load = [&](Raw &st, const Pos &p) {
+        const uint8_t *q = p.rp + static_cast<size_t>(p.sb) * CB;
+        if constexpr (FMT == T_Q4_K) {
+            const u32x4 h = ld16(q), qa = ld16(q + 16 + 32 * g), qb = ld16(q + 32 + 32 * g);
+            st.w[0] = h.x; st.w[1] = h.y; st.w[2] = h.z; st.w[3] = h.w;
+            st.w[4] = qa.x; st.w[5] = qa.y; st.w[6] = qa.z; st.w[7] = qa.w;
+            st.w[8] = qb.x; st.w[9] = qb.y; st.w[10] = qb.z; st.w[11] = qb.w;
+        } else {
+            // Q4_0: blocks 2g, 2g+1 = bytes [36g, 36g+36).  Q8_0: block g = bytes [34g, 34g+34), read
+            // from the dword at or 2 bytes before it.
+            const uint8_t *b = FMT == T_Q4_0 ? q + 36 * g : q + 34 * g - 2 * (g & 1);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) st.w[k] = ld4(b + 4 * k);
+        }
     };
 
     if (nsteps == 0) return;  // uniform per workgroup
@@ -269,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
     __shared__ int next_step;
     if (tid == 0) next_step = kWaves;
     Pos cur = at(wave);
-    Step<1> buf;
+    Raw buf;
     load(buf, cur);
     stage_x();
     __syncthreads();
@@ -278,12 +308,14 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
 
     // One step: the 16 rows' dots with super-block sb, parked in LDS (each (row, matrix, sb) slot is
     // written by exactly one step; a global store here would share vmcnt with the weight stream).
-    auto process = [&](const Step<1> &cur, const Pos &p) {
-        // A operands of this super-block (x only): the lane's 32 values of its part/sub-block.
+    auto process = [&](const Raw &cur, const Pos &p) {
+        // A operands of this chunk (x only): the lane's 32 values of its part / sub-block (Q8_0: the
+        // block both nibble sub-blocks of the pair come from).
         {
             uint32_t dw[16];
             if (a_active) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * K + p.sb * 256 + (n >> 1) * 32);
+                const int xo = FMT == T_Q8_0 ? p.sb * CE + (n >> 2) * 32 : p.sb * CE + (n >> 1) * 32;
+                const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * K + xo);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const uint4 v = src[q];
@@ -293,32 +325,71 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) dw[q] = 0u;
             }
+            if constexpr (FMT == T_Q4_0) {
+                // a block's x fills both halves of the 4 MFMAs that carry it
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                aop[t].x = a_high ? 0u : dw[2 * t];
-                aop[t].y = a_high ? 0u : dw[2 * t + 1];
-                aop[t].z = a_high ? dw[2 * t] : 0u;
-                aop[t].w = a_high ? dw[2 * t + 1] : 0u;
+                for (int t = 0; t < 8; ++t) {
+                    const int tt = t & 3;
+                    const bool on = (t >> 2) == static_cast<int>(a_high);
+                    aop[t].x = on ? dw[2 * tt] : 0u;
+                    aop[t].y = on ? dw[2 * tt + 1] : 0u;
+                    aop[t].z = on ? dw[8 + 2 * tt] : 0u;
+                    aop[t].w = on ? dw[8 + 2 * tt + 1] : 0u;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    aop[t].x = a_high ? 0u : dw[2 * t];
+                    aop[t].y = a_high ? 0u : dw[2 * t + 1];
+                    aop[t].z = a_high ? dw[2 * t] : 0u;
+                    aop[t].w = a_high ? dw[2 * t + 1] : 0u;
+                }
             }
         }
-        const float2 xs = *reinterpret_cast<const float2 *>(xsum + p.sb * 8 + 2 * g);
-        const uint32_t qv[8] = {cur.qa[0].x, cur.qa[0].y, cur.qa[0].z, cur.qa[0].w,
-                                cur.qb[0].x, cur.qb[0].y, cur.qb[0].z, cur.qb[0].w};
+        // the 8 dwords of nibbles this lane feeds to the MFMAs
+        uint32_t qv[8];
+        if constexpr (FMT == T_Q4_K) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) qv[k] = cur.w[4 + k];
+        } else if constexpr (FMT == T_Q4_0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qv[k] = __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qv[4 + k] = cur.w[5 + k];
+        } else {
+            const bool odd = g & 1;  // odd blocks start 2 bytes into the first dword
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                qv[k] = (odd ? cur.w[k + 1] : __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2)) ^ 0x80808080u;
+        }
         f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 8; ++t) d = mfma(aop[t], weights_operand(qv[t]), d);
-        uint32_t scp, mp;
-        dec(cur.hdr[0].y, cur.hdr[0].z, cur.hdr[0].w, scp, mp);
-        const float dd = f16_bits_to_f32(cur.hdr[0].x & 0xffffu);
-        const float dmin = f16_bits_to_f32(cur.hdr[0].x >> 16);
-        const float dsc0 = dd * static_cast<float>(scp & 0xffu);
-        const float dsc1 = dd * static_cast<float>((scp >> 8) & 0xffu);
-        const float dm0 = dmin * static_cast<float>(mp & 0xffu);
-        const float dm1 = dmin * static_cast<float>((mp >> 8) & 0xffu);
-        float r = dsc0 * ((d[0] + d[1]) - 128.0f * xs.x);
-        r = fmaf(dsc1, (d[2] + d[3]) - 128.0f * xs.y, r);
-        r = fmaf(-dm0, xs.x, r);
-        r = fmaf(-dm1, xs.y, r);
+        float r;
+        if constexpr (FMT == T_Q4_K) {
+            const float2 xs = *reinterpret_cast<const float2 *>(xsum + p.sb * 8 + 2 * g);
+            uint32_t scp, mp;
+            dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
+            const float dd = f16_bits_to_f32(cur.w[0] & 0xffffu);
+            const float dmin = f16_bits_to_f32(cur.w[0] >> 16);
+            const float dsc0 = dd * static_cast<float>(scp & 0xffu);
+            const float dsc1 = dd * static_cast<float>((scp >> 8) & 0xffu);
+            const float dm0 = dmin * static_cast<float>(mp & 0xffu);
+            const float dm1 = dmin * static_cast<float>((mp >> 8) & 0xffu);
+            r = dsc0 * ((d[0] + d[1]) - 128.0f * xs.x);
+            r = fmaf(dsc1, (d[2] + d[3]) - 128.0f * xs.y, r);
+            r = fmaf(-dm0, xs.x, r);
+            r = fmaf(-dm1, xs.y, r);
+        } else if constexpr (FMT == T_Q4_0) {
+            const float2 xs = *reinterpret_cast<const float2 *>(xsum + p.sb * 8 + 2 * g);
+            const float d0 = f16_bits_to_f32(cur.w[0] & 0xffffu), d1 = f16_bits_to_f32(cur.w[4] >> 16);
+            r = d0 * ((d[0] + d[1]) - 136.0f * xs.x);
+            r = fmaf(d1, (d[2] + d[3]) - 136.0f * xs.y, r);
+        } else {
+            const float xs = xsum[p.sb * 4 + g];
+            const float dq = f16_bits_to_f32((cur.w[0] >> (16 * (g & 1))) & 0xffffu);
+            r = dq * (((d[0] + d[1]) + 16.0f * (d[2] + d[3])) - 2304.0f * xs);
+        }
         // add the four lane-groups (sub-block pairs)
         r += __shfl_xor(r, 16, 64);
         r += __shfl_xor(r, 32, 64);
@@ -332,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const MfmaArgs a) {
         int claimed = 0;
         if (lane == 0) claimed = atomicAdd(&next_step, 1);
         const Pos nxt = at(__builtin_amdgcn_readfirstlane(claimed));
-        Step<1> nb;
+        Raw nb;
         load(nb, nxt);
         process(buf, cur);
         buf = nb;
@@ -365,51 +436,66 @@ struct Plan {
     size_t lds;
 };
 
-Plan plan(int total, int nsb, bool swiglu) {
+Plan plan(int total, int k, int nsb, bool swiglu) {
     Plan p;
     p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
     const int rows = (total + p.grid - 1) / p.grid;
-    const size_t K = static_cast<size_t>(nsb) * 256;
+    const size_t K = static_cast<size_t>(k);
     p.lds = 4 * K + (K / 32) * sizeof(float) + static_cast<size_t>(rows) * (swiglu ? 2 : 1) * nsb * sizeof(float);
     return p;
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <bool SWIGLU, int XR>
+template <int FMT, bool SWIGLU, int XR>
 void launch_xr(const Plan &p, const MfmaArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((q4k_mfma_kernel<SWIGLU, XR>), dim3(p.grid), dim3(kThreads), p.lds, s, a);
+    hipLaunchKernelGGL((mfma_gemv_kernel<FMT, SWIGLU, XR>), dim3(p.grid), dim3(kThreads), p.lds, s, a);
 }
 
-template <bool SWIGLU>
-void launch_sw(const Plan &p, const MfmaArgs &a, hipStream_t s) {
-    const int need = (a.nsb * 64 + kThreads - 1) / kThreads;  // float4 loads of x per thread
-    if (need <= 1) launch_xr<SWIGLU, 1>(p, a, s);
-    else if (need <= 2) launch_xr<SWIGLU, 2>(p, a, s);
-    else if (need <= 4) launch_xr<SWIGLU, 4>(p, a, s);
-    else if (need <= 6) launch_xr<SWIGLU, 6>(p, a, s);
-    else launch_xr<SWIGLU, kMaxXr>(p, a, s);
+template <int FMT, bool SWIGLU>
+void launch_sw(const Plan &p, const MfmaArgs &a, int k, hipStream_t s) {
+    const int need = (k / 4 + kThreads - 1) / kThreads;  // float4 loads of x per thread
+    if (need <= 1) launch_xr<FMT, SWIGLU, 1>(p, a, s);
+    else if (need <= 2) launch_xr<FMT, SWIGLU, 2>(p, a, s);
+    else if (need <= 4) launch_xr<FMT, SWIGLU, 4>(p, a, s);
+    else if (need <= 6) launch_xr<FMT, SWIGLU, 6>(p, a, s);
+    else launch_xr<FMT, SWIGLU, kMaxXr>(p, a, s);
 }
 
-hipError_t launch(MfmaArgs &a, bool swiglu, hipStream_t s) {
-    const Plan p = plan(a.total, a.nsb, swiglu);
-    if (swiglu) launch_sw<true>(p, a, s);
-    else launch_sw<false>(p, a, s);
+template <int FMT>
+void launch_fmt(const Plan &p, const MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
+    if (swiglu) launch_sw<FMT, true>(p, a, k, s);
+    else launch_sw<FMT, false>(p, a, k, s);
+}
+
+int chunk_elems(int type) { return type == T_Q8_0 ? Chunk<T_Q8_0>::elems : Chunk<T_Q4_K>::elems; }
+
+hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
+    const Plan p = plan(a.total, k, a.nsb, swiglu);
+    switch (type) {
+        case T_Q4_K: launch_fmt<T_Q4_K>(p, a, k, swiglu, s); break;
+        case T_Q4_0: launch_fmt<T_Q4_0>(p, a, k, swiglu, s); break;
+        case T_Q8_0: launch_fmt<T_Q8_0>(p, a, k, swiglu, s); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
-bool q4k_mfma_ok(const uint8_t *const *w, int nmat, size_t rb, const float *x, int total, int k, bool swiglu) {
-    if (nmat < 1 || nmat > kMaxStreamMats || k % 256 || rb % 16 || !aligned16(x) || total <= 0) return false;
+bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float *x, int total, int k, bool swiglu) {
+    if (type != T_Q4_K && type != T_Q4_0 && type != T_Q8_0) return false;
+    // Q4_K loads 16-byte pieces; the 32-weight formats aligned dwords
+    const size_t wal = type == T_Q4_K ? 16 : 4;
+    if (nmat < 1 || nmat > kMaxStreamMats || k % 256 || rb % wal || !aligned16(x) || total <= 0) return false;
     if (k / 4 > kMaxXr * kThreads) return false;
     for (int i = 0; i < nmat; ++i)
-        if (!aligned16(w[i])) return false;
-    return plan(total, k / 256, swiglu).lds <= kMaxLds;
+        if (reinterpret_cast<uintptr_t>(w[i]) % wal) return false;
+    return plan(total, k, k / chunk_elems(type), swiglu).lds <= kMaxLds;
 }
 
-hipError_t q4k_mfma_gemv(const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,
-                         const float *x, int k, bool add, hipStream_t s) {
+hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,
+                     const float *x, int k, bool add, hipStream_t s) {
     MfmaArgs a{};
     int total = 0;
     for (int i = 0; i < nmat; ++i) {
@@ -422,14 +508,14 @@ hipError_t q4k_mfma_gemv(const uint8_t *const *w, float *const *y, const int *ro
     a.nmat = nmat;
     a.row_bytes = rb;
     a.x = x;
-    a.nsb = k / 256;
+    a.nsb = k / chunk_elems(type);
     a.total = total;
     a.add = add ? 1 : 0;
-    return launch(a, false, s);
+    return launch(type, a, k, false, s);
 }
 
-hipError_t q4k_mfma_swiglu(const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x, float *act, int ffn,
-                           int k, hipStream_t s) {
+hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x, float *act, int ffn,
+                       int k, hipStream_t s) {
     if (ffn == 0) return hipSuccess;
     MfmaArgs a{};
     a.w[0] = wg;
@@ -439,9 +525,9 @@ hipError_t q4k_mfma_swiglu(const uint8_t *wg, const uint8_t *wu, size_t rb, cons
     a.nmat = 1;
     a.row_bytes = rb;
     a.x = x;
-    a.nsb = k / 256;
+    a.nsb = k / chunk_elems(type);
     a.total = ffn;
-    return launch(a, true, s);
+    return launch(type, a, k, true, s);
 }
 
 }  // namespace qlin

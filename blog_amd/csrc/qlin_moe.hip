@@ -136,10 +136,8 @@ hipError_t swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t
 hipError_t swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_rb, size_t u_rb, const float *x,
                   float *act, int ffn, int in_dim, hipStream_t s) {
     const uint8_t *gu[2] = {wg, wu};
-#if QLIN_Q4K_MFMA
-    if (type == T_Q4_K && g_rb == u_rb && q4k_mfma_ok(gu, 2, g_rb, x, ffn, in_dim, true))
-        return q4k_mfma_swiglu(wg, wu, g_rb, x, act, ffn, in_dim, s);
-#endif
+    if ((QLIN_Q4K_MFMA || type != T_Q4_K) && g_rb == u_rb && mfma_ok(type, gu, 2, g_rb, x, ffn, in_dim, true))
+        return mfma_swiglu(type, wg, wu, g_rb, x, act, ffn, in_dim, s);
     if (type == T_Q4_K && g_rb == u_rb && q4k_stream_ok(gu, 2, g_rb, x, ffn, in_dim, true))
         return q4k_stream_swiglu(wg, wu, g_rb, x, act, ffn, in_dim, s);
     return swiglu_indexed(type, wg, wu, 0, 0, g_rb, u_rb, x, nullptr, act, 1, ffn, in_dim, s);

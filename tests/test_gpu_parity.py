@@ -101,8 +101,8 @@ def test_dequant_reference_names():
 GEMV_CASES = [
     (Q4_K, 1, 256), (Q4_K, 3, 512), (Q4_K, 17, 3584), (Q4_K, 4097, 8448),
     (Q4_K, 512, 3584), (Q4_K, 3584, 3584), (Q4_K, 18944, 3584), (Q4_K, 3584, 18944),
-    (Q8_0, 4096, 4096), (Q8_0, 7, 96), (Q8_0, 4864, 896),
-    (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64),
+    (Q8_0, 4096, 4096), (Q8_0, 7, 96), (Q8_0, 4864, 896), (Q8_0, 33, 256), (Q8_0, 1000, 8448),
+    (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64), (Q4_0, 17, 256), (Q4_0, 300, 4608),
     (Q5_0, 2048, 1408), (Q5_0, 5, 64),
     (Q6_K, 64, 512), (Q6_K, 257, 2048),
 ]
@@ -120,15 +120,17 @@ def test_gemv_parity(qtype, out_dim, in_dim):
     assert cond_err(y, ref, vals, x) <= COND
 
 
-@pytest.mark.parametrize("out_dim,in_dim", [(300, 3584), (1000, 8448)])
-def test_gemv_q4k_generic_path_agrees(out_dim, in_dim):
-    """A weight pointer that is not 16-byte aligned takes the generic kernel: same results."""
-    w, rb, _ = qgen.random_matrix(Q4_K, out_dim, in_dim, seed=11)
+@pytest.mark.parametrize("qtype,out_dim,in_dim", [(Q4_K, 300, 3584), (Q4_K, 1000, 8448), (Q8_0, 300, 4096),
+                                                  (Q4_0, 1000, 3584)])
+def test_gemv_generic_path_agrees(qtype, out_dim, in_dim):
+    """A weight pointer 2 bytes off the alignment the matrix-core kernel needs takes the generic
+    kernel: both agree with the oracle."""
+    w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=11)
     x = qgen.random_x(1, in_dim, seed=12)
-    banner(f"gemv generic Q4_K N={out_dim} K={in_dim}")
-    y_fast = gpu_gemv(Q4_K, w, rb, x, out_dim, in_dim)
-    y_gen = gpu_gemv(Q4_K, w, rb, x, out_dim, in_dim, w_offset=2)
-    ref = orc.matmul_f64(Q4_K, w, rb, x, out_dim, in_dim)
+    banner(f"gemv generic type={qtype} N={out_dim} K={in_dim}")
+    y_fast = gpu_gemv(qtype, w, rb, x, out_dim, in_dim)
+    y_gen = gpu_gemv(qtype, w, rb, x, out_dim, in_dim, w_offset=2)
+    ref = orc.matmul_f64(qtype, w, rb, x, out_dim, in_dim)
     assert normwise_rel_err(y_fast, ref) <= FP32
     assert normwise_rel_err(y_gen, ref) <= FP32
 
@@ -375,6 +377,19 @@ def test_swiglu_stream(ffn, hid):
     banner(f"swiglu stream ffn={ffn} hid={hid}")
     qlin.quant_swiglu(Q4_K, dev(wg), dev(wu), rb, rb, dev(x), act_d, ffn, hid)
     ref = orc.swiglu(Q4_K, wg, wu, rb, rb, x, ffn, hid)
+    assert normwise_rel_err(host(act_d), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("qtype,ffn,hid", [(Q4_0, 18944, 3584), (Q8_0, 4864, 896 + 128), (Q4_0, 9, 256)])
+def test_swiglu_matrix_core_formats(qtype, ffn, hid):
+    """Fused gate/up SiLU on the 32-weight formats (C2's gate/up pair in one launch)."""
+    wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=410 + hid)
+    wu, _, _ = qgen.random_matrix(qtype, ffn, hid, seed=411 + hid)
+    x = qgen.random_x(1, hid, seed=412)[0]
+    act_d = empty_f32(ffn)
+    banner(f"swiglu type={qtype} ffn={ffn} hid={hid}")
+    qlin.quant_swiglu(qtype, dev(wg), dev(wu), rb, rb, dev(x), act_d, ffn, hid)
+    ref = orc.swiglu(qtype, wg, wu, rb, rb, x, ffn, hid)
     assert normwise_rel_err(host(act_d), ref) <= 1e-4
 
 
