@@ -36,7 +36,12 @@
 //   Q8_0 (chunk = 4 blocks of 34 B, kernel.cu:1178-1185): q + 128 = 16 h + l splits each int8
 //     weight into two nibbles, so block g becomes the nibble pair of a Q4_K sub-block pair with the
 //     same x slice in both; y += d (D_l + 16 D_h - 2304 X).
-//   Their blocks are only 2-byte aligned, so each lane loads 9 aligned dwords and realigns them
+//   Q6_K (chunk = one 210 B super-block, kernel.cu:1122-1156): the 32 ql bytes of lane group g
+//     hold the low nibbles of 32-element group (g/2, g%2) and the high nibbles of group
+//     (g/2, g%2+2), whose top 2 bits come from the matching qh bytes; u = 6-bit value is carried
+//     as bf16(128 + u).  Scales change every 16 elements, so MFMAs 0-3 and 4-7 accumulate
+//     separately and the x sums are kept per 16; y += d sum sc (D - 160 X16).
+//   Their blocks are only 2-byte aligned, so each lane loads aligned dwords and realigns them
 //     with v_alignbyte_b32.
 //
 // Work decomposition.  One workgroup per CU owns a contiguous slice of the rows.  Its work is the
@@ -69,6 +74,9 @@ template <int FMT> struct Chunk;
 template <> struct Chunk<T_Q4_K> { static constexpr int elems = 256, bytes = 144; };
 template <> struct Chunk<T_Q4_0> { static constexpr int elems = 256, bytes = 144; };
 template <> struct Chunk<T_Q8_0> { static constexpr int elems = 128, bytes = 136; };
+template <> struct Chunk<T_Q6_K> { static constexpr int elems = 256, bytes = 210; };
+// Elements per x sum kept in LDS.
+template <int FMT> constexpr int kSumElems = FMT == T_Q6_K ? 16 : 32;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -146,7 +154,7 @@ __device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *reinterpret_ca
 // A lane's raw bytes of one step: Q4_K the 16-byte header and 32 bytes of nibbles; the 32-weight
 // formats 9 aligned dwords covering the lane's blocks.
 struct Raw {
-    uint32_t w[12];
+    uint32_t w[21];
 };
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
@@ -156,6 +164,16 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_
 __device__ __forceinline__ u32x4 weights_operand(uint32_t v) {
     const uint32_t lo = v & 0x0f0f0f0fu;
     const uint32_t hi = (v >> 4) & 0x0f0f0f0fu;
+    const uint32_t k43 = 0x43434343u;
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(k43, lo, 0x04010400u);  // (q0, 43, q1, 43)
+    r.y = __builtin_amdgcn_perm(k43, lo, 0x04030402u);  // (q2, 43, q3, 43)
+    r.z = __builtin_amdgcn_perm(k43, hi, 0x04010400u);
+    r.w = __builtin_amdgcn_perm(k43, hi, 0x04030402u);
+    return r;
+}
+// The same from ready 7-bit values: 4 bytes for slots 0..3 and 4 for slots 4..7.
+__device__ __forceinline__ u32x4 weights_operand2(uint32_t lo, uint32_t hi) {
     const uint32_t k43 = 0x43434343u;
     u32x4 r;
     r.x = __builtin_amdgcn_perm(k43, lo, 0x04010400u);  // (q0, 43, q1, 43)
@@ -176,10 +194,11 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
     constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
     constexpr int CE = Chunk<FMT>::elems, CB = Chunk<FMT>::bytes;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int XS = kSumElems<FMT>;
     const int nsb = a.nsb, K = nsb * CE;
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
-    float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/32] sum(hi + lo) per sub-block
-    float *partial = xsum + K / 32;                                // [rows][NW][nsb]
+    float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/XS] sum(hi + lo) per XS elements
+    float *partial = xsum + K / XS;                                // [rows][NW][nsb]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rb = static_cast<int>(static_cast<int64_t>(a.total) * blockIdx.x / gridDim.x);
@@ -246,6 +265,18 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
             st.w[0] = h.x; st.w[1] = h.y; st.w[2] = h.z; st.w[3] = h.w;
             st.w[4] = qa.x; st.w[5] = qa.y; st.w[6] = qa.z; st.w[7] = qa.w;
             st.w[8] = qb.x; st.w[9] = qb.y; st.w[10] = qb.z; st.w[11] = qb.w;
+        } else if constexpr (FMT == T_Q6_K) {
+            // ql bytes [32g, 32g+32) and qh bytes [128+32h, +32) from the dwords at or 2 bytes before
+            // them (rows are a multiple of 4 bytes, so odd super-blocks start 2 bytes in), then the
+            // lane's 4 scales and d as 16-bit loads
+            const int h = g >> 1, sh = static_cast<int>(reinterpret_cast<uintptr_t>(q) & 3u);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) st.w[k] = ld4(q - sh + 32 * g + 4 * k);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) st.w[9 + k] = ld4(q - sh + 128 + 32 * h + 4 * k);
+            st.w[18] = *reinterpret_cast<const uint16_t *>(q + 192 + 8 * h + 2 * (g & 1));
+            st.w[19] = *reinterpret_cast<const uint16_t *>(q + 196 + 8 * h + 2 * (g & 1));
+            st.w[20] = *reinterpret_cast<const uint16_t *>(q + 208) | (static_cast<uint32_t>(sh) << 16);
         } else {
             // Q4_0: blocks 2g, 2g+1 = bytes [36g, 36g+36).  Q8_0: block g = bytes [34g, 34g+34), read
             // from the dword at or 2 bytes before it.
@@ -278,15 +309,15 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
                 lb[e] = bf16_rne(xe[e] - bf16_val(hb[e]));
                 sm += bf16_val(hb[e]) + bf16_val(lb[e]);
             }
-            // the 8 threads of a 32-element sub-block are 8 consecutive lanes (K/4 is a multiple of
-            // 64, so every wave is entirely below K/4 or entirely above it)
+            // the threads of a 16- or 32-element group are consecutive lanes, and K is a multiple of
+            // 256, so a group is entirely below K/4 or entirely above it
             sm += __shfl_xor(sm, 1, 64);
             sm += __shfl_xor(sm, 2, 64);
-            sm += __shfl_xor(sm, 4, 64);
+            if constexpr (XS == 32) sm += __shfl_xor(sm, 4, 64);
             if (i < K / 4) {
                 reinterpret_cast<uint2 *>(xpart)[i] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
                 reinterpret_cast<uint2 *>(xpart + K)[i] = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
-                if ((i & 7) == 0) xsum[i >> 3] = sm;
+                if ((i & (XS / 4 - 1)) == 0) xsum[i / (XS / 4)] = sm;
             }
         }
     };
@@ -314,7 +345,11 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
         {
             uint32_t dw[16];
             if (a_active) {
-                const int xo = FMT == T_Q8_0 ? p.sb * CE + (n >> 2) * 32 : p.sb * CE + (n >> 1) * 32;
+                // sub-block j = n >> 1; Q6_K: j is (half j/4, group (j/2)%2 + 2 (j%2)) of 32 elements
+                const int j = n >> 1;
+                const int xo = FMT == T_Q8_0   ? p.sb * CE + (n >> 2) * 32
+                               : FMT == T_Q6_K ? p.sb * CE + (j >> 2) * 128 + (((j >> 1) & 1) + 2 * (j & 1)) * 32
+                                               : p.sb * CE + j * 32;
                 const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * K + xo);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -347,7 +382,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
             }
         }
         // the 8 dwords of nibbles this lane feeds to the MFMAs
-        uint32_t qv[8];
+        uint32_t qv[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
         if constexpr (FMT == T_Q4_K) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) qv[k] = cur.w[4 + k];
@@ -356,17 +391,46 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
             for (int k = 0; k < 4; ++k) qv[k] = __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2);
 #pragma unroll
             for (int k = 0; k < 4; ++k) qv[4 + k] = cur.w[5 + k];
-        } else {
+        } else if constexpr (FMT == T_Q8_0) {
             const bool odd = g & 1;  // odd blocks start 2 bytes into the first dword
 #pragma unroll
             for (int k = 0; k < 8; ++k)
                 qv[k] = (odd ? cur.w[k + 1] : __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2)) ^ 0x80808080u;
         }
         f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 d2 = {0.0f, 0.0f, 0.0f, 0.0f};  // Q6_K: elements 16..31 of each group
+        if constexpr (FMT == T_Q6_K) {
+            const uint32_t sh = 8 * (cur.w[20] >> 16);
+            const int hs = 2 * (g & 1);  // qh bit pair of the low-nibble group; +4 for the high one
 #pragma unroll
-        for (int t = 0; t < 8; ++t) d = mfma(aop[t], weights_operand(qv[t]), d);
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t ql = __builtin_amdgcn_alignbyte(cur.w[t + 1], cur.w[t], sh >> 3);
+                const uint32_t qh = __builtin_amdgcn_alignbyte(cur.w[10 + t], cur.w[9 + t], sh >> 3);
+                const uint32_t lo = (ql & 0x0f0f0f0fu) | (((qh >> hs) & 0x03030303u) << 4);
+                const uint32_t hi = ((ql >> 4) & 0x0f0f0f0fu) | (((qh >> (hs + 4)) & 0x03030303u) << 4);
+                if (t < 4) d = mfma(aop[t], weights_operand2(lo, hi), d);
+                else d2 = mfma(aop[t], weights_operand2(lo, hi), d2);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) d = mfma(aop[t], weights_operand(qv[t]), d);
+        }
         float r;
-        if constexpr (FMT == T_Q4_K) {
+        if constexpr (FMT == T_Q6_K) {
+            // groups of this lane: low nibbles (half h, group p), high nibbles (h, p + 2); x sums per 16
+            const int gl = 8 * (g >> 1) + 2 * (g & 1), gh = gl + 4;  // 16-element unit index in the chunk
+            const float *xs = xsum + p.sb * 16;
+            const float dd = f16_bits_to_f32(cur.w[20] & 0xffffu);
+            const float s0 = static_cast<float>(static_cast<int8_t>(cur.w[18] & 0xffu));
+            const float s1 = static_cast<float>(static_cast<int8_t>((cur.w[18] >> 8) & 0xffu));
+            const float s2 = static_cast<float>(static_cast<int8_t>(cur.w[19] & 0xffu));
+            const float s3 = static_cast<float>(static_cast<int8_t>((cur.w[19] >> 8) & 0xffu));
+            r = s0 * ((d[0] + d[1]) - 160.0f * xs[gl]);
+            r = fmaf(s1, (d2[0] + d2[1]) - 160.0f * xs[gl + 1], r);
+            r = fmaf(s2, (d[2] + d[3]) - 160.0f * xs[gh], r);
+            r = fmaf(s3, (d2[2] + d2[3]) - 160.0f * xs[gh + 1], r);
+            r *= dd;
+        } else if constexpr (FMT == T_Q4_K) {
             const float2 xs = *reinterpret_cast<const float2 *>(xsum + p.sb * 8 + 2 * g);
             uint32_t scp, mp;
             dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
@@ -436,12 +500,13 @@ struct Plan {
     size_t lds;
 };
 
-Plan plan(int total, int k, int nsb, bool swiglu) {
+Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
     Plan p;
     p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
     const int rows = (total + p.grid - 1) / p.grid;
     const size_t K = static_cast<size_t>(k);
-    p.lds = 4 * K + (K / 32) * sizeof(float) + static_cast<size_t>(rows) * (swiglu ? 2 : 1) * nsb * sizeof(float);
+    p.lds = 4 * K + (K / sum_elems) * sizeof(float) +
+            static_cast<size_t>(rows) * (swiglu ? 2 : 1) * nsb * sizeof(float);
     return p;
 }
 
@@ -469,13 +534,15 @@ void launch_fmt(const Plan &p, const MfmaArgs &a, int k, bool swiglu, hipStream_
 }
 
 int chunk_elems(int type) { return type == T_Q8_0 ? Chunk<T_Q8_0>::elems : Chunk<T_Q4_K>::elems; }
+int sum_elems(int type) { return type == T_Q6_K ? kSumElems<T_Q6_K> : kSumElems<T_Q4_K>; }
 
 hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
-    const Plan p = plan(a.total, k, a.nsb, swiglu);
+    const Plan p = plan(a.total, k, a.nsb, swiglu, sum_elems(type));
     switch (type) {
         case T_Q4_K: launch_fmt<T_Q4_K>(p, a, k, swiglu, s); break;
         case T_Q4_0: launch_fmt<T_Q4_0>(p, a, k, swiglu, s); break;
         case T_Q8_0: launch_fmt<T_Q8_0>(p, a, k, swiglu, s); break;
+        case T_Q6_K: launch_fmt<T_Q6_K>(p, a, k, swiglu, s); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -484,14 +551,14 @@ hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
 }  // namespace
 
 bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float *x, int total, int k, bool swiglu) {
-    if (type != T_Q4_K && type != T_Q4_0 && type != T_Q8_0) return false;
+    if (type != T_Q4_K && type != T_Q4_0 && type != T_Q8_0 && type != T_Q6_K) return false;
     // Q4_K loads 16-byte pieces; the 32-weight formats aligned dwords
     const size_t wal = type == T_Q4_K ? 16 : 4;
     if (nmat < 1 || nmat > kMaxStreamMats || k % 256 || rb % wal || !aligned16(x) || total <= 0) return false;
     if (k / 4 > kMaxXr * kThreads) return false;
     for (int i = 0; i < nmat; ++i)
         if (reinterpret_cast<uintptr_t>(w[i]) % wal) return false;
-    return plan(total, k, k / chunk_elems(type), swiglu).lds <= kMaxLds;
+    return plan(total, k, k / chunk_elems(type), swiglu, sum_elems(type)).lds <= kMaxLds;
 }
 
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,

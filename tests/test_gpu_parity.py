@@ -104,7 +104,7 @@ GEMV_CASES = [
     (Q8_0, 4096, 4096), (Q8_0, 7, 96), (Q8_0, 4864, 896), (Q8_0, 33, 256), (Q8_0, 1000, 8448),
     (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64), (Q4_0, 17, 256), (Q4_0, 300, 4608),
     (Q5_0, 2048, 1408), (Q5_0, 5, 64),
-    (Q6_K, 64, 512), (Q6_K, 257, 2048),
+    (Q6_K, 64, 512), (Q6_K, 257, 2048), (Q6_K, 16384, 2048), (Q6_K, 33, 768), (Q6_K, 100, 7168),
 ]
 
 
@@ -207,6 +207,17 @@ def test_kats(which):
     yd = empty_f32(1, 1)
     qlin.quant_matmul_q8_1(qtype, dev(w), w.size, xq, yd, 1, 256, 1)
     assert abs(host(yd)[0, 0] - expected) <= 1e-3
+
+
+@pytest.mark.parametrize("which", ["q4k", "q6k"])
+def test_kats_matrix_core_path(which):
+    """The reference known answers through the matrix-core kernel: 16 rows of two KAT super-blocks
+    (K = 512, whose row sizes meet that kernel's alignment), x = the KAT vector twice."""
+    x, q4k, q6k = _kat_blocks()
+    qtype, blk, expected = (Q4_K, q4k, 2212.0) if which == "q4k" else (Q6_K, q6k, 948.0)
+    w = np.tile(blk, 2 * 16)
+    y = gpu_gemv(qtype, w, 2 * blk.size, np.concatenate([x, x]), 16, 512)
+    assert np.all(np.abs(y[0] - 2 * expected) <= 2e-3), y[0]
 
 
 def test_kat_q8_0_rows_and_q8_1_sums():
