@@ -54,6 +54,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--probe-only", action="store_true",
                     help="only the gate/up SwiGLU kernel, eagerly, plus a 1 GiB copy (for rocprofv3 --pmc passes)")
+    ap.add_argument("--workload", default="qwen2-7b-q4k-decode-token", choices=sorted(WORKLOADS),
+                    help="the headline decode token (default), or one of the other configurations")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -71,6 +73,10 @@ def main() -> int:
 
     if args.probe_only:
         return probe_only(torch, qlin, gen, rb_h)
+    if args.workload != "qwen2-7b-q4k-decode-token":
+        result = WORKLOADS[args.workload](args, torch, qlin, gen)
+        print(json.dumps(result), flush=True)
+        return 0
 
     log("generating synthetic Q4_K weights (28 layers + lm_head)")
     shapes = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
@@ -233,6 +239,186 @@ def read_traffic():
     except OSError:
         pass
     return None
+
+
+# ---- the other configurations (2 and 4, and DeepSeek's Q6_K lm_head) -----
+# Each is one JSON line like the headline one: a step is one pass of the configuration's launches
+# over synthetic inputs resident in HBM, timed as HIP-graph replays on the launch stream, with the
+# distinct weight copies rotated so that the 256 MB Infinity Cache cannot hold them.
+
+BLOCK = {2: (32, 18), 6: (32, 22), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+Q4_0, Q8_0, Q6_K = 2, 8, 14
+
+
+def synth_blocks(torch, qtype, rows, cols, gen, scale=0.01):
+    """Random blocks of any format: uniform bytes, with every f16 scale = f16(|N(0,1)| * scale)."""
+    be, bb = BLOCK[qtype]
+    nb = cols // be
+    w = torch.randint(0, 256, (rows, nb, bb), dtype=torch.uint8, device="cuda", generator=gen)
+    nsc = 2 if qtype == Q4_K else 1
+    dd = (torch.randn((rows, nb, nsc), device="cuda", generator=gen).abs() * scale).to(torch.float16)
+    off = 208 if qtype == Q6_K else 0
+    w[:, :, off:off + 2 * nsc] = dd.view(torch.uint8).view(rows, nb, 2 * nsc)
+    return w.view(-1)
+
+
+def graph_us(torch, qlin, fn, reps):
+    """Average microseconds of one call of fn, replayed `reps` times from a HIP graph."""
+    qlin.set_stream(torch.cuda.current_stream())
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        qlin.set_stream(torch.cuda.current_stream())
+        fn()
+    qlin.set_stream(torch.cuda.current_stream())
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def cpu_threads():
+    return min(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1), 16)
+
+
+def cpu_gemv_gbs(torch, qtype, w_dev, rb, n, k, seconds):
+    """The oracle's f32 GEMV (OpenMP over rows) on one weight copy, repeated for about `seconds`."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    threads = cpu_threads()
+    w = w_dev.cpu().numpy()
+    x = np.random.default_rng(5).standard_normal(k).astype(np.float32)
+    passes, t = 0, 0.0
+    while t < seconds:
+        t0 = time.perf_counter()
+        orc.matmul_f32(qtype, w, rb, x, n, k, threads)
+        t += time.perf_counter() - t0
+        passes += 1
+    nbytes = n * rb + 4 * (n + k)
+    return {"value": round(nbytes * passes / t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"[{n}, {k}] type {qtype} GEMV ({nbytes / 1e6:.1f} MB) x {passes} passes, {t:.1f} s; "
+                      f"oracle orc_matmul_f32 (OpenMP over rows)"}
+
+
+def gemv_config(args, torch, qlin, gen, workload, metric, qtype, shapes, copies):
+    """shapes: [(name, rows, cols)] launched in order per step; `copies` distinct sets rotate."""
+    sets = [[synth_blocks(torch, qtype, n, k, gen) for _, n, k in shapes] for _ in range(copies)]
+    xs = {k: torch.randn(k, device="cuda", generator=gen) for _, _, k in shapes}
+    ys = {n: torch.empty(n, device="cuda") for _, n, _ in shapes}
+    rbs = [qlin.row_bytes(qtype, k) for _, _, k in shapes]
+
+    def step_all():
+        for ws in sets:
+            for (name, n, k), w, rb in zip(shapes, ws, rbs):
+                qlin.quant_gemv(qtype, w, rb, xs[k], ys[n], n, k, 1)
+
+    reps = max(1, args.steps // copies)
+    us_step = graph_us(torch, qlin, step_all, reps) / copies
+    step_bytes = sum(n * rb + 4 * (n + k) for (_, n, k), rb in zip(shapes, rbs))
+    # the first matrix's kernel alone, as the roofline figure
+    _, n0, k0 = shapes[0]
+    us0 = graph_us(torch, qlin, lambda: [qlin.quant_gemv(qtype, ws[0], rbs[0], xs[k0], ys[n0], n0, k0, 1)
+                                         for ws in sets], reps) / copies
+    b0 = n0 * rbs[0] + 4 * (n0 + k0)
+    log(f"{workload}: {us_step:.2f} us/step, first matrix {us0:.2f} us")
+    result = {
+        "metric": metric, "value": round(step_bytes / us_step / 1e3, 1), "unit": "GB/s",
+        "pct_of_peak": round(100.0 * step_bytes / us_step / 1e3 / PEAK_HBM_GBS, 2),
+        "n_gpus": 1, "steps": reps * copies, "warmup": 3, "ms_per_step": round(us_step / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": f"synthetic (random type-{qtype} blocks, f32 N(0,1) activations), {copies} weight copies rotated",
+        "config": {"workload": workload, "weight_format": qtype, "matrices": [[nm, n, k] for nm, n, k in shapes],
+                   "batch": 1, "algorithmic_bytes_per_step": step_bytes, "execution": "hip graph replay"},
+        "roofline": {"bound": "hbm", "achieved": round(b0 / us0 / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(b0 / us0 / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": f"mfma_gemv_kernel<{qtype}, false, *> ({shapes[0][0]} [{n0}, {k0}])",
+                     "avg_launch_us": round(us0, 3), "algorithmic_bytes_per_launch": b0},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_gemv_gbs(torch, qtype, sets[0][0], rbs[0], n0, k0, args.cpu_seconds)
+    return result
+
+
+def wl_c1(args, torch, qlin, gen):
+    return gemv_config(args, torch, qlin, gen, "c1-q8_0-gemv-4096", "Q8_0 GEMV HBM GB/s (4096x4096, batch 1)",
+                       Q8_0, [("w", 4096, 4096)], 64)
+
+
+def wl_c2(args, torch, qlin, gen):
+    return gemv_config(args, torch, qlin, gen, "c2-q4_0-ffn-triple",
+                       "Q4_0 GEMV triple HBM GB/s (Qwen2-7B FFN gate, up, down; batch 1)", Q4_0,
+                       [("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)], 10)
+
+
+def wl_q6k(args, torch, qlin, gen):
+    return gemv_config(args, torch, qlin, gen, "deepseek-q6_k-lm-head", "Q6_K GEMV HBM GB/s ([102400, 2048], batch 1)",
+                       Q6_K, [("lm_head", 102400, 2048)], 6)
+
+
+def wl_c4(args, torch, qlin, gen):
+    """C4: Q4_K [14336, 4096] x activations [512, 4096] (f16 N(0,1) values) quantized to Q8_1 on the
+    fly, then the matrix-core GEMM; a step is both launches."""
+    M, K, N = 512, 4096, 14336
+    rb = qlin.row_bytes(Q4_K, K)
+    ws = [synth_blocks(torch, Q4_K, N, K, gen) for _ in range(2)]
+    x = torch.randn(M, K, device="cuda", generator=gen).half().float()
+    xq = torch.empty(M * qlin.lib().qlin_q8_1_row_bytes(K), dtype=torch.uint8, device="cuda")
+    y = torch.empty(M, N, device="cuda")
+
+    def step_all():
+        for w in ws:
+            qlin.quantize_q8_1(x, xq, K, M)
+            qlin.quant_matmul_q8_1(Q4_K, w, rb, xq, y, N, K, M)
+
+    reps = max(1, args.steps // 20)
+    us_step = graph_us(torch, qlin, step_all, reps) / len(ws)
+    us_gemm = graph_us(torch, qlin, lambda: [qlin.quant_matmul_q8_1(Q4_K, w, rb, xq, y, N, K, M) for w in ws],
+                       reps) / len(ws)
+    flops = 2.0 * M * N * K
+    log(f"c4: {us_step:.2f} us/step, GEMM {us_gemm:.2f} us")
+    result = {
+        "metric": "Q4_K x Q8_1 prefill GEMM TFLOP/s (M=512, K=4096, N=14336)",
+        "value": round(flops / us_step / 1e6, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps * len(ws),
+        "warmup": 3, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 (exact hi/lo split of Q8_1 values) x f16 (sc*q), f32 accumulate",
+        "data": "synthetic (random Q4_K blocks; activations f16-rounded N(0,1) quantized to Q8_1 in the step)",
+        "config": {"workload": "c4-q4k-prefill-gemm", "m": M, "k": K, "n": N, "weight_format": "Q4_K",
+                   "activation_format": "Q8_1", "algorithmic_flops_per_step": flops,
+                   "launches_per_step": ["quantize_q8_1", "quant_matmul_q8_1"], "execution": "hip graph replay"},
+        "roofline": {"bound": "mfma", "achieved": round(flops / us_gemm / 1e6, 1), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(flops / us_gemm / 1e6 / 2500.0, 4), "traffic": None,
+                     "kernel": "q4k_gemm_kernel (fp16 MFMA 16x16x32; peak = dense fp16)",
+                     "avg_launch_us": round(us_gemm, 3), "algorithmic_flops_per_launch": flops},
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        rows = 64
+        w = ws[0].view(N, -1)[:rows].contiguous().view(-1).cpu().numpy()
+        xh = x.cpu().numpy()
+        xqh = orc.quantize_q8_1(xh, K)
+        passes, t = 0, 0.0
+        while t < args.cpu_seconds:
+            t0 = time.perf_counter()
+            orc.matmul_q8_1(Q4_K, w, rb, xqh, rows, K, M)
+            t += time.perf_counter() - t0
+            passes += 1
+        result["cpu_baseline"] = {
+            "value": round(2.0 * M * rows * K * passes / t / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
+            "kind": "port", "sample": f"{rows} of the {N} weight rows x {M} tokens x {K}, {passes} passes, "
+                                      f"{t:.1f} s; oracle orc_matmul_q8_1 (reference block-dot order, f64)"}
+    return result
+
+
+WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
+             "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k}
 
 
 def cpu_baseline(torch, layer, shapes, xin, outs, seconds, bytes_per_step):
