@@ -308,4 +308,54 @@ int qlin_moe_routed_decode_indexed(int gu_type, const uint8_t *gate, const uint8
                                                             hidden, ffn_dim);
 }
 
+size_t qlin_moe_grouped_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size) {
+    if (tokens < 0 || k < 0 || n_experts <= 0 || ffn_dim <= 0 || hidden_size <= 0) return 0;
+    return qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden_size);
+}
+
+int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                   int down_type, const uint8_t *down, size_t down_bytes, int n_experts, int ffn_dim,
+                                   int in_dim, int hidden, const float *x, const int *ids, const float *rw,
+                                   void *workspace, size_t workspace_bytes, float *out, int tokens, int k) {
+    // the per-token facade's rules (TensorTool.cpp:277-305) plus the batch's own
+    if (down_type != QLIN_TYPE_Q4_K && down_type != QLIN_TYPE_Q6_K && down_type != QLIN_TYPE_Q5_0 &&
+        down_type != QLIN_TYPE_Q8_0)
+        return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (gu_type != QLIN_TYPE_Q4_K && gu_type != QLIN_TYPE_Q6_K) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (n_experts <= 0 || ffn_dim <= 0 || in_dim <= 0 || hidden <= 0 || k < 0 || tokens < 0) return QLIN_ERR_SHAPE;
+    if (!qlin::moe_grouped_shape_ok(n_experts)) return QLIN_ERR_LIMIT;
+    const bool work = tokens > 0 && k > 0;
+    if (work && (!ids || !rw || !x || !out || !workspace)) return QLIN_ERR_NULL;
+    if (work && workspace_bytes < qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden))
+        return QLIN_ERR_LIMIT;
+    if (work && (reinterpret_cast<uintptr_t>(workspace) & 255u)) return QLIN_ERR_ALIGN;
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const size_t d_rb = d_eb / static_cast<size_t>(hidden);
+    int rc = check_weight(down_type, down, d_rb, hidden, ffn_dim);
+    if (rc || (rc = check_weight(gu_type, gate, g_rb, ffn_dim, in_dim)) ||
+        (rc = check_weight(gu_type, up, g_rb, ffn_dim, in_dim)))
+        return rc;
+    if ((rc = check_f32(x, work)) || (rc = check_f32(out, work)) || (rc = check_f32(rw, work))) return rc;
+    if (!work) return QLIN_OK;
+    if (qlin::moe_grouped_up_ok(gu_type, gate, up, g_eb, g_rb, x, in_dim))
+        return launched(qlin::moe_grouped(gu_type, gate, up, g_eb, g_rb, down_type, down, d_eb, d_rb, n_experts,
+                                          ffn_dim, in_dim, hidden, x, ids, rw, workspace, out, tokens, k, stream()));
+    // other layouts: the per-token kernels, token by token, with act in the workspace
+    float *act = static_cast<float *>(workspace);
+    for (int t = 0; t < tokens; ++t) {
+        const float *xt = x + static_cast<size_t>(t) * in_dim;
+        const int *it = ids + static_cast<size_t>(t) * k;
+        const float *wt = rw + static_cast<size_t>(t) * k;
+        hipError_t e = qlin::swiglu_indexed(gu_type, gate, up, g_eb, g_eb, g_rb, g_rb, xt, it, act, k, ffn_dim,
+                                            in_dim, stream());
+        if (e == hipSuccess)
+            e = qlin::down_indexed_ordered(down_type, down, d_eb, d_rb, act, it, wt,
+                                           out + static_cast<size_t>(t) * hidden, k, hidden, ffn_dim, stream());
+        if (e != hipSuccess) return QLIN_ERR_LAUNCH;
+    }
+    return QLIN_OK;
+}
+
 }  // extern "C"

@@ -1,0 +1,73 @@
+// qlin_mfma.hpp -- operand builders shared by the matrix-core decode kernels (gfx950).
+//
+// A weight nibble q (or any 7-bit value) becomes the bf16 value 128 + q exactly: bytes (q, 0x43)
+// assembled by v_perm_b32.  Activations x are split as hi = bf16(x), lo = bf16(x - hi), so products
+// with weights are exact and hi + lo equals x to 2^-18 |x|; v_mfma_f32_16x16x32_bf16 accumulates in
+// f32.  Lane l of an MFMA supplies row / column l % 16 and k-slots 8*(l/16) .. 8*(l/16)+7.
+#pragma once
+
+#include "qlin_device.hpp"
+
+namespace qlin {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 bits of f (round to nearest even; finite inputs).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_val(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
+// Lane-constant (scale, min) decode of sub-blocks 2p and 2p+1 (kernel.cu:913-921), packed in bytes
+// 0 and 1 of the results.
+struct ScaleDecoder {
+    bool upper;
+    int sh, m_shift;
+    uint32_t lo_mask, hi_mask;
+    __device__ explicit ScaleDecoder(int p)
+        : upper(p >= 2), sh(p >= 2 ? 16 * (p - 2) : 16 * p), m_shift(p >= 2 ? 4 : 0),
+          lo_mask(p >= 2 ? 0x0f0fu : 0x3f3fu), hi_mask(p >= 2 ? 0x0303u : 0u) {}
+    __device__ __forceinline__ void operator()(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &scp,
+                                               uint32_t &mp) const {
+        const uint32_t a_sc = upper ? s2 : s0;
+        const uint32_t a_m = upper ? s2 : s1;
+        scp = ((a_sc >> sh) & lo_mask) | (((s0 >> (sh + 6)) & hi_mask) << 4);
+        mp = ((a_m >> (sh + m_shift)) & lo_mask) | (((s1 >> (sh + 6)) & hi_mask) << 4);
+    }
+};
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+// B operand of MFMA t from qs dword v: bf16(128 + q) for the 4 low nibbles, then the 4 high ones.
+// bf16 128 + q has bytes (q, 0x43); v_perm_b32 interleaves the nibble bytes with 0x43 bytes taken
+// from a constant register.
+__device__ __forceinline__ u32x4 weights_operand(uint32_t v) {
+    const uint32_t lo = v & 0x0f0f0f0fu;
+    const uint32_t hi = (v >> 4) & 0x0f0f0f0fu;
+    const uint32_t k43 = 0x43434343u;
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(k43, lo, 0x04010400u);  // (q0, 43, q1, 43)
+    r.y = __builtin_amdgcn_perm(k43, lo, 0x04030402u);  // (q2, 43, q3, 43)
+    r.z = __builtin_amdgcn_perm(k43, hi, 0x04010400u);
+    r.w = __builtin_amdgcn_perm(k43, hi, 0x04030402u);
+    return r;
+}
+// The same from ready 7-bit values: 4 bytes for slots 0..3 and 4 for slots 4..7.
+__device__ __forceinline__ u32x4 weights_operand2(uint32_t lo, uint32_t hi) {
+    const uint32_t k43 = 0x43434343u;
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(k43, lo, 0x04010400u);  // (q0, 43, q1, 43)
+    r.y = __builtin_amdgcn_perm(k43, lo, 0x04030402u);  // (q2, 43, q3, 43)
+    r.z = __builtin_amdgcn_perm(k43, hi, 0x04010400u);
+    r.w = __builtin_amdgcn_perm(k43, hi, 0x04030402u);
+    return r;
+}
+
+__device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+}  // namespace qlin

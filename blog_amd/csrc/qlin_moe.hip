@@ -29,37 +29,68 @@ __device__ __forceinline__ float row_dot(const uint8_t *row, const float *x, int
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// One wave per token: lanes hold the logits of experts lane, lane + 64, ...  The maximum is
+// order-free; the softmax denominator is summed by lane 0 in expert order, as the reference does;
+// each of the k picks is a wave argmax that prefers the lower index on equal values, which is the
+// first maximum of the reference's strict '>' scan.
 __global__ __launch_bounds__(64) void router_kernel(const float *__restrict__ logits, int *__restrict__ idx,
                                                     float *__restrict__ wout, int tokens, int ne, int k,
                                                     float scaling) {
-    const int t = blockIdx.x * 64 + threadIdx.x;
-    if (t >= tokens) return;
+    const int t = blockIdx.x, lane = threadIdx.x;
     const float *lg = logits + static_cast<size_t>(t) * ne;
-    float maxv = -INFINITY;
-    for (int e = 0; e < ne; ++e) {
-        const float v = isfinite(lg[e]) ? lg[e] : -INFINITY;
-        maxv = fmaxf(maxv, v);
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        const float l = e < ne ? lg[e] : -INFINITY;
+        v[j] = isfinite(l) ? l : -INFINITY;
     }
-    float denom = 0.0f;
-    if (isfinite(maxv))
-        for (int e = 0; e < ne; ++e) {
-            const float v = isfinite(lg[e]) ? lg[e] : -INFINITY;
-            denom += expf(v - maxv);
-        }
-    uint64_t used[4] = {0, 0, 0, 0};  // n_experts <= 256, checked by the caller
+    float maxv = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    maxv = wave_max(maxv);
+    __shared__ float ex[256];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < ne) ex[lane + 64 * j] = isfinite(maxv) ? expf(v[j] - maxv) : 0.0f;
+    __syncthreads();
+    __shared__ float denom_s;
+    if (lane == 0) {
+        float denom = 0.0f;
+        if (isfinite(maxv))
+            for (int e = 0; e < ne; ++e) denom += ex[e];
+        denom_s = denom;
+    }
+    __syncthreads();
+    const float denom = denom_s;
+    bool used[4] = {false, false, false, false};
     for (int r = 0; r < k; ++r) {
-        float best = -INFINITY;
-        int best_e = -1;
-        for (int e = 0; e < ne; ++e) {
-            if ((used[e >> 6] >> (e & 63)) & 1u) continue;
-            const float v = isfinite(lg[e]) ? lg[e] : -INFINITY;
-            if (v > best) { best = v; best_e = e; }
+        float bv = -INFINITY;
+        int be = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            if (e < ne && !used[j] && (v[j] > bv || (v[j] == bv && e < be))) {
+                bv = v[j];
+                be = e;
+            }
         }
-        if (best_e < 0) best_e = r < ne ? r : 0;
-        used[best_e >> 6] |= 1ull << (best_e & 63);
-        const float prob = (denom > 0.0f && isfinite(best)) ? expf(best - maxv) / denom : 0.0f;
-        idx[static_cast<size_t>(t) * k + r] = best_e;
-        wout[static_cast<size_t>(t) * k + r] = prob * scaling;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const float ov = __shfl_xor(bv, m, 64);
+            const int oe = __shfl_xor(be, m, 64);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        // every remaining logit is -inf: the reference falls back to expert r (or 0)
+        const int best_e = bv == -INFINITY ? (r < ne ? r : 0) : be;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) used[j] = used[j] || (lane + 64 * j == best_e);
+        if (lane == 0) {
+            const float prob = (denom > 0.0f && isfinite(bv)) ? expf(bv - maxv) / denom : 0.0f;
+            idx[static_cast<size_t>(t) * k + r] = best_e;
+            wout[static_cast<size_t>(t) * k + r] = prob * scaling;
+        }
     }
 }
 
@@ -107,7 +138,7 @@ __global__ __launch_bounds__(kBlock) void down_kernel(const uint8_t *__restrict_
 hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts, int k,
                        float routed_scaling, hipStream_t s) {
     if (tokens == 0) return hipSuccess;
-    hipLaunchKernelGGL(router_kernel, dim3((tokens + 63) / 64), dim3(64), 0, s, logits, top_idx, top_w, tokens,
+    hipLaunchKernelGGL(router_kernel, dim3(tokens), dim3(64), 0, s, logits, top_idx, top_w, tokens,
                        n_experts, k, routed_scaling);
     return hipGetLastError();
 }

@@ -160,6 +160,19 @@ int qlin_moe_routed_decode_indexed(int gate_up_type, const uint8_t *gate_exps, c
                                    int hidden_size, const float *x, const int *expert_ids,
                                    const float *route_weights, float *act_scratch, float *out, int k);
 
+/* No reference counterpart (the reference decodes one token at a time): moe_routed_decode_indexed
+ * for a batch of tokens, each selected expert's weights read once for all the routes that chose it.
+ * x [tokens, in_dim], expert_ids / route_weights [tokens, k], out [tokens, hidden_size] (+=); per
+ * token the result is that of qlin_moe_routed_decode_indexed.  workspace: device memory of at least
+ * qlin_moe_grouped_workspace_bytes(...) bytes, 256-byte aligned, not used by anything else while the
+ * call runs; n_experts <= 1024. */
+size_t qlin_moe_grouped_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size);
+int qlin_moe_routed_decode_grouped(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                   size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                   size_t down_bytes, int n_experts, int ffn_dim, int in_dim, int hidden_size,
+                                   const float *x, const int *expert_ids, const float *route_weights,
+                                   void *workspace, size_t workspace_bytes, float *out, int tokens, int k);
+
 #ifdef __cplusplus
 }
 #endif

@@ -138,6 +138,36 @@ def test_moe_facade_rejections_follow_tensortool():
     assert run(ne=0) == SHAPE
 
 
+def test_moe_grouped_validation():
+    """The batched facade: the per-token rules, plus workspace size / alignment and the expert limit;
+    a batch without work returns before any launch."""
+    def al(v):
+        return (v + 255) // 256 * 256
+    need = qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 64, 1408, 2048)
+    assert need == al(65 * 4) + al(96 * 4) + al(96 * 1408 * 4) + al(96 * 2048 * 4)
+    assert qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 0, 1408, 2048) == 0
+    a = dict(gate=FAKE, up=FAKE, gub=64 * 1408 * 1152, down=FAKE, db=64 * 2048 * 968, ne=64, ffn=1408,
+             ind=2048, hid=2048, x=FAKE, ids=FAKE, rw=FAKE, ws=FAKE, wsb=need, out=FAKE, tokens=16, k=6)
+
+    def run(gu=12, dt=6, **kw):
+        v = {**a, **kw}
+        return qlin.status("qlin_moe_routed_decode_grouped", gu, v["gate"], v["up"], v["gub"], dt, v["down"],
+                           v["db"], v["ne"], v["ffn"], v["ind"], v["hid"], v["x"], v["ids"], v["rw"], v["ws"],
+                           v["wsb"], v["out"], v["tokens"], v["k"])
+    assert run(dt=2) == UNSUP
+    assert run(gu=8) == UNSUP
+    assert run(ne=0) == SHAPE
+    assert run(tokens=-1) == SHAPE
+    assert run(ne=1025, gub=1025 * 1408 * 1152, db=1025 * 2048 * 968) == LIMIT
+    assert run(ids=0) == NULL
+    assert run(ws=0) == NULL
+    assert run(wsb=need - 1) == LIMIT
+    assert run(ws=FAKE + 4) == ALIGN
+    assert run(dt=12) == SHAPE         # Q4_K down with ffn 1408: not a multiple of 256
+    assert run(gub=64 * 1408 * 1152 - 64) == ROWB
+    assert run(tokens=0, wsb=0) == OK  # nothing to do
+
+
 def test_swiglu_and_down_validation():
     assert qlin.status("qlin_launch_quant_swiglu_indexed", 12, FAKE, FAKE, 100, 100, 144, 144, FAKE, FAKE, FAKE,
                        2, 1, 256) == ROWB

@@ -291,16 +291,18 @@ def test_q4k_gemm_c4_shape_sampled():
 
 # ---- MoE ----------------------------------------------------------------------------------------
 
-def test_router_topk():
-    rng = np.random.default_rng(71)
-    logits = rng.standard_normal((16, 64)).astype(np.float32)
+@pytest.mark.parametrize("ne", [64, 100, 256])
+def test_router_topk(ne):
+    rng = np.random.default_rng(71 + ne)
+    logits = rng.standard_normal((16, ne)).astype(np.float32)
     logits[3, :] = 0.5                 # all tied: 0..5 in order
     logits[4, 7] = np.nan
     logits[5, :] = np.nan              # nothing finite
-    logits[6, [9, 4, 60]] = 9.0        # tie at the top
+    logits[6, [9, 4, ne - 4]] = 9.0    # tie at the top
+    logits[7, ne - 1] = np.inf         # non-finite -> -inf
     idx_d = torch.zeros((16, 6), dtype=torch.int32, device="cuda")
     w_d = empty_f32(16, 6)
-    qlin.call("qlin_launch_moe_router_topk", dev(logits), idx_d, w_d, 16, 64, 6, 1.0)
+    qlin.call("qlin_launch_moe_router_topk", dev(logits), idx_d, w_d, 16, ne, 6, 1.0)
     idx_r, w_r = orc.router_topk(logits, 6, 1.0)
     assert np.array_equal(host(idx_d), idx_r)
     assert np.allclose(host(w_d), w_r, rtol=1e-5, atol=1e-7)
@@ -363,6 +365,65 @@ def test_moe_facade_deepseek_shape():
     act_ref = orc.swiglu_indexed(Q4_K, wg, wu, geb, geb, grb, grb, x, ids, ffn, hid)
     ref = orc.down_indexed_ordered(Q5_0, wdn, deb, drb, act_ref, ids, rw, out0, hid, ffn)
     assert normwise_rel_err(host(out_d), ref) <= 1e-4
+
+
+def _moe_batch(gu_type, dn_type, E, ffn, hid, tokens, k, seed):
+    wg, grb, geb = _experts(gu_type, E, ffn, hid, seed)
+    wu, _, _ = _experts(gu_type, E, ffn, hid, seed + 1)
+    wdn, drb, deb = _experts(dn_type, E, hid, ffn, seed + 2)
+    rng = np.random.default_rng(seed + 3)
+    x = rng.standard_normal((tokens, hid)).astype(np.float32)
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    ids, rw = orc.router_topk(logits, k, 1.0)
+    return wg, wu, grb, geb, wdn, drb, deb, x, np.ascontiguousarray(ids), np.ascontiguousarray(rw)
+
+
+def _moe_batch_ref(gu_type, dn_type, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid):
+    ref = out0.copy()
+    for t in range(x.shape[0]):
+        act = orc.swiglu_indexed(gu_type, wg, wu, geb, geb, grb, grb, x[t], ids[t], ffn, hid)
+        ref[t] = orc.down_indexed_ordered(dn_type, wdn, deb, drb, act, ids[t], rw[t], ref[t], hid, ffn)
+    return ref
+
+
+def _run_grouped(gu_type, dn_type, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0):
+    tokens, k = ids.shape
+    nbytes = qlin.lib().qlin_moe_grouped_workspace_bytes(tokens, k, E, ffn, hid)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
+    wsp = (ws.data_ptr() + 255) // 256 * 256
+    out_d = dev(out0)
+    qlin.call("qlin_moe_routed_decode_grouped", gu_type, dev(wg), dev(wu), wg.size, dn_type, dev(wdn), wdn.size, E,
+              ffn, hid, hid, dev(x), dev(ids), dev(rw), wsp, nbytes, out_d, tokens, k)
+    return host(out_d)
+
+
+@pytest.mark.parametrize("dn_type", [Q5_0, Q8_0])
+def test_moe_grouped_c5(dn_type):
+    """C5: DeepSeek-V2-Lite routed experts for a batch of 16 tokens (64 x [1408, 2048] Q4_K gate/up,
+    [2048, 1408] down, top-6) -- equal to the per-token reference path on every token."""
+    E, ffn, hid, tokens, k = 64, 1408, 2048, 16, 6
+    wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(Q4_K, dn_type, E, ffn, hid, tokens, k, 201)
+    ids[3, 2] = -1                  # an empty route
+    ids[5, :] = ids[4, :]           # two tokens with the same experts
+    out0 = np.random.default_rng(7).standard_normal((tokens, hid)).astype(np.float32)
+    banner(f"moe grouped C5 down={dn_type}")
+    got = _run_grouped(Q4_K, dn_type, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+    ref = _moe_batch_ref(Q4_K, dn_type, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(got - out0, ref - out0) <= 1e-4
+    assert normwise_rel_err(got, ref) <= 1e-5
+
+
+def test_moe_grouped_many_routes_per_expert_and_fallback():
+    """Routes beyond one pass per expert (8 experts, 24 tokens x 4 routes), and Q6_K gate/up, which
+    takes the per-token kernels inside the same entry point."""
+    for gu_type, seed in ((Q4_K, 301), (Q6_K, 311)):
+        E, ffn, hid, tokens, k = 8, 128, 512, 24, 4
+        wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(gu_type, Q8_0, E, ffn, hid, tokens, k, seed)
+        out0 = np.zeros((tokens, hid), np.float32)
+        banner(f"moe grouped passes gu={gu_type}")
+        got = _run_grouped(gu_type, Q8_0, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+        ref = _moe_batch_ref(gu_type, Q8_0, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+        assert normwise_rel_err(got, ref) <= 1e-4
 
 
 # ---- batched and fused streaming launches ------------------------------------------------------
