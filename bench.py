@@ -470,7 +470,7 @@ def wl_c5(args, torch, qlin, gen):
                    "per_token_facade_us_per_step": round(us_tok, 2), "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(nbytes / us / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "whole step (group_kernel, up_kernel, down_kernel<Q5_0>, combine_kernel)",
+                     "kernel": "whole step (router_kernel, group_kernel, stream_kernel<Q4_K> gate/up, stream_kernel<Q5_0> down, combine_kernel)",
                      "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": nbytes},
     }
 

@@ -323,7 +323,7 @@ int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8
         return QLIN_ERR_UNSUPPORTED_TYPE;
     if (gu_type != QLIN_TYPE_Q4_K && gu_type != QLIN_TYPE_Q6_K) return QLIN_ERR_UNSUPPORTED_TYPE;
     if (n_experts <= 0 || ffn_dim <= 0 || in_dim <= 0 || hidden <= 0 || k < 0 || tokens < 0) return QLIN_ERR_SHAPE;
-    if (!qlin::moe_grouped_shape_ok(n_experts)) return QLIN_ERR_LIMIT;
+    if (!qlin::moe_grouped_shape_ok(n_experts, static_cast<int64_t>(tokens) * k)) return QLIN_ERR_LIMIT;
     const bool work = tokens > 0 && k > 0;
     if (work && (!ids || !rw || !x || !out || !workspace)) return QLIN_ERR_NULL;
     if (work && workspace_bytes < qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden))
@@ -339,7 +339,7 @@ int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8
         return rc;
     if ((rc = check_f32(x, work)) || (rc = check_f32(out, work)) || (rc = check_f32(rw, work))) return rc;
     if (!work) return QLIN_OK;
-    if (qlin::moe_grouped_up_ok(gu_type, gate, up, g_eb, g_rb, x, in_dim))
+    if (qlin::moe_grouped_up_ok(gu_type, gate, up, g_eb, g_rb, x, in_dim, ffn_dim, n_experts, tokens * k))
         return launched(qlin::moe_grouped(gu_type, gate, up, g_eb, g_rb, down_type, down, d_eb, d_rb, n_experts,
                                           ffn_dim, in_dim, hidden, x, ids, rw, workspace, out, tokens, k, stream()));
     // other layouts: the per-token kernels, token by token, with act in the workspace

@@ -72,9 +72,9 @@ hipError_t down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_byt
 
 // Batched routed decode, each selected expert read once per pass over its routes (qlin_moe_grouped.hip).
 size_t moe_grouped_workspace(int tokens, int k, int n_experts, int ffn_dim, int hidden);
-bool moe_grouped_shape_ok(int n_experts);
+bool moe_grouped_shape_ok(int n_experts, int64_t routes);
 bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
-                       const float *x, int in_dim);
+                       const float *x, int in_dim, int ffn_dim, int n_experts, int routes);
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int n_experts, int ffn_dim, int in_dim,
                        int hidden, const float *x, const int *ids, const float *rw, void *workspace, float *out,

@@ -65,6 +65,17 @@ __device__ __forceinline__ u32x4 weights_operand2(uint32_t lo, uint32_t hi) {
     return r;
 }
 
+// v summed over lanes n, n+16, n+32, n+48 (the four lane-groups of an MFMA), in lanes 0..15: the
+// gfx950 half-wave and row swaps, (v_n + v_n+32) + (v_n+16 + v_n+48).
+__device__ __forceinline__ float sum_lane_groups(float v) {
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);
+    const float a = v + __builtin_bit_cast(float, static_cast<uint32_t>(s32[1]));
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, a),
+                                                      false, false);
+    return a + __builtin_bit_cast(float, static_cast<uint32_t>(s16[1]));
+}
+
 __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);

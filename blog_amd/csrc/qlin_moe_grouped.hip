@@ -6,54 +6,496 @@
 //   act_r  = silu(Wg[e_r] x_t) * (Wu[e_r] x_t)               for routes r of t with 0 <= e_r < E
 //   out[t] += sum_r fmaf(Wd[e_r] act_r, w_r, .)  in route order r = 0 .. k-1
 // The reference decodes one token at a time, so an expert chosen by several tokens of a batch is
-// read once per token; here the routes are first grouped by expert (a stable counting sort on the
-// device), then
-//   gate/up: one workgroup per (expert, 64 rows) reads those rows of Wg and Wu once and applies
-//     them to up to kGroup routes' x vectors per pass (Q4_K on the matrix cores, the same operands
-//     as the decode GEMV);
-//   down: one wave per (expert, row) decodes the row once and dots it with up to kGroup
-//     activations per pass;
+// read once per token.  Here the routes are first grouped by expert (a stable counting sort on the
+// device, which also lists the selected experts), then two streaming launches read the selected
+// experts' rows once per pass of up to NQ routes:
+//   gate/up (Q4_K) and down (Q5_0, Q8_0), both on the bf16 matrix cores: one workgroup per
+//     CU takes a contiguous range of the selected experts' 16-row tiles, and its waves claim
+//     (tile, matrix, chunk) steps in memory order from an LDS counter, loading the next step while
+//     computing the current one, as the decode GEMV does;
 //   combine: per (token, hidden row), the route results in route order.
+// Shapes or layouts outside those kernels' preconditions take per-element kernels (up_kernel,
+// down_kernel) with the same results.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
 
+#include <algorithm>
+
 namespace qlin {
 namespace {
 
-constexpr int kGroup = 4;  // routes of one expert per pass
+constexpr int kGroup = 4;  // routes of one expert per pass of the per-element kernels
 constexpr int kMaxExperts = 1024;
+constexpr int kRouteBits = 21;  // routes per call < 2^21: the expert scan packs (count, selected)
+constexpr int kIdsChunk = 4096;
 
 struct Groups {
     int *offset;  // [E + 1] first position of expert e in list
     int *list;    // [R] route indices grouped by expert, increasing within an expert
+    int4 *seg;    // [E] the selected experts in increasing id order: (expert, first position, count, 0)
+    int *nsel;    // number of selected experts
 };
 
 // Stable counting sort of the R = tokens * k routes by expert id (invalid ids are left out).  One
-// workgroup: thread e counts and then lists expert e's routes, which keeps them in route order.
-__global__ __launch_bounds__(256) void group_kernel(const int *__restrict__ ids, int R, int E, Groups gr) {
-    __shared__ int cnt[kMaxExperts + 1];
-    for (int e = threadIdx.x; e < E; e += 256) {
+// workgroup: the ids are staged in LDS, thread e counts and then lists expert e's routes in route
+// order, and a scan over the experts gives the offsets and the compacted selected-expert records.
+__global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids, int R, int E, Groups gr) {
+    __shared__ int4 s_ids4[kIdsChunk / 4];
+    __shared__ int s_wave[16];
+    const int *s_ids = reinterpret_cast<const int *>(s_ids4);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // a chunk of ids into LDS, padded with -1 to a multiple of 16 (read 16 at a time below)
+    auto stage = [&](int base) {
+        const int n = min(kIdsChunk, R - base);
+        int *dst = reinterpret_cast<int *>(s_ids4);
+        for (int i = tid; i < ((n + 15) & ~15); i += 1024) dst[i] = i < n ? ids[base + i] : -1;
+        return n;
+    };
+    auto count16 = [&](int i, int e) {
         int c = 0;
-        for (int r = 0; r < R; ++r) c += ids[r] == e;
-        cnt[e] = c;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {  // exclusive prefix sum in place
-        int acc = 0;
-        for (int e = 0; e < E; ++e) {
-            const int c = cnt[e];
-            cnt[e] = acc;
-            acc += c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int4 v = s_ids4[i / 4 + j];
+            c += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
         }
-        cnt[E] = acc;
+        return c;
+    };
+    int c = 0;
+    for (int base = 0; base < R; base += kIdsChunk) {
+        if (base) __syncthreads();
+        const int n = stage(base);
+        __syncthreads();
+        if (tid < E)
+            for (int i = 0; i < n; i += 16) c += count16(i, tid);
     }
+    // exclusive scan over the experts of count | selected << kRouteBits
+    const int v = tid < E ? c | (static_cast<int>(c > 0) << kRouteBits) : 0;
+    int inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += t;
+    }
+    if (lane == 63) s_wave[wave] = inc;
     __syncthreads();
-    for (int e = threadIdx.x; e <= E; e += 256) gr.offset[e] = cnt[e];
-    for (int e = threadIdx.x; e < E; e += 256) {
-        int pos = cnt[e];
-        for (int r = 0; r < R; ++r)
-            if (ids[r] == e) gr.list[pos++] = r;
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += s_wave[w];
+    const int excl = before + inc - v;
+    constexpr int kMask = (1 << kRouteBits) - 1;
+    const int pos0 = excl & kMask;
+    if (tid < E) {
+        gr.offset[tid] = pos0;
+        if (c > 0) gr.seg[excl >> kRouteBits] = make_int4(tid, pos0, c, 0);
+    }
+    if (tid == 1023) {  // threads past E add nothing, so the last inclusive value is the total
+        gr.offset[E] = (before + inc) & kMask;
+        *gr.nsel = (before + inc) >> kRouteBits;
+    }
+    int pos = pos0;
+    for (int base = 0; base < R; base += kIdsChunk) {
+        int n = min(kIdsChunk, R - base);
+        if (R > kIdsChunk) {  // the count pass left only the last chunk in LDS
+            __syncthreads();
+            n = stage(base);
+            __syncthreads();
+        }
+        if (tid < E && c > 0)
+            for (int i = 0; i < n; i += 16) {
+                if (count16(i, tid) == 0) continue;
+                for (int j = i; j < i + 16; ++j)
+                    if (s_ids[j] == tid) gr.list[pos++] = base + j;
+            }
+    }
+}
+
+// ---- streaming grouped kernels (matrix cores) ---------------------------------------------------
+
+constexpr int kSWaves = 16;
+constexpr int kSThreads = kSWaves * 64;
+
+// One step = 16 rows x one chunk of a row.
+//   Q4_K (gate/up): a chunk is one super-block; the A operand is the decode GEMV's block-diagonal
+//     layout (rows = 8 sub-blocks x hi/lo of one route), 8 MFMAs per route.
+//   Q5_0 / Q8_0 (down): a chunk is 4 blocks, lane-group g decoding block g.  A rows are
+//     (block b, route r of a pair, hi/lo): row i = 4b + 2r + p, nonzero only in lane-group b's
+//     k-slots, so one set of tpb MFMAs serves two routes and D rows 4g .. 4g+3 of a lane hold its
+//     block's dots for both.  MFMA t takes qs dword t of the block: the 4 low nibbles (elements
+//     4t .. 4t+3) and the 4 high ones (elements 16+4t ..), or for Q8_0 the bytes q+128 = 16h + l
+//     split into nibbles, with A slots (x, 16x) so that one D sums both.
+//   Per block: sum x*w = d * (D - corr * X), X = sum of x (hi + lo) over the block, because the
+//   operand is bf16(128 + u) with u = q + 16 (Q5_0), or l / h (Q8_0: 128*17 + 128).
+template <int FMT> struct StepFmt;
+// w0, w1: relative cost of a 16-row tile per pass and per route (fitted to measured launch times
+// at 1 .. 4 routes per expert); the workgroups split the selected experts' tiles by this cost.
+template <> struct StepFmt<T_Q4_K> {
+    static constexpr int ce = 256, bb = 144, cb = 144, tpb = 0, w0 = 4, w1 = 1;
+};
+template <> struct StepFmt<T_Q5_0> {
+    static constexpr int ce = 128, bb = 22, cb = 88, nd = 5, tpb = 4, w0 = 8, w1 = 1;
+    static constexpr float corr = 144.0f;
+};
+template <> struct StepFmt<T_Q8_0> {
+    static constexpr int ce = 128, bb = 34, cb = 136, nd = 8, tpb = 8, w0 = 8, w1 = 1;
+    static constexpr float corr = 2304.0f;
+};
+
+struct StreamArgs {
+    const uint8_t *w0, *w1;  // gate/up: Wg, Wu; down: Wd (w1 = w0)
+    size_t eb, rb;           // expert and row bytes
+    const float *x;          // gate/up: x [tokens, K]; down: act [R, K]
+    int x_div;               // the x row of route r is r / x_div (k for gate/up, 1 for down)
+    const int *list;
+    const int4 *seg;
+    const int *nsel;
+    float *out;              // gate/up: act [R, rows]; down: per-route results [R, rows]
+    int rows, K, nchunk, tpe;  // rows per expert, inner dimension, chunks per row, 16-row tiles per expert
+    int piece;                 // tiles whose step partials fit in LDS at once
+};
+
+__device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// A value the whole wave holds alike, moved to scalar registers (LDS and vector loads give VGPRs).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni(int64_t v) {
+    const uint64_t u = static_cast<uint64_t>(v);
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(uni(static_cast<int>(u >> 32)))) << 32) |
+                                static_cast<uint32_t>(uni(static_cast<int>(u))));
+}
+
+// bits 0..3 of b to bit 0 of bytes 0..3 (the four shifted copies of b do not overlap)
+__device__ __forceinline__ uint32_t spread4(uint32_t b) { return __umul24(b & 0xfu, 0x204081u) & 0x01010101u; }
+
+// Cost of one 16-row tile of an expert with cnt routes: its passes and its routes.
+template <int FMT, int NQ>
+__device__ __forceinline__ int64_t tile_cost(int cnt) {
+    return static_cast<int64_t>((cnt + NQ - 1) / NQ) * StepFmt<FMT>::w0 + static_cast<int64_t>(cnt) * StepFmt<FMT>::w1;
+}
+
+template <int FMT, int NQ>
+__global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
+    using F = StepFmt<FMT>;
+    constexpr bool UP = FMT == T_Q4_K;
+    constexpr int NW = UP ? 2 : 1;  // matrices per output row (gate, up)
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int K = a.K, nblk = K / 32, nchunk = a.nchunk;
+    // staging of the pass's routes: Q4_K bf16 planes [NQ][2][K]; others slot vectors
+    // [NQ][2][nblk][tpb] (8 bf16 each); then the block sums X [NQ][nblk] and the step partials
+    // [NW][NQ][nchunk][rows of the piece]
+    const size_t stage_bytes = UP ? static_cast<size_t>(NQ) * 4 * K : static_cast<size_t>(NQ) * 2 * nblk * F::tpb * 16;
+    uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);
+    uint4 *slots = reinterpret_cast<uint4 *>(smem);
+    float *xsum = reinterpret_cast<float *>(smem + stage_bytes);
+    float *partial = xsum + NQ * nblk;
+    __shared__ int next_step;
+    __shared__ int64_t s_pref[kMaxExperts + 1];  // cost of the selected experts before s
+    __shared__ int64_t s_wave[kSWaves];
+    __shared__ uint4 s_zero[8];  // down: the A operand of lanes whose k-slots are empty
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int nsel = *a.nsel;
+    if (nsel == 0) return;  // uniform
+    if (tid < 8) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);  // before the barriers below
+
+    // Each workgroup takes an equal share of the total cost, in tiles: tile t of selected expert s
+    // starts at cost s_pref[s] + t * tile_cost and belongs to the workgroup whose range holds that.
+    {
+        const int64_t v = tid < nsel ? static_cast<int64_t>(a.tpe) * tile_cost<FMT, NQ>(a.seg[tid].z) : 0;
+        int64_t inc = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int64_t t = __shfl_up(inc, d, 64);
+            if (lane >= d) inc += t;
+        }
+        if (lane == 63) s_wave[wave] = inc;
+        __syncthreads();
+        int64_t before = 0;
+        for (int w = 0; w < wave; ++w) before += s_wave[w];
+        if (tid == 0) s_pref[0] = 0;
+        if (tid < nsel) s_pref[tid + 1] = before + inc;
+        __syncthreads();
+    }
+    const int64_t C = uni(s_pref[nsel]);
+    const int64_t c0 = C * blockIdx.x / gridDim.x, c1 = C * (blockIdx.x + 1) / gridDim.x;
+    if (c0 >= c1) return;  // uniform
+    int s_first = 0;
+    for (int hi = nsel - 1; s_first < hi;) {  // first expert whose range ends after c0
+        const int mid = (s_first + hi) >> 1;
+        if (s_pref[mid + 1] > c0) hi = mid;
+        else s_first = mid + 1;
+    }
+
+    // A-operand role of this lane (row n of A, k-slots of lane-group g)
+    const bool a_active = (n >> 2) == g;
+    const int a_part = n & 1;
+    const bool a_high = (n >> 1) & 1;       // Q4_K: sub-block 2g+1 uses slots 4..7
+    const int a_pair = (n >> 1) & 1;        // others: route of the pair
+    const ScaleDecoder dec(g);
+    // others: lane-group g's block starts bb*g bytes into the chunk; its payload (after d) is read
+    // from the dword at or 2 bytes before it
+    const int pl_dw = (F::bb * g + 2) >> 2, pl_sh = (F::bb * g + 2) & 3;
+
+    struct Raw {
+        uint32_t w[12];
+    };
+    struct Pos {
+        int s, which, tile, ch;
+        const uint8_t *rp;
+    };
+
+    for (int s = uni(s_first); s < nsel; ++s) {
+        const int64_t ps = uni(s_pref[s]);
+        if (ps >= c1) break;
+        const int4 sg = a.seg[s];
+        const int e = uni(sg.x), beg = uni(sg.y), cnt = uni(sg.z);
+        const int64_t ct = tile_cost<FMT, NQ>(cnt);
+        const int lt0 = static_cast<int>(max(ceil_div(c0 - ps, ct), int64_t{0}));
+        const int lt1 = static_cast<int>(min(ceil_div(c1 - ps, ct), static_cast<int64_t>(a.tpe)));
+        if (lt0 >= lt1) continue;  // uniform
+        const uint8_t *we0 = a.w0 + static_cast<size_t>(e) * a.eb;
+        const uint8_t *we1 = a.w1 + static_cast<size_t>(e) * a.eb;
+        // the tiles are taken in pieces of at most a.piece (the LDS partials' capacity)
+        int r0, r1, ntile, nrows, pstride, nsteps;
+        auto set_piece = [&](int pt0) {
+            const int pt1 = min(pt0 + a.piece, lt1);
+            r0 = pt0 * 16;
+            r1 = min(pt1 * 16, a.rows);
+            ntile = pt1 - pt0;
+            nrows = r1 - r0;
+            pstride = ntile * 16;
+            nsteps = ntile * NW * nchunk;
+        };
+
+        // step s in memory order: matrix, then tile, then chunk (past the end: the last step)
+        auto at = [&](int st) {
+            Pos p;
+            p.s = st;
+            const int c = min(st, nsteps - 1);
+            const int tw = c / nchunk;
+            p.ch = c - tw * nchunk;
+            p.which = NW == 2 && tw >= ntile;
+            p.tile = tw - p.which * ntile;
+            const int row = min(r0 + p.tile * 16 + n, r1 - 1);
+            p.rp = (p.which ? we1 : we0) + static_cast<size_t>(row) * a.rb;
+            return p;
+        };
+        auto load = [&](Raw &st, const Pos &p) {
+            const uint8_t *q = p.rp + static_cast<size_t>(p.ch) * F::cb;
+            if constexpr (UP) {
+                const u32x4 h = ld16(q), qa = ld16(q + 16 + 32 * g), qb = ld16(q + 32 + 32 * g);
+                st.w[0] = h.x; st.w[1] = h.y; st.w[2] = h.z; st.w[3] = h.w;
+                st.w[4] = qa.x; st.w[5] = qa.y; st.w[6] = qa.z; st.w[7] = qa.w;
+                st.w[8] = qb.x; st.w[9] = qb.y; st.w[10] = qb.z; st.w[11] = qb.w;
+            } else {
+                // d as a 16-bit load; nd + 1 dwords of payload, the last clamped into the chunk
+                // (with a shift of 0 it is not used)
+                st.w[0] = ld_u16(q + F::bb * g);
+#pragma unroll
+                for (int k = 0; k <= F::nd; ++k)
+                    st.w[1 + k] = *reinterpret_cast<const uint32_t *>(q + 4 * min(pl_dw + k, F::cb / 4 - 1));
+            }
+        };
+
+        auto process = [&](const Raw &cur, const Pos &p, int nq) {
+            float *pp = partial + (static_cast<size_t>(p.which) * NQ * nchunk + p.ch) * pstride + p.tile * 16 + n;
+            const bool store = g == 0 && p.tile * 16 + n < nrows;
+            if constexpr (UP) {
+                u32x4 B[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) B[t] = weights_operand(cur.w[4 + t]);
+                uint32_t scp, mp;
+                dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
+                const float dd = f16_bits_to_f32(cur.w[0] & 0xffffu);
+                const float dmin = f16_bits_to_f32(cur.w[0] >> 16);
+                const float dsc0 = dd * static_cast<float>(scp & 0xffu);
+                const float dsc1 = dd * static_cast<float>((scp >> 8) & 0xffu);
+                const float dm0 = dmin * static_cast<float>(mp & 0xffu);
+                const float dm1 = dmin * static_cast<float>((mp >> 8) & 0xffu);
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                    if (q >= nq) break;  // uniform
+                    // this lane's A row: part a_part of sub-block n >> 1 (block-diagonal, as the decode GEMV)
+                    uint32_t dw[16];
+                    if (a_active) {
+                        const uint4 *src = reinterpret_cast<const uint4 *>(xpart + (2 * q + a_part) * K + p.ch * 256 +
+                                                                           (n >> 1) * 32);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const uint4 v = src[c];
+                            dw[4 * c] = v.x; dw[4 * c + 1] = v.y; dw[4 * c + 2] = v.z; dw[4 * c + 3] = v.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 16; ++c) dw[c] = 0u;
+                    }
+                    f32x4 D = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        u32x4 ao;
+                        ao.x = a_high ? 0u : dw[2 * t];
+                        ao.y = a_high ? 0u : dw[2 * t + 1];
+                        ao.z = a_high ? dw[2 * t] : 0u;
+                        ao.w = a_high ? dw[2 * t + 1] : 0u;
+                        D = mfma(ao, B[t], D);
+                    }
+                    const float2 xs = *reinterpret_cast<const float2 *>(xsum + q * nblk + p.ch * 8 + 2 * g);
+                    float r = dsc0 * ((D[0] + D[1]) - 128.0f * xs.x);
+                    r = fmaf(dsc1, (D[2] + D[3]) - 128.0f * xs.y, r);
+                    r = fmaf(-dm0, xs.x, r);
+                    r = fmaf(-dm1, xs.y, r);
+                    r = sum_lane_groups(r);
+                    if (store) pp[q * nchunk * pstride] = r;
+                }
+            } else {
+                uint32_t C[F::nd];
+#pragma unroll
+                for (int k = 0; k < F::nd; ++k) C[k] = __builtin_amdgcn_alignbyte(cur.w[2 + k], cur.w[1 + k], pl_sh);
+                const float d = f16_bits_to_f32(cur.w[0]);
+                u32x4 B[F::tpb];
+#pragma unroll
+                for (int t = 0; t < F::tpb; ++t) {
+                    if constexpr (FMT == T_Q5_0) {
+                        const uint32_t qh = C[0], qs = C[1 + t];
+                        const uint32_t lo = (qs & 0x0f0f0f0fu) | (spread4(qh >> (4 * t)) << 4);
+                        const uint32_t hi = ((qs >> 4) & 0x0f0f0f0fu) | (spread4(qh >> (16 + 4 * t)) << 4);
+                        B[t] = weights_operand2(lo, hi);
+                    } else {
+                        B[t] = weights_operand(C[t] ^ 0x80808080u);
+                    }
+                }
+                const int blk = p.ch * 4 + g;
+#pragma unroll
+                for (int q = 0; q < NQ; q += 2) {
+                    if (q >= nq) break;  // uniform
+                    const uint4 *src = a_active ? slots + ((static_cast<size_t>(q + a_pair) * 2 + a_part) * nblk + blk) *
+                                                              F::tpb
+                                                : s_zero;
+                    f32x4 D = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int t = 0; t < F::tpb; ++t) {
+                        const uint4 v = src[t];
+                        D = mfma(u32x4{v.x, v.y, v.z, v.w}, B[t], D);
+                    }
+                    const float r0 = sum_lane_groups(d * ((D[0] + D[1]) - F::corr * xsum[q * nblk + blk]));
+                    const float r1 = sum_lane_groups(d * ((D[2] + D[3]) - F::corr * xsum[(q + 1) * nblk + blk]));
+                    if (store) {
+                        pp[q * nchunk * pstride] = r0;
+                        if (q + 1 < nq) pp[(q + 1) * nchunk * pstride] = r1;
+                    }
+                }
+            }
+        };
+
+        for (int q0 = 0; q0 < cnt; q0 += NQ) {
+            const int nq = min(NQ, cnt - q0);
+            set_piece(lt0);
+            Pos cur = at(wave);
+            Raw buf;
+            load(buf, cur);  // the first weights are requested before the activations are staged
+
+            // stage the pass's routes (hi = bf16(x), lo = bf16(x - hi); X sums hi + lo)
+            if constexpr (UP) {
+                const int per = K / 4;  // float4s per route, a multiple of 64: whole waves per route
+                for (int it = tid; it < nq * per; it += kSThreads) {
+                    const int q = it / per, c = it - q * per;
+                    const int route = a.list[beg + q0 + q];
+                    const float4 v = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(route / a.x_div) * K)[c];
+                    const float xe[4] = {v.x, v.y, v.z, v.w};
+                    uint32_t hb[4], lb[4];
+                    float sm = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        hb[i] = bf16_rne(xe[i]);
+                        lb[i] = bf16_rne(xe[i] - bf16_val(hb[i]));
+                        sm += bf16_val(hb[i]) + bf16_val(lb[i]);
+                    }
+                    sm += __shfl_xor(sm, 1, 64);
+                    sm += __shfl_xor(sm, 2, 64);
+                    sm += __shfl_xor(sm, 4, 64);
+                    uint16_t *xp = xpart + static_cast<size_t>(q) * 2 * K;
+                    reinterpret_cast<uint2 *>(xp)[c] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+                    reinterpret_cast<uint2 *>(xp + K)[c] = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+                    if ((c & 7) == 0) xsum[q * nblk + (c >> 3)] = sm;
+                }
+            } else {
+                // one thread per (route, block, t): the 8 values of slot vector t (the tpb threads of a
+                // block are consecutive lanes, and the item count is a multiple of tpb)
+                const int per = nblk * F::tpb;
+                for (int it = tid; it < nq * per; it += kSThreads) {
+                    const int q = it / per, rem = it - q * per, blk = rem / F::tpb, t = rem - blk * F::tpb;
+                    const int route = a.list[beg + q0 + q];
+                    const float4 *xr = reinterpret_cast<const float4 *>(
+                        a.x + static_cast<size_t>(route / a.x_div) * K + blk * 32);
+                    float xe[8];
+                    const float4 u = xr[t];
+                    xe[0] = u.x; xe[1] = u.y; xe[2] = u.z; xe[3] = u.w;
+                    if constexpr (FMT != T_Q8_0) {
+                        const float4 u2 = xr[4 + t];
+                        xe[4] = u2.x; xe[5] = u2.y; xe[6] = u2.z; xe[7] = u2.w;
+                    }
+                    uint32_t hb[8], lb[8];
+                    float sm = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        if (FMT == T_Q8_0 && i >= 4) {
+                            // 16x, exactly 16 times the parts of x
+                            hb[i] = bf16_rne(16.0f * bf16_val(hb[i - 4]));
+                            lb[i] = bf16_rne(16.0f * bf16_val(lb[i - 4]));
+                        } else {
+                            hb[i] = bf16_rne(xe[i]);
+                            lb[i] = bf16_rne(xe[i] - bf16_val(hb[i]));
+                            sm += bf16_val(hb[i]) + bf16_val(lb[i]);
+                        }
+                    }
+#pragma unroll
+                    for (int m = 1; m < F::tpb; m <<= 1) sm += __shfl_xor(sm, m, 64);
+                    uint4 *dst = slots + (static_cast<size_t>(q) * 2 * nblk + blk) * F::tpb + t;
+                    dst[0] = make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),
+                                        hb[6] | (hb[7] << 16));
+                    dst[static_cast<size_t>(nblk) * F::tpb] = make_uint4(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16),
+                                                                         lb[4] | (lb[5] << 16), lb[6] | (lb[7] << 16));
+                    if (t == 0) xsum[q * nblk + blk] = sm;
+                }
+            }
+            for (int pt0 = lt0;;) {
+                if (tid == 0) next_step = kSWaves;
+                __syncthreads();  // staging (and the previous piece's outputs) done
+
+                while (cur.s < nsteps) {
+                    int claimed = 0;
+                    if (lane == 0) claimed = atomicAdd(&next_step, 1);
+                    const Pos nxt = at(__builtin_amdgcn_readfirstlane(claimed));
+                    Raw nb;
+                    load(nb, nxt);
+                    process(buf, cur, nq);
+                    buf = nb;
+                    cur = nxt;
+                }
+                __syncthreads();
+
+                // the piece's outputs: chunk partials summed in chunk order, consecutive threads on
+                // consecutive rows of one route
+                for (int i = tid; i < nq * nrows; i += kSThreads) {
+                    const int q = i / nrows, lr = i - q * nrows;
+                    const float *pq = partial + static_cast<size_t>(q) * nchunk * pstride + lr;
+                    float v0 = 0.0f, v1 = 0.0f;
+                    for (int ch = 0; ch < nchunk; ++ch) {
+                        v0 += pq[ch * pstride];
+                        if constexpr (UP) v1 += pq[(static_cast<size_t>(NQ) * nchunk + ch) * pstride];
+                    }
+                    const int route = a.list[beg + q0 + q];
+                    a.out[static_cast<size_t>(route) * a.rows + r0 + lr] = UP ? v0 / (1.0f + expf(-v0)) * v1 : v0;
+                }
+                pt0 += a.piece;
+                if (pt0 >= lt1) break;
+                set_piece(pt0);
+                cur = at(wave);
+                load(buf, cur);
+            }
+            // the next pass rewrites the staging area, last read before the barrier above, and the
+            // partials only after its own first barrier
+        }
     }
 }
 
@@ -234,116 +676,6 @@ __global__ __launch_bounds__(256) void down_kernel(const DownArgs a) {
     }
 }
 
-// 32-weight formats: each lane decodes a pair of blocks (Q4_0 36 B, Q5_0 44 B, Q8_0 68 B, all
-// multiples of 4, so the pair is read as aligned dwords, exactly in bounds) into 64 weights and dots
-// them with the pass's activations held in LDS.  32 lanes per row, two rows per wave, 64 rows per
-// workgroup.  The activations are stored in 64-float segments padded to 68 floats, so that the
-// lanes, which read one segment each at the same offset, fall in different LDS banks.
-template <int T> struct Pair;
-template <> struct Pair<T_Q4_0> { static constexpr int dw = 9; };
-template <> struct Pair<T_Q5_0> { static constexpr int dw = 11; };
-template <> struct Pair<T_Q8_0> { static constexpr int dw = 17; };
-
-// weight e (0..31) of block j (0, 1) of a pair held in dwords w
-template <int T>
-__device__ __forceinline__ void pair_block(const uint32_t *w, int j, float &d, float q[32]) {
-    if constexpr (T == T_Q8_0) {
-        d = f16_bits_to_f32(j ? w[8] >> 16 : w[0] & 0xffffu);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const uint32_t v = j ? w[9 + c] : __builtin_amdgcn_alignbyte(w[c + 1], w[c], 2);
-#pragma unroll
-            for (int b = 0; b < 4; ++b) q[4 * c + b] = static_cast<float>(static_cast<int8_t>((v >> (8 * b)) & 0xffu));
-        }
-    } else {
-        uint32_t qs[4], qh = 0;
-        if constexpr (T == T_Q5_0) {
-            d = f16_bits_to_f32(j ? w[5] >> 16 : w[0] & 0xffffu);
-            qh = j ? w[6] : __builtin_amdgcn_alignbyte(w[1], w[0], 2);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) qs[c] = j ? w[7 + c] : __builtin_amdgcn_alignbyte(w[c + 2], w[c + 1], 2);
-        } else {
-            d = f16_bits_to_f32(j ? w[4] >> 16 : w[0] & 0xffffu);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) qs[c] = j ? w[5 + c] : __builtin_amdgcn_alignbyte(w[c + 1], w[c], 2);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t byte = (qs[e >> 2] >> (8 * (e & 3))) & 0xffu;
-            int lo = static_cast<int>(byte & 0xfu), hi = static_cast<int>(byte >> 4);
-            if constexpr (T == T_Q5_0) {
-                lo |= static_cast<int>((qh >> e) & 1u) << 4;
-                hi |= static_cast<int>((qh >> (e + 16)) & 1u) << 4;
-                q[e] = static_cast<float>(lo - 16);
-                q[e + 16] = static_cast<float>(hi - 16);
-            } else {
-                q[e] = static_cast<float>(lo - 8);
-                q[e + 16] = static_cast<float>(hi - 8);
-            }
-        }
-    }
-}
-
-template <int T>
-__global__ __launch_bounds__(256) void down_pair_kernel(const DownArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float xa[];  // [kGroup][ffn / 64][68]
-    const int e = blockIdx.x;
-    const int beg = a.gr.offset[e], cnt = a.gr.offset[e + 1] - beg;
-    if (cnt == 0) return;  // uniform per workgroup
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31;
-    const int npairs = a.ffn / 64, qstride = npairs * 68;
-    for (int q0 = 0; q0 < cnt; q0 += kGroup) {
-        const int nq = min(kGroup, cnt - q0);
-        __syncthreads();
-        for (int i = tid; i < kGroup * a.ffn; i += 256) {
-            const int q = i / a.ffn, c = i - q * a.ffn;
-            xa[q * qstride + (c >> 6) * 68 + (c & 63)] =
-                a.act[static_cast<size_t>(a.gr.list[beg + min(q0 + q, cnt - 1)]) * a.ffn + c];
-        }
-        __syncthreads();
-        for (int rr = 0; rr < 16; rr += 2) {
-            const int h = blockIdx.y * 64 + wave * 16 + rr + (lane >> 5);
-            const int hc = min(h, a.hidden - 1);
-            const uint8_t *row = a.w + static_cast<size_t>(e) * a.eb + static_cast<size_t>(hc) * a.rb;
-            float acc[kGroup] = {};
-            for (int p = l32; p < npairs; p += 32) {
-                uint32_t w[Pair<T>::dw];
-                const uint8_t *pp = row + static_cast<size_t>(p) * 2 * Block<T>::bytes;
-#pragma unroll
-                for (int c = 0; c < Pair<T>::dw; ++c) w[c] = *reinterpret_cast<const uint32_t *>(pp + 4 * c);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    float d, q[32];
-                    pair_block<T>(w, j, d, q);
-                    const int base = 68 * p + 32 * j;
-#pragma unroll
-                    for (int c = 0; c < 32; c += 4) {
-                        float wv[4];
-#pragma unroll
-                        for (int b = 0; b < 4; ++b) wv[b] = d * q[c + b];
-#pragma unroll
-                        for (int qq = 0; qq < kGroup; ++qq) {
-                            const float4 xv = *reinterpret_cast<const float4 *>(xa + qq * qstride + base + c);
-                            acc[qq] = fmaf(wv[0], xv.x, acc[qq]);
-                            acc[qq] = fmaf(wv[1], xv.y, acc[qq]);
-                            acc[qq] = fmaf(wv[2], xv.z, acc[qq]);
-                            acc[qq] = fmaf(wv[3], xv.w, acc[qq]);
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int qq = 0; qq < kGroup; ++qq) {
-                float v = acc[qq];
-#pragma unroll
-                for (int m = 1; m < 32; m <<= 1) v += __shfl_xor(v, m, 64);
-                if (qq < nq && l32 == 0 && h < a.hidden)
-                    a.yr[static_cast<size_t>(a.gr.list[beg + q0 + qq]) * a.hidden + h] = v;
-            }
-        }
-    }
-}
-
 // out[t, h] += sum over t's routes in order of fmaf(yr, w, .), skipping invalid experts.
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ yr, const int *__restrict__ ids,
                                                       const float *__restrict__ rw, float *__restrict__ out,
@@ -362,11 +694,56 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-// the pair kernel reads whole block pairs as aligned dwords and keeps kGroup activations in LDS
-bool down_pairs_ok(int type, const uint8_t *w, size_t eb, size_t rb, int ffn) {
-    if (type != T_Q4_0 && type != T_Q5_0 && type != T_Q8_0) return false;
-    return ffn % 64 == 0 && rb % 4 == 0 && eb % 4 == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0 &&
-           static_cast<size_t>(kGroup) * (ffn / 64) * 68 * sizeof(float) <= 160 * 1024;
+constexpr size_t kMaxLds = 160 * 1024;
+// the streaming kernel's static LDS (cost prefix, scan totals, step counter), with some margin
+constexpr size_t kStreamStaticLds = (kMaxExperts + 1 + kSWaves) * sizeof(int64_t) + 256;
+
+// A streaming launch: one workgroup per CU, routes per pass, and the tiles whose partials fit in
+// LDS at once (a workgroup's share is taken in pieces of that many).  The number of selected experts
+// is only known on the device: a piece is sized for twice an even share of min(E, R) of them.
+struct StreamPlan {
+    bool ok = false;
+    int nq = 0, grid = 0, piece = 0;
+    size_t lds = 0;
+};
+
+template <int FMT>
+StreamPlan stream_plan(int rows, int K, int E, int R) {
+    using F = StepFmt<FMT>;
+    constexpr int NW = FMT == T_Q4_K ? 2 : 1;
+    constexpr size_t budget = kMaxLds - kStreamStaticLds;
+    StreamPlan p;
+    const int nblk = K / 32, nchunk = K / F::ce, tpe = (rows + 15) / 16;
+    const int grid = device_info().cu_count;
+    const int64_t share = (static_cast<int64_t>(min(E, R)) * tpe + grid - 1) / grid;
+    for (int nq = 4; nq >= 2; nq -= 2) {
+        const size_t stage = FMT == T_Q4_K ? static_cast<size_t>(nq) * 4 * K
+                                           : static_cast<size_t>(nq) * 2 * nblk * F::tpb * 16;
+        const size_t fixed = stage + static_cast<size_t>(nq) * nblk * sizeof(float);
+        const size_t per_tile = static_cast<size_t>(NW) * nq * nchunk * 16 * sizeof(float);
+        if (fixed + per_tile > budget) continue;
+        const int64_t cap = static_cast<int64_t>((budget - fixed) / per_tile);
+        p.ok = true;
+        p.nq = nq;
+        p.grid = grid;
+        p.piece = static_cast<int>(std::min<int64_t>(cap, std::max<int64_t>(1, 2 * share)));
+        p.lds = fixed + static_cast<size_t>(p.piece) * per_tile;
+        return p;
+    }
+    return p;
+}
+
+template <int FMT>
+void launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
+    if (p.nq == 4) hipLaunchKernelGGL((stream_kernel<FMT, 4>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+    else hipLaunchKernelGGL((stream_kernel<FMT, 2>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+}
+
+// The streaming down kernel reads 4-block chunks as aligned dwords (the chunk sizes 88 and 136
+// bytes are multiples of 4, so every chunk starts 4-aligned once the weights do).
+bool down_stream_ok(int type, const uint8_t *w, int ffn) {
+    if (type != T_Q5_0 && type != T_Q8_0) return false;
+    return ffn % 128 == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0;
 }
 
 }  // namespace
@@ -374,21 +751,26 @@ bool down_pairs_ok(int type, const uint8_t *w, size_t eb, size_t rb, int ffn) {
 size_t moe_grouped_workspace(int tokens, int k, int n_experts, int ffn, int hidden) {
     const size_t R = static_cast<size_t>(tokens) * k;
     return align256((n_experts + 1) * sizeof(int)) + align256(R * sizeof(int)) +
-           align256(R * ffn * sizeof(float)) + align256(R * hidden * sizeof(float));
+           align256(n_experts * sizeof(int4)) + align256(sizeof(int)) + align256(R * ffn * sizeof(float)) +
+           align256(R * hidden * sizeof(float));
 }
 
-bool moe_grouped_shape_ok(int n_experts) { return n_experts <= kMaxExperts; }
+bool moe_grouped_shape_ok(int n_experts, int64_t routes) {
+    return n_experts <= kMaxExperts && routes < (int64_t{1} << kRouteBits);
+}
 
-bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t eb, size_t rb, const float *x, int K) {
+bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t eb, size_t rb, const float *x, int K,
+                       int ffn, int E, int R) {
     const auto al = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
-    return type == T_Q4_K && K % 256 == 0 && rb % 16 == 0 && eb % 16 == 0 && al(wg, 16) && al(wu, 16) && al(x, 16) &&
-           static_cast<size_t>(kGroup) * (4 * K + K / 8) <= 160 * 1024;
+    if (type != T_Q4_K || K % 256 || rb % 16 || eb % 16 || !al(wg, 16) || !al(wu, 16) || !al(x, 16)) return false;
+    return stream_plan<T_Q4_K>(ffn, K, E, R).ok || static_cast<size_t>(kGroup) * (4 * K + K / 8) <= kMaxLds;
 }
 
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int E, int ffn, int K, int hidden,
                        const float *x, const int *ids, const float *rw, void *ws, float *out, int tokens, int k,
                        hipStream_t s) {
+    (void)gu_type;  // Q4_K (moe_grouped_up_ok)
     const int R = tokens * k;
     if (R == 0 || hidden == 0) return hipSuccess;
     uint8_t *p = static_cast<uint8_t *>(ws);
@@ -397,34 +779,47 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
     p += align256((E + 1) * sizeof(int));
     gr.list = reinterpret_cast<int *>(p);
     p += align256(static_cast<size_t>(R) * sizeof(int));
+    gr.seg = reinterpret_cast<int4 *>(p);
+    p += align256(static_cast<size_t>(E) * sizeof(int4));
+    gr.nsel = reinterpret_cast<int *>(p);
+    p += align256(sizeof(int));
     float *act = reinterpret_cast<float *>(p);
     p += align256(static_cast<size_t>(R) * ffn * sizeof(float));
     float *yr = reinterpret_cast<float *>(p);
 
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(256), 0, s, ids, R, E, gr);
-    UpArgs ua{wg, wu, g_eb, g_rb, x, gr, act, ffn, K, k};
-    const size_t lds = static_cast<size_t>(kGroup) * (4 * K + K / 8);
-    hipLaunchKernelGGL(up_kernel, dim3(E, (ffn + 63) / 64), dim3(256), lds, s, ua);
-    DownArgs da{wd, d_eb, d_rb, act, gr, yr, hidden, ffn};
-    const dim3 dgrid(E, (hidden + 63) / 64);
-    const bool pairs = down_pairs_ok(d_type, wd, d_eb, d_rb, ffn);
-    const size_t plds = static_cast<size_t>(kGroup) * (ffn / 64) * 68 * sizeof(float);
-    switch (d_type) {
-        case T_Q4_0:
-            if (pairs) hipLaunchKernelGGL(down_pair_kernel<T_Q4_0>, dgrid, dim3(256), plds, s, da);
-            else hipLaunchKernelGGL(down_kernel<T_Q4_0>, dgrid, dim3(256), 0, s, da);
-            break;
-        case T_Q5_0:
-            if (pairs) hipLaunchKernelGGL(down_pair_kernel<T_Q5_0>, dgrid, dim3(256), plds, s, da);
-            else hipLaunchKernelGGL(down_kernel<T_Q5_0>, dgrid, dim3(256), 0, s, da);
-            break;
-        case T_Q8_0:
-            if (pairs) hipLaunchKernelGGL(down_pair_kernel<T_Q8_0>, dgrid, dim3(256), plds, s, da);
-            else hipLaunchKernelGGL(down_kernel<T_Q8_0>, dgrid, dim3(256), 0, s, da);
-            break;
-        case T_Q4_K: hipLaunchKernelGGL(down_kernel<T_Q4_K>, dgrid, dim3(256), 0, s, da); break;
-        case T_Q6_K: hipLaunchKernelGGL(down_kernel<T_Q6_K>, dgrid, dim3(256), 0, s, da); break;
-        default: return hipErrorInvalidValue;
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, ids, R, E, gr);
+
+    const StreamPlan up = stream_plan<T_Q4_K>(ffn, K, E, R);
+    if (up.ok) {
+        const StreamArgs ua{wg,  wu,  g_eb, g_rb,   x,         k,          gr.list, gr.seg,
+                            gr.nsel, act, ffn, K, K / 256, (ffn + 15) / 16, up.piece};
+        launch_stream<T_Q4_K>(up, ua, s);
+    } else {
+        const UpArgs ua{wg, wu, g_eb, g_rb, x, gr, act, ffn, K, k};
+        const size_t lds = static_cast<size_t>(kGroup) * (4 * K + K / 8);
+        hipLaunchKernelGGL(up_kernel, dim3(E, (ffn + 63) / 64), dim3(256), lds, s, ua);
+    }
+
+    StreamPlan dn;
+    if (down_stream_ok(d_type, wd, ffn)) {
+        if (d_type == T_Q5_0) dn = stream_plan<T_Q5_0>(hidden, ffn, E, R);
+        else dn = stream_plan<T_Q8_0>(hidden, ffn, E, R);
+    }
+    if (dn.ok) {
+        const StreamArgs da{wd,      wd, d_eb,   d_rb, act,       1,                  gr.list, gr.seg,
+                            gr.nsel, yr, hidden, ffn, ffn / 128, (hidden + 15) / 16, dn.piece};
+        if (d_type == T_Q5_0) launch_stream<T_Q5_0>(dn, da, s);
+        else launch_stream<T_Q8_0>(dn, da, s);
+    } else {
+        const DownArgs da{wd, d_eb, d_rb, act, gr, yr, hidden, ffn};
+        const dim3 dgrid(E, (hidden + 63) / 64);
+        switch (d_type) {
+            case T_Q5_0: hipLaunchKernelGGL(down_kernel<T_Q5_0>, dgrid, dim3(256), 0, s, da); break;
+            case T_Q8_0: hipLaunchKernelGGL(down_kernel<T_Q8_0>, dgrid, dim3(256), 0, s, da); break;
+            case T_Q4_K: hipLaunchKernelGGL(down_kernel<T_Q4_K>, dgrid, dim3(256), 0, s, da); break;
+            case T_Q6_K: hipLaunchKernelGGL(down_kernel<T_Q6_K>, dgrid, dim3(256), 0, s, da); break;
+            default: return hipErrorInvalidValue;
+        }
     }
     const int64_t outs = static_cast<int64_t>(tokens) * hidden;
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s, yr, ids, rw,

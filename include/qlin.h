@@ -165,7 +165,7 @@ int qlin_moe_routed_decode_indexed(int gate_up_type, const uint8_t *gate_exps, c
  * x [tokens, in_dim], expert_ids / route_weights [tokens, k], out [tokens, hidden_size] (+=); per
  * token the result is that of qlin_moe_routed_decode_indexed.  workspace: device memory of at least
  * qlin_moe_grouped_workspace_bytes(...) bytes, 256-byte aligned, not used by anything else while the
- * call runs; n_experts <= 1024. */
+ * call runs; n_experts <= 1024 and tokens * k < 2^21 (else QLIN_ERR_LIMIT). */
 size_t qlin_moe_grouped_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size);
 int qlin_moe_routed_decode_grouped(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
                                    size_t gate_up_bytes, int down_type, const uint8_t *down_exps,

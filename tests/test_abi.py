@@ -144,7 +144,7 @@ def test_moe_grouped_validation():
     def al(v):
         return (v + 255) // 256 * 256
     need = qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 64, 1408, 2048)
-    assert need == al(65 * 4) + al(96 * 4) + al(96 * 1408 * 4) + al(96 * 2048 * 4)
+    assert need == al(65 * 4) + al(96 * 4) + al(64 * 16) + al(4) + al(96 * 1408 * 4) + al(96 * 2048 * 4)
     assert qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 0, 1408, 2048) == 0
     a = dict(gate=FAKE, up=FAKE, gub=64 * 1408 * 1152, down=FAKE, db=64 * 2048 * 968, ne=64, ffn=1408,
              ind=2048, hid=2048, x=FAKE, ids=FAKE, rw=FAKE, ws=FAKE, wsb=need, out=FAKE, tokens=16, k=6)
@@ -159,6 +159,7 @@ def test_moe_grouped_validation():
     assert run(ne=0) == SHAPE
     assert run(tokens=-1) == SHAPE
     assert run(ne=1025, gub=1025 * 1408 * 1152, db=1025 * 2048 * 968) == LIMIT
+    assert run(tokens=1 << 18, k=8) == LIMIT   # 2^21 routes: beyond the device-side grouping
     assert run(ids=0) == NULL
     assert run(ws=0) == NULL
     assert run(wsb=need - 1) == LIMIT

@@ -413,17 +413,46 @@ def test_moe_grouped_c5(dn_type):
     assert normwise_rel_err(got, ref) <= 1e-5
 
 
-def test_moe_grouped_many_routes_per_expert_and_fallback():
-    """Routes beyond one pass per expert (8 experts, 24 tokens x 4 routes), and Q6_K gate/up, which
-    takes the per-token kernels inside the same entry point."""
-    for gu_type, seed in ((Q4_K, 301), (Q6_K, 311)):
-        E, ffn, hid, tokens, k = 8, 128, 512, 24, 4
-        wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(gu_type, Q8_0, E, ffn, hid, tokens, k, seed)
-        out0 = np.zeros((tokens, hid), np.float32)
-        banner(f"moe grouped passes gu={gu_type}")
-        got = _run_grouped(gu_type, Q8_0, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
-        ref = _moe_batch_ref(gu_type, Q8_0, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
-        assert normwise_rel_err(got, ref) <= 1e-4
+@pytest.mark.parametrize("gu_type,dn_type,ffn", [(Q4_K, Q8_0, 128), (Q4_K, Q5_0, 256), (Q4_K, Q5_0, 96),
+                                                  (Q6_K, Q8_0, 128)])
+def test_moe_grouped_many_routes_per_expert_and_fallback(gu_type, dn_type, ffn):
+    """Routes beyond one pass per expert (8 experts, 24 tokens x 4 routes, about 12 per expert), most
+    workgroups without a tile, a down width that is not a multiple of 128 (96: the per-element down
+    kernel), and Q6_K gate/up, which takes the per-token kernels inside the same entry point."""
+    E, hid, tokens, k = 8, 512, 24, 4
+    seed = 301 + ffn + 10 * dn_type + gu_type
+    wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(gu_type, dn_type, E, ffn, hid, tokens, k, seed)
+    out0 = np.zeros((tokens, hid), np.float32)
+    banner(f"moe grouped passes gu={gu_type} dn={dn_type} ffn={ffn}")
+    got = _run_grouped(gu_type, dn_type, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+    ref = _moe_batch_ref(gu_type, dn_type, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(got, ref) <= 1e-4
+
+
+def test_moe_grouped_skewed_routing():
+    """One expert chosen by every token (200 routes: 50 passes) beside 15 light ones: the workgroups
+    split the tiles by cost, so the light experts' tiles pack densely and are taken in several LDS
+    pieces per workgroup."""
+    E, ffn, hid, tokens, k = 16, 1024, 512, 200, 2
+    wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(Q4_K, Q5_0, E, ffn, hid, tokens, k, 341)
+    ids = np.ascontiguousarray(np.stack([np.zeros(tokens, np.int32), 1 + np.arange(tokens, dtype=np.int32) % 15], 1))
+    out0 = np.zeros((tokens, hid), np.float32)
+    banner("moe grouped skewed routing")
+    got = _run_grouped(Q4_K, Q5_0, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+    ref = _moe_batch_ref(Q4_K, Q5_0, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(got, ref) <= 1e-4
+
+
+def test_moe_grouped_wide_input_two_routes_per_pass():
+    """in_dim 10240: four routes' staged activations would not fit in LDS, so gate/up runs two routes
+    per pass; every expert has more than two routes (4 experts, 8 tokens x 2 routes)."""
+    E, ffn, hid, tokens, k = 4, 256, 10240, 8, 2
+    wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(Q4_K, Q5_0, E, ffn, hid, tokens, k, 331)
+    out0 = np.zeros((tokens, hid), np.float32)
+    banner("moe grouped wide input")
+    got = _run_grouped(Q4_K, Q5_0, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+    ref = _moe_batch_ref(Q4_K, Q5_0, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(got, ref) <= 1e-4
 
 
 # ---- batched and fused streaming launches ------------------------------------------------------
