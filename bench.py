@@ -362,6 +362,56 @@ def wl_q6k(args, torch, qlin, gen):
                        Q6_K, [("lm_head", 102400, 2048)], 6)
 
 
+def wl_c3(args, torch, qlin, gen):
+    """C3: the quantized-linear work of one decode token of a Qwen2.5-0.5B-architecture model in Q8_0
+    (24 layers of q/k/v, o, gate/up + SiLU, down, then the lm_head): 97 launches, as the default
+    workload does for Qwen2-7B.  Attention, norms and RoPE are outside this path."""
+    L, H, KVD, F, V = 24, 896, 128, 4864, 151936
+    rb_h, rb_f = qlin.row_bytes(Q8_0, H), qlin.row_bytes(Q8_0, F)
+    shapes = [("q", H, H), ("k", KVD, H), ("v", KVD, H), ("o", H, H), ("gate", F, H), ("up", F, H), ("down", H, F)]
+    layers = [{nm: synth_blocks(torch, Q8_0, n, k, gen) for nm, n, k in shapes} for _ in range(L)]
+    lm_head = synth_blocks(torch, Q8_0, V, H, gen)
+    x_h, x_f = torch.randn(H, device="cuda", generator=gen), torch.randn(F, device="cuda", generator=gen)
+    y = {nm: torch.empty(n, device="cuda") for nm, n, _ in shapes}
+    act, logits = torch.empty(F, device="cuda"), torch.empty(V, device="cuda")
+
+    def step():
+        for Lw in layers:
+            qlin.quant_gemv_multi(Q8_0, [Lw["q"], Lw["k"], Lw["v"]], rb_h, x_h, [y["q"], y["k"], y["v"]], [H, KVD, KVD], H)
+            qlin.quant_gemv(Q8_0, Lw["o"], rb_h, x_h, y["o"], H, H, 1)
+            qlin.quant_swiglu(Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, x_h, act, F, H)
+            qlin.quant_gemv(Q8_0, Lw["down"], rb_f, act, y["down"], H, F, 1)
+        qlin.quant_gemv(Q8_0, lm_head, rb_h, x_h, logits, V, H, 1)
+
+    per_layer = ((H + 2 * KVD) * rb_h + 4 * (H + H + 2 * KVD) + H * rb_h + 8 * H
+                 + 2 * F * rb_h + 4 * (H + F) + H * rb_f + 4 * (F + H))
+    nbytes = L * per_layer + V * rb_h + 4 * (H + V)
+    reps = max(1, args.steps // 4)
+    us = graph_us(torch, qlin, step, reps)
+    # the launches that take the most time together: the 24 gate/up SwiGLU launches
+    us_sw = graph_us(torch, qlin, lambda: [qlin.quant_swiglu(Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, x_h, act, F, H)
+                                           for Lw in layers], reps) / L
+    sw_bytes = 2 * F * rb_h + 4 * (H + F)
+    log(f"c3: {us:.2f} us/token ({1e6 / us:.0f} tok/s), gate/up SwiGLU {us_sw:.2f} us/launch")
+    result = {
+        "metric": "decode GEMV HBM GB/s + tokens/s, Qwen2.5-0.5B-arch Q8_0 linear work per token, 1 GPU",
+        "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
+        "tokens_per_s": round(1e6 / us, 1), "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random Q8_0 blocks, f32 N(0,1) activations)",
+        "config": {"workload": "c3-q8_0-decode-token", "layers": L, "hidden": H, "ffn": F, "kv_dim": KVD, "vocab": V,
+                   "weight_format": "Q8_0", "batch": 1, "launches_per_step": 4 * L + 1,
+                   "algorithmic_bytes_per_step": nbytes, "execution": "hip graph replay"},
+        "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "mfma_gemv_kernel<8, true, *> (Q8_0 gate/up SwiGLU, 2 x [4864, 896])",
+                     "avg_launch_us": round(us_sw, 3), "algorithmic_bytes_per_launch": sw_bytes},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_gemv_gbs(torch, Q8_0, layers[0]["gate"], rb_h, F, H, args.cpu_seconds)
+    return result
+
+
 def wl_c4(args, torch, qlin, gen):
     """C4: Q4_K [14336, 4096] x activations [512, 4096] (f16 N(0,1) values) quantized to Q8_1 on the
     fly, then the matrix-core GEMM; a step is both launches."""
@@ -476,7 +526,7 @@ def wl_c5(args, torch, qlin, gen):
 
 
 WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
-             "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k}
+             "c3-q8_0-decode-token": wl_c3, "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k}
 
 
 def cpu_baseline(torch, layer, shapes, xin, outs, seconds, bytes_per_step):

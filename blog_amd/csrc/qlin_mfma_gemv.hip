@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
                 sm += bf16_val(hb[e]) + bf16_val(lb[e]);
             }
             // the threads of a 16- or 32-element group are consecutive lanes, and K is a multiple of
-            // 256, so a group is entirely below K/4 or entirely above it
+            // 128, so a group is entirely below K/4 or entirely above it
             sm += __shfl_xor(sm, 1, 64);
             sm += __shfl_xor(sm, 2, 64);
             if constexpr (XS == 32) sm += __shfl_xor(sm, 4, 64);
@@ -498,7 +498,9 @@ bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float
     if (type != T_Q4_K && type != T_Q4_0 && type != T_Q8_0 && type != T_Q6_K) return false;
     // Q4_K loads 16-byte pieces; the 32-weight formats aligned dwords
     const size_t wal = type == T_Q4_K ? 16 : 4;
-    if (nmat < 1 || nmat > kMaxStreamMats || k % 256 || rb % wal || !aligned16(x) || total <= 0) return false;
+    // whole chunks (Q8_0: 128 weights, the others 256); x is staged as float4s in groups of 8 lanes
+    if (nmat < 1 || nmat > kMaxStreamMats || k % chunk_elems(type) || rb % wal || !aligned16(x) || total <= 0)
+        return false;
     if (k / 4 > kMaxXr * kThreads) return false;
     for (int i = 0; i < nmat; ++i)
         if (reinterpret_cast<uintptr_t>(w[i]) % wal) return false;

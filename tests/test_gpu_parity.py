@@ -102,6 +102,7 @@ GEMV_CASES = [
     (Q4_K, 1, 256), (Q4_K, 3, 512), (Q4_K, 17, 3584), (Q4_K, 4097, 8448),
     (Q4_K, 512, 3584), (Q4_K, 3584, 3584), (Q4_K, 18944, 3584), (Q4_K, 3584, 18944),
     (Q8_0, 4096, 4096), (Q8_0, 7, 96), (Q8_0, 4864, 896), (Q8_0, 33, 256), (Q8_0, 1000, 8448),
+    (Q8_0, 896, 896), (Q8_0, 896, 4864), (Q8_0, 128, 128),
     (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64), (Q4_0, 17, 256), (Q4_0, 300, 4608),
     (Q5_0, 2048, 1408), (Q5_0, 5, 64),
     (Q6_K, 64, 512), (Q6_K, 257, 2048), (Q6_K, 16384, 2048), (Q6_K, 33, 768), (Q6_K, 100, 7168),
@@ -121,7 +122,7 @@ def test_gemv_parity(qtype, out_dim, in_dim):
 
 
 @pytest.mark.parametrize("qtype,out_dim,in_dim", [(Q4_K, 300, 3584), (Q4_K, 1000, 8448), (Q8_0, 300, 4096),
-                                                  (Q4_0, 1000, 3584)])
+                                                  (Q8_0, 300, 896), (Q4_0, 1000, 3584)])
 def test_gemv_generic_path_agrees(qtype, out_dim, in_dim):
     """A weight pointer 2 bytes off the alignment the matrix-core kernel needs takes the generic
     kernel: both agree with the oracle."""
@@ -481,7 +482,8 @@ def test_swiglu_stream(ffn, hid):
     assert normwise_rel_err(host(act_d), ref) <= 1e-4
 
 
-@pytest.mark.parametrize("qtype,ffn,hid", [(Q4_0, 18944, 3584), (Q8_0, 4864, 896 + 128), (Q4_0, 9, 256)])
+@pytest.mark.parametrize("qtype,ffn,hid", [(Q4_0, 18944, 3584), (Q8_0, 4864, 896 + 128), (Q8_0, 4864, 896),
+                                          (Q4_0, 9, 256)])
 def test_swiglu_matrix_core_formats(qtype, ffn, hid):
     """Fused gate/up SiLU on the 32-weight formats (C2's gate/up pair in one launch)."""
     wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=410 + hid)
@@ -492,6 +494,18 @@ def test_swiglu_matrix_core_formats(qtype, ffn, hid):
     qlin.quant_swiglu(qtype, dev(wg), dev(wu), rb, rb, dev(x), act_d, ffn, hid)
     ref = orc.swiglu(qtype, wg, wu, rb, rb, x, ffn, hid)
     assert normwise_rel_err(host(act_d), ref) <= 1e-4
+
+
+def test_gemv_multi_c3_qkv():
+    """C3's q, k, v ([896|128|128, 896] Q8_0, 128-weight chunks) in one matrix-core launch."""
+    shapes = [896, 128, 128]
+    mats = [qgen.random_matrix(Q8_0, n, 896, seed=520 + i) for i, n in enumerate(shapes)]
+    x = qgen.random_x(1, 896, seed=530)
+    ys = [empty_f32(n) for n in shapes]
+    banner("gemv multi c3 qkv")
+    qlin.quant_gemv_multi(Q8_0, [dev(w) for w, _, _ in mats], mats[0][1], dev(x), ys, shapes, 896)
+    for (w, rb, _), y, n in zip(mats, ys, shapes):
+        assert normwise_rel_err(host(y), orc.matmul_f64(Q8_0, w, rb, x, n, 896)[0]) <= FP32
 
 
 def test_gemv_multi_generic_types():
