@@ -37,7 +37,9 @@ constexpr int kBN = kWaves * kNT * 16;    // weight rows per workgroup (256)
 constexpr int kMT = 4;                    // 16-token tiles per workgroup
 constexpr int kBM = kMT * 16;             // tokens per workgroup (64)
 constexpr int kPlane = 2 * kMT * 8 * 64;  // uint4s of one buffer's A planes (hi, lo): 64 KB
-constexpr int kBuf = kPlane + kMT * 16;   // plus the s8 operands
+constexpr int kBuf = kPlane + kMT * 64;   // plus the min-term operands [mt][lane] (lanes >= 16 stay zero)
+constexpr int kSJ = kThreads / kMT / 64;  // staging waves per token tile
+constexpr int kJJ = 8 / kSJ;              // sub-blocks each staging thread converts
 constexpr size_t kLds = 2 * kBuf * sizeof(uint4);  // two buffers
 
 struct GemmArgs {
@@ -56,20 +58,6 @@ __device__ __forceinline__ f32x4 mfma(const uint4 &a, const uint4 &b, const f32x
 
 __device__ __forceinline__ uint32_t h2u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ f16x2 u2h(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
-
-// 6-bit (scale, min) of sub-block J from scale bytes s[0..11] held in three dwords (kernel.cu:913-921).
-template <int J>
-__device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc, uint32_t &mn) {
-    const uint32_t s[3] = {s0, s1, s2};
-    auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-    if constexpr (J < 4) {
-        sc = byte(J) & 63u;
-        mn = byte(J + 4) & 63u;
-    } else {
-        sc = (byte(J + 4) & 0xfu) | ((byte(J - 4) >> 6) << 4);
-        mn = (byte(J + 4) >> 4) | ((byte(J) >> 6) << 4);
-    }
-}
 
 // B operand of sub-block J for this lane: 8 nibbles (k = 8g .. 8g+7 of the sub-block) times sc.
 template <int J>
@@ -105,11 +93,14 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) wrow[t] = a.w + static_cast<size_t>(min(o0 + t * 16 + n, a.n - 1)) * a.rb;
 
-    // staging role: token tile smt, slot lane sl (token si, k-group sg), sub-blocks 4*sjh .. 4*sjh+3
-    const int smt = tid >> 7, sjh = (tid >> 6) & 1, sl = tid & 63, si = sl & 15, sg = sl >> 4;
+    // staging role: token tile smt, slot lane sl (token si, k-group sg), sub-blocks kJJ*sjh .. +kJJ-1
+    const int smt = tid / (kSJ * 64), sjh = (tid >> 6) % kSJ, sl = tid & 63, si = sl & 15, sg = sl >> 4;
     const int tok = m0 + smt * 16 + si;
-    const bool tok_ok = tok < a.m;
     const uint8_t *xrow = a.xq + static_cast<size_t>(min(tok, a.m - 1)) * a.xrb;
+
+    // min-term operand entries of lane-groups 1..3 stay zero (staging writes lanes 0..15 only)
+    for (int i = tid; i < 2 * kMT * 64; i += kThreads)
+        if ((i & 63) >= 16) s8ops(i / (kMT * 64))[i % (kMT * 64)] = make_uint4(0u, 0u, 0u, 0u);
 
     f32x4 acc[kMT][kNT];
 #pragma unroll
@@ -123,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
         uint2 qs[kNT][4];
     };
     struct XRaw {
-        uint32_t bh[4], q0[4], q1[4];
+        uint32_t bh[kJJ], q0[kJJ], q1[kJJ];
     };
     // past the end a fetch reloads the last super-block (valid addresses, never used)
     auto fetch_w = [&](WRaw &w, int sb) {
@@ -139,8 +130,8 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
     auto fetch_x = [&](XRaw &x, int sb) {
         sb = min(sb, a.nsb - 1);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const uint8_t *blk = xrow + static_cast<size_t>(sb * 8 + 4 * sjh + jj) * 36;
+        for (int jj = 0; jj < kJJ; ++jj) {
+            const uint8_t *blk = xrow + static_cast<size_t>(sb * 8 + kJJ * sjh + jj) * 36;
             x.bh[jj] = *reinterpret_cast<const uint32_t *>(blk);
             x.q0[jj] = *reinterpret_cast<const uint32_t *>(blk + 4 + 8 * sg);
             x.q1[jj] = *reinterpret_cast<const uint32_t *>(blk + 8 + 8 * sg);
@@ -153,10 +144,10 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
     auto stage = [&](const XRaw &x, int buf) {
         uint4 *pl = plane(buf);
         const f16x2 off = splat(-1152.0f);
-        uint32_t s8h[4];
+        uint32_t s8h[kJJ];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int j = 4 * sjh + jj;
+        for (int jj = 0; jj < kJJ; ++jj) {
+            const int j = kJJ * sjh + jj;
             const f16x2 d2 = u2h((x.bh[jj] & 0xffffu) * 0x10001u);
             const uint32_t u[2] = {x.q0[jj] ^ 0x80808080u, x.q1[jj] ^ 0x80808080u};
             uint32_t hi[4], lo[4];
@@ -168,16 +159,16 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
                 hi[e] = h2u(h2);
                 lo[e] = h2u(__builtin_elementwise_fma(d2, q2, -h2));
             }
-            uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]), L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            if (!tok_ok) H = L = make_uint4(0u, 0u, 0u, 0u);
-            pl[((0 * kMT + smt) * 8 + j) * 64 + sl] = H;
-            pl[((1 * kMT + smt) * 8 + j) * 64 + sl] = L;
-            s8h[jj] = tok_ok ? x.bh[jj] >> 16 : 0u;
+            // tokens past m repeat the last row: their D rows are never stored
+            pl[((0 * kMT + smt) * 8 + j) * 64 + sl] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            pl[((1 * kMT + smt) * 8 + j) * 64 + sl] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            s8h[jj] = x.bh[jj] >> 16;
         }
-        // the s8 operand row of token si: halves s8_0 .. s8_7 (written by the two threads of sg == 0)
+        // the s8 operand row of token si: halves s8_0 .. s8_7 (written by the threads of sg == 0)
         if (sg == 0) {
-            uint2 *dst = reinterpret_cast<uint2 *>(&s8ops(buf)[smt * 16 + si]) + sjh;
-            *dst = make_uint2(s8h[0] | (s8h[1] << 16), s8h[2] | (s8h[3] << 16));
+            uint16_t *dst = reinterpret_cast<uint16_t *>(&s8ops(buf)[smt * 64 + si]) + kJJ * sjh;
+#pragma unroll
+            for (int jj = 0; jj < kJJ; ++jj) dst[jj] = static_cast<uint16_t>(s8h[jj]);
         }
     };
 
@@ -195,17 +186,30 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
         for (int i = 0; i < kMT; ++i)
 #pragma unroll
             for (int t = 0; t < kNT; ++t) D[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        uint32_t mins[kNT][8];
+        // All 8 scales of a tile at once (kernel.cu:913-921 on whole dwords): bytes j of sl are sub-block
+        // j < 4, of sh sub-block 4 + j; as fp16 pairs (sc_2i, sc_2i+1) via the bytes (v, 0x64) = 1024 + v.
+        const f16x2 off = splat(-1024.0f);
+        auto pairs = [&](uint32_t v, f16x2 *dst) {
+            dst[0] = u2h(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u)) + off;
+            dst[1] = u2h(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)) + off;
+        };
+        f16x2 scp[kNT][4], cp[kNT][4];
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+            const uint32_t s0 = w.hdr[t].y, s2 = w.hdr[t].w;
+            pairs(s0 & 0x3f3f3f3fu, scp[t]);
+            pairs((s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u), scp[t] + 2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cp[t][i] = scp[t][i] * off;
+        }
         auto sub_block = [&](auto jc) {
             constexpr int J = decltype(jc)::value;
             uint4 B[kNT];
 #pragma unroll
             for (int t = 0; t < kNT; ++t) {
-                uint32_t sc, mn;
-                scale_min<J>(w.hdr[t].y, w.hdr[t].z, w.hdr[t].w, sc, mn);
-                mins[t][J] = mn;
-                const f16x2 sc2 = splat(static_cast<float>(sc));
-                B[t] = weights_b<J>(w.qs[t][J >> 1], sc2, sc2 * splat(-1024.0f));
+                const f16x2 sc2 = __builtin_shufflevector(scp[t][J >> 1], scp[t][J >> 1], J & 1, J & 1);
+                const f16x2 c2 = __builtin_shufflevector(cp[t][J >> 1], cp[t][J >> 1], J & 1, J & 1);
+                B[t] = weights_b<J>(w.qs[t][J >> 1], sc2, c2);
             }
             // hi for every (token tile, row tile), then lo: consecutive MFMAs never feed each other
 #pragma unroll
@@ -216,6 +220,9 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 #pragma unroll
                     for (int t = 0; t < kNT; ++t) D[i][t] = mfma(av, B[t], D[i][t]);
                 }
+            // no hoisting of the next sub-block's LDS reads above these MFMAs: the registers they
+            // would hold push the kernel past its 256 VGPRs (measured 3% faster)
+            __builtin_amdgcn_sched_barrier(0);
         };
         sub_block(std::integral_constant<int, 0>{});
         sub_block(std::integral_constant<int, 1>{});
@@ -226,19 +233,20 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
         sub_block(std::integral_constant<int, 6>{});
         sub_block(std::integral_constant<int, 7>{});
 
-        // min term: sum_j s8_j * m_j on one more MFMA (k-slots 0..7 carried by lane-group 0)
+        // min term: sum_j s8_j * m_j on one more MFMA.  Only k-slots 0..7 (lane-group 0) carry s8; the
+        // other lanes' A entries are zeros in LDS, so their B entries (finite mins) add nothing.
         const uint4 *s8 = s8ops(buf);
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
-            uint4 b2 = make_uint4(0u, 0u, 0u, 0u);
-            if (g == 0) {
-                auto mh = [&](int j) { return h2u(f16x2{static_cast<_Float16>(static_cast<float>(mins[t][j])),
-                                                        static_cast<_Float16>(static_cast<float>(mins[t][j + 1]))}); };
-                b2 = make_uint4(mh(0), mh(2), mh(4), mh(6));
-            }
+            // the 8 mins of the tile, as the scales above (bytes j of ml: sub-block j < 4; of mh: 4 + j)
+            const uint32_t s1 = w.hdr[t].z, s2 = w.hdr[t].w;
+            f16x2 mp[4];
+            pairs(s1 & 0x3f3f3f3fu, mp);
+            pairs(((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u), mp + 2);
+            const uint4 b2 = make_uint4(h2u(mp[0]), h2u(mp[1]), h2u(mp[2]), h2u(mp[3]));
 #pragma unroll
             for (int i = 0; i < kMT; ++i) {
-                const uint4 a2 = g == 0 ? s8[i * 16 + n] : make_uint4(0u, 0u, 0u, 0u);
+                const uint4 a2 = s8[i * 64 + lane];
                 const f32x4 d2 = mfma(a2, b2, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
