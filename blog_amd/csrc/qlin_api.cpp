@@ -114,6 +114,10 @@ const char *qlin_status_string(int status) {
         case QLIN_ERR_LIMIT: return "argument beyond a documented limit";
         case QLIN_ERR_LAUNCH: return "HIP launch failed";
         case QLIN_ERR_ALIGN: return "misaligned pointer";
+        case QLIN_ERR_IO: return "cannot open or map the file";
+        case QLIN_ERR_FORMAT: return "malformed or unsupported GGUF file";
+        case QLIN_ERR_NOT_FOUND: return "no such tensor, key or index, or a value of another type";
+        case QLIN_ERR_ALLOC: return "device allocation or copy failed";
         default: return "unknown status";
     }
 }

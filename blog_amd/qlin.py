@@ -14,9 +14,19 @@ LIB_PATH = os.path.join(PKG, "libqlin.so")
 
 Q4_0, Q5_0, Q8_0, Q8_1, Q4_K, Q6_K = 2, 6, 8, 9, 12, 14
 STATUS = {0: "QLIN_OK", 1: "QLIN_ERR_UNSUPPORTED_TYPE", 2: "QLIN_ERR_SHAPE", 3: "QLIN_ERR_NULL",
-          4: "QLIN_ERR_ROW_BYTES", 5: "QLIN_ERR_LIMIT", 6: "QLIN_ERR_LAUNCH", 7: "QLIN_ERR_ALIGN"}
+          4: "QLIN_ERR_ROW_BYTES", 5: "QLIN_ERR_LIMIT", 6: "QLIN_ERR_LAUNCH", 7: "QLIN_ERR_ALIGN",
+          8: "QLIN_ERR_IO", 9: "QLIN_ERR_FORMAT", 10: "QLIN_ERR_NOT_FOUND", 11: "QLIN_ERR_ALLOC"}
 
 P, I, I64, SZ, F = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
+S, U32, U64 = C.c_char_p, C.c_uint32, C.c_uint64
+PP, PI, PI64, PU64, PSZ, PD = (C.POINTER(C.c_void_p), C.POINTER(C.c_int), C.POINTER(C.c_int64),
+                               C.POINTER(C.c_uint64), C.POINTER(C.c_size_t), C.POINTER(C.c_double))
+
+
+class GgufTensorInfo(C.Structure):
+    """struct qlin_gguf_tensor (include/qlin_gguf.h)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("n_dims", C.c_int), ("shape", C.c_int64 * 4),
+                ("nbytes", C.c_uint64), ("offset", C.c_uint64), ("data", C.c_void_p)]
 
 # name -> (restype, argtypes); every symbol of include/qlin.h
 SIGNATURES = {
@@ -48,6 +58,29 @@ SIGNATURES = {
     "qlin_moe_routed_decode_indexed": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, P, I]),
     "qlin_moe_grouped_workspace_bytes": (SZ, [I, I, I, I, I]),
     "qlin_moe_routed_decode_grouped": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, SZ, P, I, I]),
+    # include/qlin_gguf.h
+    "qlin_gguf_open": (I, [S, PP]),
+    "qlin_gguf_close": (None, [P]),
+    "qlin_gguf_version": (U32, [P]),
+    "qlin_gguf_alignment": (U32, [P]),
+    "qlin_gguf_tensor_count": (I64, [P]),
+    "qlin_gguf_find_tensor": (I64, [P, S]),
+    "qlin_gguf_tensor_info": (I, [P, I64, C.POINTER(GgufTensorInfo)]),
+    "qlin_gguf_metadata_count": (I64, [P]),
+    "qlin_gguf_metadata_key": (S, [P, I64]),
+    "qlin_gguf_metadata_type": (I, [P, S]),
+    "qlin_gguf_get_i64": (I, [P, S, PI64]),
+    "qlin_gguf_get_f64": (I, [P, S, PD]),
+    "qlin_gguf_get_str": (I, [P, S, PP, PSZ]),
+    "qlin_gguf_get_array_info": (I, [P, S, PI, PI64]),
+    "qlin_gguf_get_array_i64": (I, [P, S, I64, PI64]),
+    "qlin_gguf_get_array_f64": (I, [P, S, I64, PD]),
+    "qlin_gguf_get_array_str": (I, [P, S, I64, PP, PSZ]),
+    "qlin_pool_create": (I, [PP]),
+    "qlin_pool_destroy": (None, [P]),
+    "qlin_pool_weight": (I, [P, P, S, PP, PU64]),
+    "qlin_pool_expert_view": (I, [P, P, S, I, PP, PU64, PI64, PI64]),
+    "qlin_pool_resident_bytes": (U64, [P]),
 }
 
 
@@ -64,6 +97,14 @@ def lib() -> C.CDLL:
     """Loads the HIP library; raises if it has not been built (no fallback path exists)."""
     global _lib
     if _lib is None:
+        # torch ships its own HIP runtime (torch/lib/libamdhip64.so, soname libamdhip64.so.7).  Loaded
+        # first, it satisfies this library's libamdhip64.so.7 dependency, so the process has one HIP
+        # runtime; loaded after, it would bring a second one next to /opt/rocm's, and device memory of
+        # one is unusable from the other.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: run `python -m blog_amd.build` (HIP/gfx950 build)")
         L = C.CDLL(LIB_PATH)

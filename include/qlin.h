@@ -46,7 +46,11 @@ typedef enum qlin_status {
     QLIN_ERR_ROW_BYTES = 4,        /* row / expert stride smaller than the packed data it holds */
     QLIN_ERR_LIMIT = 5,            /* argument beyond a documented limit (e.g. n_experts > 256) */
     QLIN_ERR_LAUNCH = 6,           /* the HIP runtime rejected the launch */
-    QLIN_ERR_ALIGN = 7             /* pointer misaligned for its element type */
+    QLIN_ERR_ALIGN = 7,            /* pointer misaligned for its element type */
+    QLIN_ERR_IO = 8,               /* GGUF reader: the file cannot be opened or mapped */
+    QLIN_ERR_FORMAT = 9,           /* GGUF reader: malformed or unsupported file contents */
+    QLIN_ERR_NOT_FOUND = 10,       /* GGUF reader: no such tensor, key or index, or another value type */
+    QLIN_ERR_ALLOC = 11            /* weight pool: device allocation or copy failed */
 } qlin_status;
 
 /* Human-readable name of a status code. */

@@ -11,13 +11,13 @@ import pytest
 from blog_amd import qlin
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "qlin.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("qlin.h", "qlin_gguf.h")]
 
 OK, UNSUP, SHAPE, NULL, ROWB, LIMIT, LAUNCH, ALIGN = range(8)
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(qlin_\w+)\s*\(", text)))
 
