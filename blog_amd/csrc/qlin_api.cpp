@@ -312,6 +312,73 @@ int qlin_moe_routed_decode_indexed(int gu_type, const uint8_t *gate, const uint8
                                                             hidden, ffn_dim);
 }
 
+static bool embed_mla_type(int t) {
+    return t == QLIN_TYPE_Q4_K || t == QLIN_TYPE_Q6_K || t == QLIN_TYPE_Q5_0 || t == QLIN_TYPE_Q8_0;
+}
+
+int qlin_launch_quant_embedding(int type, const int *input, float *output, const uint8_t *table, size_t rb,
+                                int hidden, int input_size) {
+    if (!embed_mla_type(type)) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (hidden < 0 || input_size < 0 || hidden % elems_of(type)) return QLIN_ERR_SHAPE;
+    if (rb < min_row_bytes(type, hidden)) return QLIN_ERR_ROW_BYTES;
+    const bool work = hidden > 0 && input_size > 0;
+    if (!work) return QLIN_OK;
+    if (!input || !table) return QLIN_ERR_NULL;
+    int rc = check_f32(output, true);
+    if (rc) return rc;
+    if (!aligned(input, 4) || !aligned(table, 2) || rb % 2) return QLIN_ERR_ALIGN;
+    return launched(qlin::quant_embedding(type, input, output, table, rb, hidden, input_size, stream()));
+}
+
+// kv_b of n_heads * (qk_nope + v_head) rows of kv_lora weights
+static int check_kv_b(int type, const uint8_t *w, size_t rb, int n_heads, int qk_nope, int qk_rope, int v_head,
+                      int kv_lora) {
+    if (!embed_mla_type(type)) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (n_heads < 0 || qk_nope < 0 || qk_rope < 0 || v_head < 0 || kv_lora < 0 || kv_lora % elems_of(type))
+        return QLIN_ERR_SHAPE;
+    if (rb < min_row_bytes(type, kv_lora)) return QLIN_ERR_ROW_BYTES;
+    if (!aligned(w, 2) || rb % 2) return QLIN_ERR_ALIGN;
+    return QLIN_OK;
+}
+
+int qlin_launch_mla_absorb_q_nope(int type, const float *q, const uint8_t *w, size_t rb, float *q_abs, int n_heads,
+                                  int qk_nope, int qk_rope, int v_head, int kv_lora) {
+    int rc = check_kv_b(type, w, rb, n_heads, qk_nope, qk_rope, v_head, kv_lora);
+    if (rc) return rc;
+    const bool work = n_heads > 0 && kv_lora > 0;
+    if (!work) return QLIN_OK;
+    if (!w) return QLIN_ERR_NULL;
+    if ((rc = check_f32(q_abs, true)) || (rc = check_f32(q, qk_nope > 0))) return rc;
+    return launched(qlin::mla_absorb_q_nope(type, q, w, rb, q_abs, n_heads, qk_nope, qk_rope, v_head, kv_lora,
+                                            stream()));
+}
+
+int qlin_launch_mla_absorb_q4_xsum_delta(const float *q, const uint8_t *w, size_t rb, float *delta, int n_heads,
+                                         int qk_nope, int qk_rope, int v_head, int kv_lora) {
+    int rc = check_kv_b(QLIN_TYPE_Q4_K, w, rb, n_heads, qk_nope, qk_rope, v_head, kv_lora);
+    if (rc) return rc;
+    const bool work = n_heads > 0 && kv_lora > 0;
+    if (!work) return QLIN_OK;
+    if (!w) return QLIN_ERR_NULL;
+    if ((rc = check_f32(delta, true)) || (rc = check_f32(q, qk_nope > 0))) return rc;
+    return launched(qlin::mla_absorb_q4_xsum_delta(q, w, rb, delta, n_heads, qk_nope, qk_rope, v_head, kv_lora,
+                                                   stream()));
+}
+
+int qlin_launch_mla_absorb_v(int type, const uint8_t *w, size_t rb, const float *latent, const float *delta,
+                             float *attn, int n_heads, int qk_nope, int v_head, int kv_lora) {
+    int rc = check_kv_b(type, w, rb, n_heads, qk_nope, 0, v_head, kv_lora);
+    if (rc) return rc;
+    const bool work = n_heads > 0 && v_head > 0;
+    if (!work) return QLIN_OK;
+    if (!w) return QLIN_ERR_NULL;
+    if ((rc = check_f32(attn, true)) || (rc = check_f32(latent, kv_lora > 0)) ||
+        (rc = check_f32(delta, type == QLIN_TYPE_Q4_K && kv_lora > 0)))
+        return rc;
+    return launched(qlin::mla_absorb_v(type, w, rb, latent, delta, attn, n_heads, qk_nope, v_head, kv_lora,
+                                       stream()));
+}
+
 size_t qlin_moe_grouped_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size) {
     if (tokens < 0 || k < 0 || n_experts <= 0 || ffn_dim <= 0 || hidden_size <= 0) return 0;
     return qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden_size);

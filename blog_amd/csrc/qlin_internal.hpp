@@ -80,4 +80,14 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
                        int hidden, const float *x, const int *ids, const float *rw, void *workspace, float *out,
                        int tokens, int k, hipStream_t s);
 
+// Quantized embedding rows and the MLA latent-absorption products over kv_b (qlin_embed_mla.hip).
+hipError_t quant_embedding(int type, const int *ids, float *out, const uint8_t *table, size_t row_bytes, int hidden,
+                           int n, hipStream_t s);
+hipError_t mla_absorb_q_nope(int type, const float *q, const uint8_t *w, size_t row_bytes, float *q_abs, int n_heads,
+                             int qk_nope, int qk_rope, int v_head, int kv_lora, hipStream_t s);
+hipError_t mla_absorb_q4_xsum_delta(const float *q, const uint8_t *w, size_t row_bytes, float *delta, int n_heads,
+                                    int qk_nope, int qk_rope, int v_head, int kv_lora, hipStream_t s);
+hipError_t mla_absorb_v(int type, const uint8_t *w, size_t row_bytes, const float *latent, const float *delta,
+                        float *attn, int n_heads, int qk_nope, int v_head, int kv_lora, hipStream_t s);
+
 }  // namespace qlin

@@ -177,6 +177,27 @@ int qlin_moe_routed_decode_grouped(int gate_up_type, const uint8_t *gate_exps, c
                                    const float *x, const int *expert_ids, const float *route_weights,
                                    void *workspace, size_t workspace_bytes, float *out, int tokens, int k);
 
+/* launch_quant_embedding (kernel.cuh:141-142): output[t, :] = the dequantized row input[t] of a
+ * quantized table [vocab, hidden_size] (Q4_K, Q6_K, Q5_0 or Q8_0; bit-exact element values).  As in
+ * the reference, the ids must be rows of the table; they are device data and are not checked. */
+int qlin_launch_quant_embedding(int type, const int *input, float *output, const uint8_t *table, size_t row_bytes,
+                                int hidden_size, int input_size);
+
+/* MLA latent absorption over kv_b [n_heads * (qk_nope + v_head), kv_lora] (kernel.cuh:300-305, 328-330):
+ *   q_nope:     q_abs[h, l] = sum_{d < qk_nope} W[h*(qk_nope+v_head) + d, l] * q[h*(qk_nope+qk_rope) + d]
+ *   xsum_delta: (Q4_K kv_b) delta[h, b] = sum_{d < qk_nope} q[h, d] * (-dmin * m) of 32-block b of row
+ *               h*(qk_nope+v_head) + d, for b < ceil(kv_lora / 32)
+ *   v:          attn[h, v] = sum_k W[h*(qk_nope+v_head) + qk_nope + v, k] * attn_latent[h*kv_lora + k],
+ *               plus, for Q4_K, sum_b (-dmin * m)(that row, b) * attn_xsum_delta[h, b]. */
+int qlin_launch_mla_absorb_q_nope(int type, const float *q, const uint8_t *kv_b_weight, size_t row_bytes,
+                                  float *q_abs, int n_heads, int qk_nope, int qk_rope, int v_head, int kv_lora);
+int qlin_launch_mla_absorb_q4_xsum_delta(const float *q, const uint8_t *kv_b_weight, size_t row_bytes,
+                                         float *q_abs_xsum_delta, int n_heads, int qk_nope, int qk_rope,
+                                         int v_head, int kv_lora);
+int qlin_launch_mla_absorb_v(int type, const uint8_t *kv_b_weight, size_t row_bytes, const float *attn_latent,
+                             const float *attn_xsum_delta, float *attn, int n_heads, int qk_nope, int v_head,
+                             int kv_lora);
+
 #ifdef __cplusplus
 }
 #endif

@@ -124,4 +124,34 @@ inline void launch_dequantize_q6k_to_f16(const uint8_t *src, uint16_t *out, int6
     check(qlin_launch_dequantize_q6k_to_f16(src, out, n), "launch_dequantize_q6k_to_f16");
 }
 
+// kernel.cuh:141-142
+inline void launch_quant_embedding(DType quant_type, const int *input, float *output, const uint8_t *table,
+                                   size_t row_bytes, int hidden_size, int input_size) {
+    check(qlin_launch_quant_embedding(static_cast<int>(quant_type), input, output, table, row_bytes, hidden_size,
+                                      input_size),
+          "launch_quant_embedding");
+}
+
+// kernel.cuh:300-305, 328-330
+inline void launch_mla_absorb_q_nope(DType quant_type, const float *q, const uint8_t *kv_b_weight, size_t row_bytes,
+                                     float *q_abs, int n_heads, int qk_nope, int qk_rope, int v_head, int kv_lora) {
+    check(qlin_launch_mla_absorb_q_nope(static_cast<int>(quant_type), q, kv_b_weight, row_bytes, q_abs, n_heads,
+                                        qk_nope, qk_rope, v_head, kv_lora),
+          "launch_mla_absorb_q_nope");
+}
+inline void launch_mla_absorb_q4_xsum_delta(const float *q, const uint8_t *kv_b_weight, size_t row_bytes,
+                                            float *q_abs_xsum_delta, int n_heads, int qk_nope, int qk_rope,
+                                            int v_head, int kv_lora) {
+    check(qlin_launch_mla_absorb_q4_xsum_delta(q, kv_b_weight, row_bytes, q_abs_xsum_delta, n_heads, qk_nope,
+                                               qk_rope, v_head, kv_lora),
+          "launch_mla_absorb_q4_xsum_delta");
+}
+inline void launch_mla_absorb_v(DType quant_type, const uint8_t *kv_b_weight, size_t row_bytes,
+                                const float *attn_latent, const float *attn_xsum_delta, float *attn, int n_heads,
+                                int qk_nope, int v_head, int kv_lora) {
+    check(qlin_launch_mla_absorb_v(static_cast<int>(quant_type), kv_b_weight, row_bytes, attn_latent, attn_xsum_delta,
+                                   attn, n_heads, qk_nope, v_head, kv_lora),
+          "launch_mla_absorb_v");
+}
+
 }  // namespace qlin_ref

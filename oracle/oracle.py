@@ -67,6 +67,10 @@ def _declare(L: C.CDLL) -> None:
         "orc_swiglu_indexed": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
         "orc_down_indexed_ordered": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
         "orc_argmax": (I, [P, I]),
+        "orc_quant_embedding": (I, [I, P, I, P, SZ, I, P]),
+        "orc_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
+        "orc_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),
+        "orc_mla_absorb_v": (I, [I, P, SZ, P, P, P, I, I, I, I]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -220,3 +224,35 @@ def down_indexed_ordered(qtype, wd, d_eb, d_rb, act, expert_ids, route_w, out, h
 def argmax(v: np.ndarray) -> int:
     v = np.ascontiguousarray(v, dtype=np.float32)
     return int(lib().orc_argmax(_p(v), v.size))
+
+
+def quant_embedding(qtype: int, ids: np.ndarray, table: np.ndarray, rb: int, hidden: int) -> np.ndarray:
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.zeros((len(ids), hidden), np.float32)
+    _ok(lib().orc_quant_embedding(qtype, _p(ids), len(ids), _p(table), rb, hidden, _p(out)), "orc_quant_embedding")
+    return out
+
+
+def mla_absorb_q_nope(qtype, q, w, rb, n_heads, qk_nope, qk_rope, v_head, kv_lora) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.zeros(n_heads * kv_lora, np.float64)
+    _ok(lib().orc_mla_absorb_q_nope(qtype, _p(q), _p(w), rb, _p(out), n_heads, qk_nope, qk_rope, v_head, kv_lora),
+        "orc_mla_absorb_q_nope")
+    return out
+
+
+def mla_absorb_q4_xsum_delta(q, w, rb, n_heads, qk_nope, qk_rope, v_head, kv_lora) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.zeros(n_heads * ((kv_lora + 31) // 32), np.float64)
+    _ok(lib().orc_mla_absorb_q4_xsum_delta(_p(q), _p(w), rb, _p(out), n_heads, qk_nope, qk_rope, v_head, kv_lora),
+        "orc_mla_absorb_q4_xsum_delta")
+    return out
+
+
+def mla_absorb_v(qtype, w, rb, latent, delta, n_heads, qk_nope, v_head, kv_lora) -> np.ndarray:
+    latent = np.ascontiguousarray(latent, np.float32)
+    delta = np.ascontiguousarray(delta if delta is not None else np.zeros(1), np.float32)
+    out = np.zeros(n_heads * v_head, np.float64)
+    _ok(lib().orc_mla_absorb_v(qtype, _p(w), rb, _p(latent), _p(delta), _p(out), n_heads, qk_nope, v_head, kv_lora),
+        "orc_mla_absorb_v")
+    return out

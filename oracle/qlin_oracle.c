@@ -539,6 +539,79 @@ int orc_down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_bytes,
     return 0;
 }
 
+/* kernel.cu:2678-2693 (quant_embedding_kernel): out[t, :] = the dequantized row ids[t]. */
+int orc_quant_embedding(int type, const int *ids, int n, const uint8_t *table, size_t row_bytes, int hidden,
+                        float *out) {
+    if (check_shape(type, hidden)) return -1;
+    for (int t = 0; t < n; ++t)
+        if (deq_row(type, table + (size_t)ids[t] * row_bytes, hidden, out + (size_t)t * hidden)) return -1;
+    return 0;
+}
+
+/* kernel.cu:3018-3045 (mla_absorb_q_nope_kernel), in double: the head's first qk_nope kv_b rows,
+ * column l, against q[h, :qk_nope]. */
+int orc_mla_absorb_q_nope(int type, const float *q, const uint8_t *w, size_t row_bytes, double *q_abs, int n_heads,
+                          int qk_nope, int qk_rope, int v_head, int kv_lora) {
+    if (check_shape(type, kv_lora)) return -1;
+    float *row = (float *)malloc(sizeof(float) * (size_t)kv_lora);
+    if (!row) return -1;
+    for (int i = 0; i < n_heads * kv_lora; ++i) q_abs[i] = 0.0;
+    for (int h = 0; h < n_heads; ++h)
+        for (int d = 0; d < qk_nope; ++d) {
+            deq_row(type, w + ((size_t)h * (qk_nope + v_head) + d) * row_bytes, kv_lora, row);
+            const double qv = q[(size_t)h * (qk_nope + qk_rope) + d];
+            for (int l = 0; l < kv_lora; ++l) q_abs[(size_t)h * kv_lora + l] += (double)row[l] * qv;
+        }
+    free(row);
+    return 0;
+}
+
+/* -dmin * m of 32-block b of a Q4_K row, in f32 as kernel.cu:3004-3014 (q4k_min_coeff_at) forms it. */
+static float q4k_min_coeff(const uint8_t *row, int b) {
+    const uint8_t *sb = row + (size_t)(b >> 3) * 144;
+    int sc, m;
+    orc_q4k_scale_min(b & 7, sb + 4, &sc, &m);
+    return -(orc_f16_to_f32(rd16(sb + 2)) * (float)m);
+}
+
+/* kernel.cu:3052-3075 (mla_absorb_q4_xsum_delta_kernel), Q4_K kv_b, in double. */
+int orc_mla_absorb_q4_xsum_delta(const float *q, const uint8_t *w, size_t row_bytes, double *out, int n_heads,
+                                 int qk_nope, int qk_rope, int v_head, int kv_lora) {
+    if (check_shape(ORC_Q4_K, kv_lora)) return -1;
+    const int nblk = (kv_lora + 31) / 32;
+    for (int h = 0; h < n_heads; ++h)
+        for (int b = 0; b < nblk; ++b) {
+            double acc = 0.0;
+            for (int d = 0; d < qk_nope; ++d)
+                acc += (double)q[(size_t)h * (qk_nope + qk_rope) + d] *
+                       (double)q4k_min_coeff(w + ((size_t)h * (qk_nope + v_head) + d) * row_bytes, b);
+            out[(size_t)h * nblk + b] = acc;
+        }
+    return 0;
+}
+
+/* kernel.cu:3417-3453 (mla_absorb_v_kernel), in double: the head's v rows (after its qk_nope rows)
+ * against attn_latent[h, :]; Q4_K adds sum_b (-dmin * m)(row, b) * xsum_delta[h, b]. */
+int orc_mla_absorb_v(int type, const uint8_t *w, size_t row_bytes, const float *latent, const float *delta,
+                     double *attn, int n_heads, int qk_nope, int v_head, int kv_lora) {
+    if (check_shape(type, kv_lora)) return -1;
+    float *row = (float *)malloc(sizeof(float) * (size_t)kv_lora);
+    if (!row) return -1;
+    const int nblk = (kv_lora + 31) / 32;
+    for (int h = 0; h < n_heads; ++h)
+        for (int v = 0; v < v_head; ++v) {
+            const uint8_t *r = w + ((size_t)h * (qk_nope + v_head) + qk_nope + v) * row_bytes;
+            deq_row(type, r, kv_lora, row);
+            double acc = 0.0;
+            for (int k = 0; k < kv_lora; ++k) acc += (double)row[k] * (double)latent[(size_t)h * kv_lora + k];
+            if (type == ORC_Q4_K)
+                for (int b = 0; b < nblk; ++b) acc += (double)q4k_min_coeff(r, b) * (double)delta[(size_t)h * nblk + b];
+            attn[(size_t)h * v_head + v] = acc;
+        }
+    free(row);
+    return 0;
+}
+
 int orc_argmax(const float *v, int n) {
     float best = -INFINITY;
     int idx = 0;

@@ -15,6 +15,9 @@
  *   MoE            kernel.cu:1289-1385 (quant_swiglu[_indexed]_kernel),
  *                  2253-2287 (quant_down_f32_indexed_accum_ordered_kernel),
  *                  3463-3511 (moe_router_topk_kernel), 3531-3592 (argmax, lowest index on ties)
+ *   embedding, MLA kernel.cu:2678-2693 (quant_embedding_kernel), 3004-3075 (q4k_min_coeff_at,
+ *                  mla_absorb_q_nope_kernel, mla_absorb_q4_xsum_delta_kernel), 3417-3453
+ *                  (mla_absorb_v_kernel)
  *   block traits   src/format/gguf/GgufFile.cpp:35-55; dtype codes src/tensor/TensorCommon.h:15-33
  *   Q4_0           not implemented by the reference (trait only, GgufFile.cpp:40); restated from
  *                  the published ggml block_q4_0 format (d f16, 16 bytes of split-half nibbles,
@@ -31,6 +34,9 @@
  *   GEMV / matmul   double-precision truth against closed forms, linearity, and f32 orders.
  *   router, SwiGLU, brute force on tiny inputs, the tie (lowest index) and NaN rules, numpy.
  *   down-accumulate
+ *   embedding, MLA  the dequantized rows (pinned above) against numpy restatements of each sum
+ *                   (transposed per-head products, the -dmin*m block coefficients from the scale
+ *                   bytes); no reference test covers these kernels.
  *   Q5_0            parity unpinned: the reference has the codec (kernel.cu:1159-1175) but no test;
  *                   checked only against that formula as read and an independent encoder.
  *   Q4_0            parity unpinned: the reference has no implementation; checked only against the
@@ -131,6 +137,16 @@ int orc_down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_bytes,
 
 /* Index of the maximum, lowest index on ties (kernel.cu:3531-3592). */
 int orc_argmax(const float *v, int n);
+
+/* Embedding rows and MLA absorption (kernel.cu:2678-2693, 3004-3075, 3417-3453), sums in double. */
+int orc_quant_embedding(int type, const int *ids, int n, const uint8_t *table, size_t row_bytes, int hidden,
+                        float *out);
+int orc_mla_absorb_q_nope(int type, const float *q, const uint8_t *w, size_t row_bytes, double *q_abs, int n_heads,
+                          int qk_nope, int qk_rope, int v_head, int kv_lora);
+int orc_mla_absorb_q4_xsum_delta(const float *q, const uint8_t *w, size_t row_bytes, double *out, int n_heads,
+                                 int qk_nope, int qk_rope, int v_head, int kv_lora);
+int orc_mla_absorb_v(int type, const uint8_t *w, size_t row_bytes, const float *latent, const float *delta,
+                     double *attn, int n_heads, int qk_nope, int v_head, int kv_lora);
 
 #ifdef __cplusplus
 }

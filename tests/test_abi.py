@@ -178,6 +178,30 @@ def test_swiglu_and_down_validation():
                        FAKE, 2, 1, 33) == SHAPE
 
 
+def test_embedding_and_mla_validation():
+    """Types and shapes the reference's launchers take (launch.cu:561-579, 920-962, 1061-1080); others
+    are statuses, and empty work returns before any launch."""
+    E = "qlin_launch_quant_embedding"
+    assert qlin.status(E, 2, FAKE, FAKE, FAKE, 18, 32, 4) == UNSUP          # Q4_0: not a reference case
+    assert qlin.status(E, 12, FAKE, FAKE, FAKE, 144, 100, 4) == SHAPE      # hidden not whole super-blocks
+    assert qlin.status(E, 12, FAKE, FAKE, FAKE, 143, 256, 4) == ROWB
+    assert qlin.status(E, 12, 0, FAKE, FAKE, 144, 256, 4) == NULL
+    assert qlin.status(E, 12, FAKE + 2, FAKE, FAKE, 144, 256, 4) == ALIGN
+    assert qlin.status(E, 12, 0, 0, 0, 144, 256, 0) == OK
+    Q = "qlin_launch_mla_absorb_q_nope"
+    assert qlin.status(Q, 2, FAKE, FAKE, 18, FAKE, 16, 128, 64, 128, 512) == UNSUP
+    assert qlin.status(Q, 12, FAKE, FAKE, 144, FAKE, 16, 128, 64, 128, 500) == SHAPE
+    assert qlin.status(Q, 12, FAKE, FAKE, 287, FAKE, 16, 128, 64, 128, 512) == ROWB
+    assert qlin.status(Q, 12, FAKE, 0, 288, FAKE, 16, 128, 64, 128, 512) == NULL
+    assert qlin.status(Q, 12, 0, 0, 288, 0, 0, 128, 64, 128, 512) == OK
+    D = "qlin_launch_mla_absorb_q4_xsum_delta"
+    assert qlin.status(D, FAKE, FAKE, 288, FAKE, 16, -1, 64, 128, 512) == SHAPE
+    assert qlin.status(D, FAKE, FAKE, 288, 0, 16, 128, 64, 128, 512) == NULL
+    V = "qlin_launch_mla_absorb_v"
+    assert qlin.status(V, 12, FAKE, 288, FAKE, 0, FAKE, 16, 128, 128, 512) == NULL   # Q4_K needs the deltas
+    assert qlin.status(V, 14, FAKE, 420, FAKE, 0, FAKE, 16, 128, 0, 512) == OK
+
+
 def test_cpp_shim_compiles():
     """The C++ shim with the reference's launcher names builds against the C ABI."""
     gxx = shutil.which("g++")
