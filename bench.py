@@ -468,14 +468,19 @@ def wl_c4(args, torch, qlin, gen):
 
 
 def wl_c5(args, torch, qlin, gen):
-    """C5: DeepSeek-V2-Lite routed experts for 16 decode tokens -- 64 experts of Q4_K gate/up
-    [1408, 2048] and Q5_0 down [2048, 1408], router logits N(0,1), top-6 with scaling 1.0.  A step is
-    the router and the grouped routed decode (the 2 shared experts are not part of this step)."""
+    """C5: a DeepSeek-V2-Lite MoE FFN layer for 16 decode tokens -- 64 routed experts of Q4_K gate/up
+    [1408, 2048] and Q5_0 down [2048, 1408], router logits N(0,1), top-6 with scaling 1.0, plus the 2
+    shared experts (Q4_K gate/up [2816, 2048], Q4_K down [2048, 2816]).  A step is the router, the
+    grouped routed decode and the shared experts (MoE.cpp:29-52 after the norm): the batched SwiGLU
+    over the 16 tokens, then the batched down projection added into the same output."""
     E, ffn, hid, tokens, k = 64, 1408, 2048, 16, 6
+    sffn = 2816
     Q5_0 = 6
-    copies = 4  # 4 x 329 MB of expert weights rotate through the step
+    copies = 4  # 4 x 339 MB of expert weights rotate through the step
     mats = [(synth_blocks(torch, Q4_K, E * ffn, hid, gen), synth_blocks(torch, Q4_K, E * ffn, hid, gen),
-             synth_blocks(torch, Q5_0, E * hid, ffn, gen)) for _ in range(copies)]
+             synth_blocks(torch, Q5_0, E * hid, ffn, gen), synth_blocks(torch, Q4_K, sffn, hid, gen),
+             synth_blocks(torch, Q4_K, sffn, hid, gen), synth_blocks(torch, Q4_K, hid, sffn, gen))
+            for _ in range(copies)]
     x = torch.randn(tokens, hid, device="cuda", generator=gen)
     logits = torch.randn(tokens, E, device="cuda", generator=gen)
     ids = torch.empty(tokens, k, dtype=torch.int32, device="cuda")
@@ -485,42 +490,52 @@ def wl_c5(args, torch, qlin, gen):
     ws = torch.empty(nws + 256, dtype=torch.uint8, device="cuda")
     wsp = (ws.data_ptr() + 255) // 256 * 256
     act = torch.empty(k, ffn, device="cuda")
+    sact = torch.empty(sffn, device="cuda")
+    sacts = torch.empty(tokens, sffn, device="cuda")
     gub, db = mats[0][0].numel(), mats[0][2].numel()
+    s_rb, sd_rb = qlin.row_bytes(Q4_K, hid), qlin.row_bytes(Q4_K, sffn)
 
     def step_grouped():
-        for wg, wu, wd in mats:
+        for wg, wu, wd, sg, su, sd in mats:
             qlin.call("qlin_launch_moe_router_topk", logits, ids, rw, tokens, E, k, 1.0)
             qlin.call("qlin_moe_routed_decode_grouped", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, x, ids,
                       rw, wsp, nws, out, tokens, k)
+            qlin.call("qlin_launch_quant_swiglu_rows", Q4_K, sg, su, s_rb, s_rb, x, sacts, sffn, hid, tokens)
+            qlin.call("qlin_launch_quant_matmul_add", Q4_K, sd, sd_rb, sacts, out, hid, sffn, tokens)
 
     def step_per_token():
-        for wg, wu, wd in mats:
+        for wg, wu, wd, sg, su, sd in mats:
             qlin.call("qlin_launch_moe_router_topk", logits, ids, rw, tokens, E, k, 1.0)
             for t in range(tokens):
                 qlin.call("qlin_moe_routed_decode_indexed", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid,
                           x[t], ids[t], rw[t], act, out[t], k)
+                qlin.call("qlin_launch_quant_swiglu", Q4_K, sg, su, s_rb, s_rb, x[t], sact, sffn, hid)
+                qlin.call("qlin_launch_quant_gemv_add", Q4_K, sd, sd_rb, sact, out[t], hid, sffn)
 
     reps = max(1, args.steps // 20)
     us = graph_us(torch, qlin, step_grouped, reps) / copies
     us_tok = graph_us(torch, qlin, step_per_token, max(1, reps // 4)) / copies
     distinct = int(torch.unique(ids[ids >= 0]).numel())
     per_expert = 2 * ffn * qlin.row_bytes(Q4_K, hid) + hid * qlin.row_bytes(Q5_0, ffn)
-    nbytes = distinct * per_expert + 4 * tokens * (hid + hid) + 4 * tokens * E
+    shared = 2 * sffn * s_rb + hid * sd_rb
+    nbytes = distinct * per_expert + shared + 4 * tokens * (hid + hid) + 4 * tokens * E
     log(f"c5: grouped {us:.2f} us/step, per-token facade {us_tok:.2f} us, {distinct} distinct experts")
     return {
-        "metric": "MoE routed decode HBM GB/s (DeepSeek-V2-Lite shape, 16 tokens, top-6 of 64)",
+        "metric": "MoE layer decode HBM GB/s (DeepSeek-V2-Lite shape, 16 tokens, top-6 of 64 + 2 shared)",
         "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / 8000, 2),
         "n_gpus": 1, "steps": reps * copies, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (random Q4_K / Q5_0 expert blocks, f32 N(0,1) x and router logits), 4 weight copies",
         "config": {"workload": "c5-moe-grouped", "experts": E, "ffn": ffn, "hidden": hid, "tokens": tokens,
-                   "top_k": k, "gate_up": "Q4_K", "down": "Q5_0", "distinct_experts": distinct,
-                   "algorithmic_bytes_per_step": nbytes,
-                   "launches_per_step": "router_topk + moe_routed_decode_grouped (group, gate/up, down, combine)",
+                   "top_k": k, "gate_up": "Q4_K", "down": "Q5_0", "shared_ffn": sffn, "shared": "Q4_K",
+                   "distinct_experts": distinct, "algorithmic_bytes_per_step": nbytes,
+                   "launches_per_step": "router_topk + moe_routed_decode_grouped (group, gate/up, down, "
+                                        "combine) + quant_swiglu_rows + quant_matmul_add (shared experts)",
                    "per_token_facade_us_per_step": round(us_tok, 2), "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(nbytes / us / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "whole step (router_kernel, group_kernel, stream_kernel<Q4_K> gate/up, stream_kernel<Q5_0> down, combine_kernel)",
+                     "kernel": "whole step (router_kernel, group_kernel, stream_kernel<Q4_K> gate/up, "
+                               "stream_kernel<Q5_0> down, combine_kernel, q4k_dense_kernel SwiGLU and add)",
                      "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": nbytes},
     }
 

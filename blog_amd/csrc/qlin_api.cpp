@@ -150,6 +150,11 @@ int qlin_launch_quant_matmul(int type, const uint8_t *w, size_t rb, const float 
     return gemv_common(type, w, rb, x, y, out_dim, in_dim, m, false);
 }
 
+int qlin_launch_quant_matmul_add(int type, const uint8_t *w, size_t rb, const float *x, float *y, int out_dim,
+                                 int in_dim, int m) {
+    return gemv_common(type, w, rb, x, y, out_dim, in_dim, m, true);
+}
+
 int qlin_launch_quant_gemv_multi(int type, int n_mats, const uint8_t *const *weights, size_t rb, const float *x,
                                  float *const *ys, const int *out_dims, int in_dim) {
     if (n_mats < 0) return QLIN_ERR_SHAPE;
@@ -203,6 +208,24 @@ int qlin_launch_quant_swiglu(int type, const uint8_t *wg, const uint8_t *wu, siz
     if ((rc = check_f32(x, work)) || (rc = check_f32(act, work))) return rc;
     if (!work) return QLIN_OK;
     return launched(qlin::swiglu(type, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim, stream()));
+}
+
+int qlin_launch_quant_swiglu_rows(int type, const uint8_t *wg, const uint8_t *wu, size_t g_rb, size_t u_rb,
+                                  const float *x, float *act, int ffn_dim, int in_dim, int m) {
+    int rc = check_weight(type, wg, g_rb, ffn_dim, in_dim);
+    if (rc || (rc = check_weight(type, wu, u_rb, ffn_dim, in_dim))) return rc;
+    if (m < 0) return QLIN_ERR_SHAPE;
+    const bool work = ffn_dim > 0 && m > 0;
+    if ((rc = check_f32(x, work)) || (rc = check_f32(act, work))) return rc;
+    if (!work) return QLIN_OK;
+    if (m > 1 && g_rb == u_rb && qlin::dense_ok(type, wg, wu, g_rb, x, in_dim))
+        return launched(qlin::dense_matmul(type, wg, wu, g_rb, x, act, ffn_dim, in_dim, m, 2, stream()));
+    for (int r = 0; r < m; ++r) {
+        const hipError_t e = qlin::swiglu(type, wg, wu, g_rb, u_rb, x + static_cast<size_t>(r) * in_dim,
+                                          act + static_cast<size_t>(r) * ffn_dim, ffn_dim, in_dim, stream());
+        if (e != hipSuccess) return launched(e);
+    }
+    return QLIN_OK;
 }
 
 int qlin_launch_quant_swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb,

@@ -1,0 +1,169 @@
+// qlin_dense.hip -- quantized matmul over a few rows of f32 activations on the f32 matrix cores, gfx950.
+//
+//   y[r, o] = sum_k w(o, k) * x[r, k]          (kernel.cu:1254-1279, quant_matmul_kernel; m > 1)
+//   y[r, o] += ...                              (the gemm + add of SharedExperts.cpp:42-48)
+//   act[r, o] = g / (1 + expf(-g)) * u,  g, u the rows of the gate and up matrices
+//                                               (the gemm, gemm, silu_mul of SharedExperts.cpp:34-40)
+//
+// w(o, k) is the canonical dequantized f32 element (the bit-exact decode of kernel.cu:913-930), and
+// the products w * x are summed in f32 by v_mfma_f32_16x16x4_f32: the contraction the reference runs
+// one warp per (r, o), with the same f32 operands and only the summation order changed.
+//
+// Layout.  A workgroup owns a tile of 16 output rows and all of K; its 8 waves take the 256-element
+// super-blocks of K in turn (wave w: w, w + 8, ...).  Lane l supplies output row l % 16 and token
+// l % 16 of the current 16-token tile, and k-slot g = l / 16 of each MFMA: the 8 MFMAs of 32-element
+// sub-block j cover its elements 8g .. 8g+7 in slot g, so a lane reads 8 consecutive weights and 8
+// consecutive activations per sub-block.  D holds tokens 4g .. 4g+3 of row l % 16.  The waves'
+// partials meet in LDS and are summed in wave order.  A grid row per 64 tokens.
+#include "qlin_device.hpp"
+#include "qlin_internal.hpp"
+#include "qlin_mfma.hpp"
+
+namespace qlin {
+namespace {
+
+constexpr int kDWaves = 8, kDThreads = kDWaves * 64;
+constexpr int kDTokens = 64;  // tokens per grid row (4 tiles of 16)
+
+enum : int { kStore = 0, kAdd = 1, kSwiGLU = 2 };
+
+struct DenseArgs {
+    const uint8_t *w0, *w1;  // w1: the up matrix of kSwiGLU
+    size_t rb;
+    const float *x;
+    float *y;
+    int n, k, m;
+};
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// The raw bytes a lane needs of one Q4_K super-block: the header (d, dmin, 12 scale bytes) and,
+// for each pair c of sub-blocks, qs bytes 32c + 8g .. 32c + 8g + 7 (low nibbles: sub-block 2c,
+// high nibbles: sub-block 2c + 1).
+struct Q4KRaw {
+    u32x4 h;
+    uint32_t q[8];
+};
+
+__device__ __forceinline__ void load_q4k(Q4KRaw &r, const uint8_t *sb, int g) {
+    r.h = ld16(sb);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(sb + 16 + 32 * c + 8 * g);
+        r.q[2 * c] = v.x;
+        r.q[2 * c + 1] = v.y;
+    }
+}
+
+// Elements 8g .. 8g+7 of sub-block j, canonical values (d * sc) * q - dmin * m.
+__device__ __forceinline__ void q4k_values(const Q4KRaw &r, int j, float (&v)[8]) {
+    int sc, mn;
+    q4k_scale_min(j, r.h.y, r.h.z, r.h.w, sc, mn);
+    const float d = f16_bits_to_f32(r.h.x & 0xffffu), dmin = f16_bits_to_f32(r.h.x >> 16);
+    const float dsc = mul_rn(d, static_cast<float>(sc)), dm = mul_rn(dmin, static_cast<float>(mn));
+    const int sh = 4 * (j & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t q = (r.q[2 * (j >> 1) + (i >> 2)] >> (8 * (i & 3) + sh)) & 15u;
+        v[i] = sub_rn(mul_rn(dsc, static_cast<float>(q)), dm);
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a) {
+    constexpr int NW = MODE == kSwiGLU ? 2 : 1;
+    __shared__ f32x4 part[kDWaves][NW][4][64];  // [wave][matrix][token tile][lane]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int K = a.k, nsb = K / 256;
+    const int row0 = blockIdx.x * 16;
+    const int row = min(row0 + n, a.n - 1);
+    const int t0 = blockIdx.y * kDTokens;
+    const int ntt = min(4, (a.m - t0 + 15) / 16);  // token tiles of this grid row
+    const uint8_t *rp[2] = {a.w0 + static_cast<size_t>(row) * a.rb, a.w1 + static_cast<size_t>(row) * a.rb};
+
+    f32x4 D[NW][4];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) D[w][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int sb = wave; sb < nsb; sb += kDWaves) {
+        Q4KRaw raw[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) load_q4k(raw[w], rp[w] + static_cast<size_t>(sb) * 144, g);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            if (tt >= ntt) break;  // uniform
+            // token of this lane's A row (tokens past m read the last one; their D rows are dropped)
+            const int tok = min(t0 + tt * 16 + n, a.m - 1);
+            const float *xr = a.x + static_cast<size_t>(tok) * K + sb * 256 + 8 * g;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 x0 = *reinterpret_cast<const float4 *>(xr + 32 * j);
+                const float4 x1 = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    float v[8];
+                    q4k_values(raw[w], j, v);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) D[w][tt] = mfma_f32(xv[i], v[i], D[w][tt]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+            if (tt < ntt) part[wave][w][tt][lane] = D[w][tt];
+    __syncthreads();
+
+    // outputs: row o = row0 + (i % 16), token t0 + i / 16; D element r of lane l is token 4(l/16) + r
+    const int rows = min(16, a.n - row0);
+    for (int i = tid; i < ntt * 256; i += kDThreads) {
+        const int tl = i >> 4, o = i & 15;  // token within the grid row, row within the tile
+        const int t = t0 + tl;
+        if (o >= rows || t >= a.m) continue;
+        const int tt = tl >> 4, l = ((tl & 15) >> 2) * 16 + o, r = tl & 3;
+        float v0 = 0.0f, v1 = 0.0f;
+        for (int wv = 0; wv < kDWaves; ++wv) {
+            v0 += part[wv][0][tt][l][r];
+            if constexpr (NW == 2) v1 += part[wv][NW - 1][tt][l][r];
+        }
+        float *yo = a.y + static_cast<size_t>(t) * a.n + row0 + o;
+        if constexpr (MODE == kSwiGLU) *yo = v0 / (1.0f + expf(-v0)) * v1;
+        else if constexpr (MODE == kAdd) *yo += v0;
+        else *yo = v0;
+    }
+}
+
+}  // namespace
+
+bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t rb, const float *x, int k) {
+    const auto al = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+    if (type != T_Q4_K) return false;
+    return k % 256 == 0 && rb % 16 == 0 && al(w0, 16) && (!w1 || al(w1, 16)) && al(x, 16);
+}
+
+hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t rb, const float *x, float *y, int n,
+                        int k, int m, int mode, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    if (type != T_Q4_K) return hipErrorInvalidValue;
+    const DenseArgs a{w0, w1 ? w1 : w0, rb, x, y, n, k, m};
+    const dim3 grid((n + 15) / 16, (m + kDTokens - 1) / kDTokens);
+    switch (mode) {
+        case kStore: hipLaunchKernelGGL(q4k_dense_kernel<kStore>, grid, dim3(kDThreads), 0, s, a); break;
+        case kAdd: hipLaunchKernelGGL(q4k_dense_kernel<kAdd>, grid, dim3(kDThreads), 0, s, a); break;
+        case kSwiGLU: hipLaunchKernelGGL(q4k_dense_kernel<kSwiGLU>, grid, dim3(kDThreads), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace qlin

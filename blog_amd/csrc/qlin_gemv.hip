@@ -4,9 +4,10 @@
 // reference's quant_gemv_kernel / quant_gemv_add_kernel (AI/codes/local-llm/src/backend/cuda/ops/
 // kernel.cu:1192-1244).  The summation order is ours (results agree within fp32 rounding).
 //
-// Q4_K with m == 1 and 16-byte aligned operands goes to the persistent streaming kernel
-// (qlin_q4k_stream.hip); everything else takes the generic per-element kernel below, which
-// decodes each weight with the reference's per-element formula.
+// m == 1 goes to the matrix-core decode kernels (qlin_mfma_gemv.hip) or the streaming Q4_K kernel
+// (qlin_q4k_stream.hip), Q4_K with m > 1 to the f32 matrix-core kernel (qlin_dense.hip); everything
+// else takes the generic per-element kernel below, which decodes each weight with the reference's
+// per-element formula.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 
@@ -85,6 +86,7 @@ hipError_t gemv(int type, const uint8_t *w, size_t rb, const float *x, float *y,
         return mfma_gemv(type, &w, &y, &n, 1, rb, x, k, add, s);
     if (type == T_Q4_K && m == 1 && q4k_stream_ok(&w, 1, rb, x, n, k, false))
         return q4k_stream_gemv(&w, &y, &n, 1, rb, x, k, add, s);
+    if (m > 1 && dense_ok(type, w, nullptr, rb, x, k)) return dense_matmul(type, w, nullptr, rb, x, y, n, k, m, add, s);
     return gemv_generic(type, w, rb, x, y, n, k, m, add, s);
 }
 

@@ -14,7 +14,7 @@ struct DeviceInfo {
 };
 const DeviceInfo &device_info();
 
-// y[r, o] (=|+=) sum_k W[o, k] x[r, k] for r < m.  add => y += (m must be 1 for add).
+// y[r, o] (=|+=) sum_k W[o, k] x[r, k] for r < m.
 hipError_t gemv(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y, int out_dim,
                 int in_dim, int m, bool add, hipStream_t s);
 
@@ -38,6 +38,12 @@ hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const i
                      size_t row_bytes, const float *x, int in_dim, bool add, hipStream_t s);
 hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
                        int ffn_dim, int in_dim, hipStream_t s);
+
+// Q4_K over m > 1 rows of f32 activations on the f32 matrix cores (qlin_dense.hip): mode 0 stores
+// y[r, o], 1 adds into it, 2 writes act[r, o] = silu(gate . x_r) * (up . x_r) with w1 the up matrix.
+bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, const float *x, int in_dim);
+hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, const float *x, float *y,
+                        int out_dim, int in_dim, int m, int mode, hipStream_t s);
 
 // The per-element fallback used for any type / alignment (exposed for tests of the fast paths).
 hipError_t gemv_generic(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,

@@ -172,17 +172,19 @@ __device__ __forceinline__ int64_t tile_cost(int cnt) {
     return static_cast<int64_t>((cnt + NQ - 1) / NQ) * StepFmt<FMT>::w0 + static_cast<int64_t>(cnt) * StepFmt<FMT>::w1;
 }
 
-template <int FMT, int NQ>
+// SW: gate and up matrices with SiLU(gate) * up out (Q4_K); otherwise one matrix, its dot out.
+template <int FMT, int NQ, bool SW>
 __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     using F = StepFmt<FMT>;
-    constexpr bool UP = FMT == T_Q4_K;
-    constexpr int NW = UP ? 2 : 1;  // matrices per output row (gate, up)
+    constexpr bool K4 = FMT == T_Q4_K;  // super-block steps, block-diagonal A
+    constexpr int NW = SW ? 2 : 1;      // matrices per output row (gate, up)
+    static_assert(!SW || K4, "the SwiGLU pair is Q4_K");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int K = a.K, nblk = K / 32, nchunk = a.nchunk;
     // staging of the pass's routes: Q4_K bf16 planes [NQ][2][K]; others slot vectors
     // [NQ][2][nblk][tpb] (8 bf16 each); then the block sums X [NQ][nblk] and the step partials
     // [NW][NQ][nchunk][rows of the piece]
-    const size_t stage_bytes = UP ? static_cast<size_t>(NQ) * 4 * K : static_cast<size_t>(NQ) * 2 * nblk * F::tpb * 16;
+    const size_t stage_bytes = K4 ? static_cast<size_t>(NQ) * 4 * K : static_cast<size_t>(NQ) * 2 * nblk * F::tpb * 16;
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);
     uint4 *slots = reinterpret_cast<uint4 *>(smem);
     float *xsum = reinterpret_cast<float *>(smem + stage_bytes);
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
         };
         auto load = [&](Raw &st, const Pos &p) {
             const uint8_t *q = p.rp + static_cast<size_t>(p.ch) * F::cb;
-            if constexpr (UP) {
+            if constexpr (K4) {
                 const u32x4 h = ld16(q), qa = ld16(q + 16 + 32 * g), qb = ld16(q + 32 + 32 * g);
                 st.w[0] = h.x; st.w[1] = h.y; st.w[2] = h.z; st.w[3] = h.w;
                 st.w[4] = qa.x; st.w[5] = qa.y; st.w[6] = qa.z; st.w[7] = qa.w;
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
         auto process = [&](const Raw &cur, const Pos &p, int nq) {
             float *pp = partial + (static_cast<size_t>(p.which) * NQ * nchunk + p.ch) * pstride + p.tile * 16 + n;
             const bool store = g == 0 && p.tile * 16 + n < nrows;
-            if constexpr (UP) {
+            if constexpr (K4) {
                 u32x4 B[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t) B[t] = weights_operand(cur.w[4 + t]);
@@ -395,7 +397,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             load(buf, cur);  // the first weights are requested before the activations are staged
 
             // stage the pass's routes (hi = bf16(x), lo = bf16(x - hi); X sums hi + lo)
-            if constexpr (UP) {
+            if constexpr (K4) {
                 const int per = K / 4;  // float4s per route, a multiple of 64: whole waves per route
                 for (int it = tid; it < nq * per; it += kSThreads) {
                     const int q = it / per, c = it - q * per;
@@ -482,10 +484,10 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                     float v0 = 0.0f, v1 = 0.0f;
                     for (int ch = 0; ch < nchunk; ++ch) {
                         v0 += pq[ch * pstride];
-                        if constexpr (UP) v1 += pq[(static_cast<size_t>(NQ) * nchunk + ch) * pstride];
+                        if constexpr (SW) v1 += pq[(static_cast<size_t>(NQ) * nchunk + ch) * pstride];
                     }
                     const int route = a.list[beg + q0 + q];
-                    a.out[static_cast<size_t>(route) * a.rows + r0 + lr] = UP ? v0 / (1.0f + expf(-v0)) * v1 : v0;
+                    a.out[static_cast<size_t>(route) * a.rows + r0 + lr] = SW ? v0 / (1.0f + expf(-v0)) * v1 : v0;
                 }
                 pt0 += a.piece;
                 if (pt0 >= lt1) break;
@@ -707,10 +709,10 @@ struct StreamPlan {
     size_t lds = 0;
 };
 
-template <int FMT>
+template <int FMT, bool SW>
 StreamPlan stream_plan(int rows, int K, int E, int R) {
     using F = StepFmt<FMT>;
-    constexpr int NW = FMT == T_Q4_K ? 2 : 1;
+    constexpr int NW = SW ? 2 : 1;
     constexpr size_t budget = kMaxLds - kStreamStaticLds;
     StreamPlan p;
     const int nblk = K / 32, nchunk = K / F::ce, tpe = (rows + 15) / 16;
@@ -733,17 +735,20 @@ StreamPlan stream_plan(int rows, int K, int E, int R) {
     return p;
 }
 
-template <int FMT>
+template <int FMT, bool SW>
 void launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
-    if (p.nq == 4) hipLaunchKernelGGL((stream_kernel<FMT, 4>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
-    else hipLaunchKernelGGL((stream_kernel<FMT, 2>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+    if (p.nq == 4) hipLaunchKernelGGL((stream_kernel<FMT, 4, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+    else hipLaunchKernelGGL((stream_kernel<FMT, 2, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
 }
 
-// The streaming down kernel reads 4-block chunks as aligned dwords (the chunk sizes 88 and 136
-// bytes are multiples of 4, so every chunk starts 4-aligned once the weights do).
-bool down_stream_ok(int type, const uint8_t *w, int ffn) {
+// The streaming down kernel reads Q5_0 / Q8_0 4-block chunks as aligned dwords (88 and 136 bytes,
+// multiples of 4, so every chunk starts 4-aligned once the weights do), and Q4_K super-blocks as
+// 16-byte pieces (144 bytes = 9 x 16).
+bool down_stream_ok(int type, const uint8_t *w, size_t eb, int ffn) {
+    const auto al = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+    if (type == T_Q4_K) return ffn % 256 == 0 && eb % 16 == 0 && al(w, 16);
     if (type != T_Q5_0 && type != T_Q8_0) return false;
-    return ffn % 128 == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0;
+    return ffn % 128 == 0 && al(w, 4);
 }
 
 }  // namespace
@@ -763,7 +768,7 @@ bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t eb
                        int ffn, int E, int R) {
     const auto al = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
     if (type != T_Q4_K || K % 256 || rb % 16 || eb % 16 || !al(wg, 16) || !al(wu, 16) || !al(x, 16)) return false;
-    return stream_plan<T_Q4_K>(ffn, K, E, R).ok || static_cast<size_t>(kGroup) * (4 * K + K / 8) <= kMaxLds;
+    return stream_plan<T_Q4_K, true>(ffn, K, E, R).ok || static_cast<size_t>(kGroup) * (4 * K + K / 8) <= kMaxLds;
 }
 
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
@@ -789,11 +794,11 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
 
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, ids, R, E, gr);
 
-    const StreamPlan up = stream_plan<T_Q4_K>(ffn, K, E, R);
+    const StreamPlan up = stream_plan<T_Q4_K, true>(ffn, K, E, R);
     if (up.ok) {
         const StreamArgs ua{wg,  wu,  g_eb, g_rb,   x,         k,          gr.list, gr.seg,
                             gr.nsel, act, ffn, K, K / 256, (ffn + 15) / 16, up.piece};
-        launch_stream<T_Q4_K>(up, ua, s);
+        launch_stream<T_Q4_K, true>(up, ua, s);
     } else {
         const UpArgs ua{wg, wu, g_eb, g_rb, x, gr, act, ffn, K, k};
         const size_t lds = static_cast<size_t>(kGroup) * (4 * K + K / 8);
@@ -801,15 +806,18 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
     }
 
     StreamPlan dn;
-    if (down_stream_ok(d_type, wd, ffn)) {
-        if (d_type == T_Q5_0) dn = stream_plan<T_Q5_0>(hidden, ffn, E, R);
-        else dn = stream_plan<T_Q8_0>(hidden, ffn, E, R);
+    if (down_stream_ok(d_type, wd, d_eb, ffn)) {
+        if (d_type == T_Q5_0) dn = stream_plan<T_Q5_0, false>(hidden, ffn, E, R);
+        else if (d_type == T_Q8_0) dn = stream_plan<T_Q8_0, false>(hidden, ffn, E, R);
+        else dn = stream_plan<T_Q4_K, false>(hidden, ffn, E, R);
     }
     if (dn.ok) {
-        const StreamArgs da{wd,      wd, d_eb,   d_rb, act,       1,                  gr.list, gr.seg,
-                            gr.nsel, yr, hidden, ffn, ffn / 128, (hidden + 15) / 16, dn.piece};
-        if (d_type == T_Q5_0) launch_stream<T_Q5_0>(dn, da, s);
-        else launch_stream<T_Q8_0>(dn, da, s);
+        const int nchunk = ffn / (d_type == T_Q4_K ? 256 : 128);
+        const StreamArgs da{wd,      wd, d_eb,   d_rb, act,    1,                  gr.list, gr.seg,
+                            gr.nsel, yr, hidden, ffn,  nchunk, (hidden + 15) / 16, dn.piece};
+        if (d_type == T_Q5_0) launch_stream<T_Q5_0, false>(dn, da, s);
+        else if (d_type == T_Q8_0) launch_stream<T_Q8_0, false>(dn, da, s);
+        else launch_stream<T_Q4_K, false>(dn, da, s);
     } else {
         const DownArgs da{wd, d_eb, d_rb, act, gr, yr, hidden, ffn};
         const dim3 dgrid(E, (hidden + 63) / 64);

@@ -40,6 +40,8 @@ SIGNATURES = {
     "qlin_launch_quant_gemv": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_launch_quant_gemv_add": (I, [I, P, SZ, P, P, I, I]),
     "qlin_launch_quant_matmul": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_matmul_add": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_swiglu_rows": (I, [I, P, P, SZ, SZ, P, P, I, I, I]),
     "qlin_launch_quant_gemv_multi": (I, [I, I, P, SZ, P, P, P, I]),
     "qlin_q8_1_row_bytes": (SZ, [I]),
     "qlin_launch_quantize_q8_1": (I, [P, P, I, I, I]),
@@ -178,6 +180,14 @@ def quant_swiglu(qtype, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim):
 
 def quant_matmul(qtype, w, rb, x, y, out_dim, in_dim, m):
     call("qlin_launch_quant_matmul", qtype, w, rb, x, y, out_dim, in_dim, m)
+
+
+def quant_matmul_add(qtype, w, rb, x, y, out_dim, in_dim, m):
+    call("qlin_launch_quant_matmul_add", qtype, w, rb, x, y, out_dim, in_dim, m)
+
+
+def quant_swiglu_rows(qtype, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim, m):
+    call("qlin_launch_quant_swiglu_rows", qtype, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim, m)
 
 
 def quantize_q8_1(x, xq, in_dim, m, store_raw_sum=False):

@@ -85,6 +85,12 @@ int qlin_launch_quant_gemv_add(int type, const uint8_t *weight, size_t row_bytes
 int qlin_launch_quant_matmul(int type, const uint8_t *weight, size_t row_bytes, const float *x, float *y,
                              int out_dim, int in_dim, int m);
 
+/* y[r, o] += sum_k W[o, k] x[r, k], r < m.  For m == 1 the same as qlin_launch_quant_gemv_add; for
+ * m > 1 it replaces the gemm into a scratch tensor followed by TensorTool::add that the shared
+ * experts run for a batch of tokens (SharedExperts.cpp:42-48). */
+int qlin_launch_quant_matmul_add(int type, const uint8_t *weight, size_t row_bytes, const float *x, float *y,
+                                 int out_dim, int in_dim, int m);
+
 /* n_mats (1..4) GEMVs that share x, as one launch: ys[i][o] = W_i[o] . x for o < out_dims[i].
  * weights, ys and out_dims are host arrays of n_mats entries (the pointers they hold are device
  * pointers); all weights have the same type, in_dim and row_bytes.  No reference counterpart: the
@@ -113,6 +119,13 @@ int qlin_launch_quant_matmul_q8_1(int type, const uint8_t *weight, size_t row_by
 int qlin_launch_quant_swiglu(int type, const uint8_t *gate_weight, const uint8_t *up_weight,
                              size_t gate_row_bytes, size_t up_row_bytes, const float *x, float *act,
                              int ffn_dim, int in_dim);
+
+/* act[r, o] = silu(Wg[o].x[r]) * (Wu[o].x[r]) for m rows of x ([m, in_dim]) into act ([m, ffn_dim]).
+ * For m == 1 the same as qlin_launch_quant_swiglu; for m > 1 it replaces the two gemms and silu_mul
+ * of the shared experts over a batch of tokens (SharedExperts.cpp:34-40). */
+int qlin_launch_quant_swiglu_rows(int type, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                  size_t gate_row_bytes, size_t up_row_bytes, const float *x, float *act,
+                                  int ffn_dim, int in_dim, int m);
 
 /* act[r, o] for route r on expert expert_ids[r] (device array; id < 0 writes 0).
  * Replaces launch_quant_swiglu_indexed (launch.cu:170-189). */

@@ -56,6 +56,19 @@ inline void launch_quant_matmul(DType t, const uint8_t *weight, size_t row_bytes
     check(qlin_launch_quant_matmul(static_cast<int>(t), weight, row_bytes, x, y, out_dim, in_dim, m),
           "launch_quant_matmul");
 }
+// The batched forms of launch_quant_gemv_add and launch_quant_swiglu (SharedExperts.cpp:34-48 for m > 1).
+inline void launch_quant_matmul_add(DType t, const uint8_t *weight, size_t row_bytes, const float *x, float *y,
+                                    int out_dim, int in_dim, int m) {
+    check(qlin_launch_quant_matmul_add(static_cast<int>(t), weight, row_bytes, x, y, out_dim, in_dim, m),
+          "launch_quant_matmul_add");
+}
+inline void launch_quant_swiglu_rows(DType t, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                     size_t gate_row_bytes, size_t up_row_bytes, const float *x, float *act,
+                                     int ffn_dim, int in_dim, int m) {
+    check(qlin_launch_quant_swiglu_rows(static_cast<int>(t), gate_weight, up_weight, gate_row_bytes, up_row_bytes,
+                                        x, act, ffn_dim, in_dim, m),
+          "launch_quant_swiglu_rows");
+}
 
 // No reference counterpart: q, k and v (or any matrices reading the same x) in one launch.
 inline void launch_quant_gemv_multi(DType t, int n_mats, const uint8_t *const *weights, size_t row_bytes,

@@ -151,6 +151,57 @@ def test_gemv_several_rows(qtype, m):
     assert normwise_rel_err(host(yd), ref) <= FP32
 
 
+@pytest.mark.parametrize("out_dim,in_dim,m", [(200, 1024, 2), (1000, 3584, 16), (2816, 2048, 17), (96, 256, 64),
+                                           (40, 4608, 65), (33, 512, 130)])
+def test_matmul_rows_f32_matrix_cores(out_dim, in_dim, m):
+    """Q4_K over m > 1 rows (launch_quant_matmul, kernel.cu:1254-1279): the f32 matrix-core kernel
+    with row tails (out_dim % 16), fewer and more super-blocks than waves (in_dim 256 .. 4608), and
+    token tails within and across 64-token grid rows."""
+    w, rb, vals = qgen.random_matrix(Q4_K, out_dim, in_dim, seed=out_dim + m)
+    x = qgen.random_x(m, in_dim, seed=m + 7)
+    banner(f"dense matmul n={out_dim} k={in_dim} m={m}")
+    yd = empty_f32(m, out_dim)
+    qlin.quant_matmul(Q4_K, dev(w), rb, dev(x), yd, out_dim, in_dim, m)
+    y = host(yd)
+    ref = orc.matmul_f64(Q4_K, w, rb, x, out_dim, in_dim)
+    assert normwise_rel_err(y, ref) <= FP32
+    assert cond_err(y, ref, vals, x) <= COND
+
+
+@pytest.mark.parametrize("qtype,m", [(Q4_K, 16), (Q4_K, 1), (Q8_0, 3)])
+def test_matmul_add_rows(qtype, m):
+    """y[r] += W x[r] for a batch (the shared experts' down projection added into the MoE output,
+    SharedExperts.cpp:42-48): each row equals the reference's gemv_add on that row."""
+    out_dim, in_dim = 2048, 2816 if qtype == Q4_K else 512
+    w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=41 + m)
+    x = qgen.random_x(m, in_dim, seed=42 + m)
+    y0 = np.random.default_rng(43).standard_normal((m, out_dim)).astype(np.float32) * 10
+    yd = dev(y0)
+    banner(f"matmul_add type={qtype} m={m}")
+    qlin.quant_matmul_add(qtype, dev(w), rb, dev(x), yd, out_dim, in_dim, m)
+    got = host(yd)
+    for r in range(m):
+        ref = orc.gemv_add(qtype, w, rb, x[r], y0[r], out_dim, in_dim)
+        assert normwise_rel_err(got[r] - y0[r], ref - y0[r]) <= FP32
+
+
+@pytest.mark.parametrize("qtype,ffn,hid,m", [(Q4_K, 2816, 2048, 16), (Q4_K, 200, 768, 5), (Q4_K, 200, 768, 1),
+                                            (Q8_0, 96, 512, 3)])
+def test_swiglu_rows(qtype, ffn, hid, m):
+    """act[r] = silu(Wg x[r]) * (Wu x[r]) for a batch: C5's shared experts ([2816, 2048] Q4_K gate/up,
+    16 tokens), a short batch, one row (the single-row kernel) and a type without the batched kernel
+    (one launch per row)."""
+    wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=ffn + m)
+    wu, _, _ = qgen.random_matrix(qtype, ffn, hid, seed=ffn + m + 1)
+    x = qgen.random_x(m, hid, seed=m + 3)
+    act_d = empty_f32(m, ffn)
+    banner(f"swiglu_rows type={qtype} ffn={ffn} m={m}")
+    qlin.quant_swiglu_rows(qtype, dev(wg), dev(wu), rb, rb, dev(x), act_d, ffn, hid, m)
+    got = host(act_d)
+    for r in range(m):
+        assert normwise_rel_err(got[r], orc.swiglu(qtype, wg, wu, rb, rb, x[r], ffn, hid)) <= 1e-4
+
+
 @pytest.mark.parametrize("qtype", [Q4_K, Q8_0, Q5_0])
 def test_gemv_add(qtype):
     in_dim = 512
@@ -415,7 +466,7 @@ def test_moe_grouped_c5(dn_type):
 
 
 @pytest.mark.parametrize("gu_type,dn_type,ffn", [(Q4_K, Q8_0, 128), (Q4_K, Q5_0, 256), (Q4_K, Q5_0, 96),
-                                                  (Q6_K, Q8_0, 128)])
+                                                  (Q6_K, Q8_0, 128), (Q4_K, Q4_K, 512)])
 def test_moe_grouped_many_routes_per_expert_and_fallback(gu_type, dn_type, ffn):
     """Routes beyond one pass per expert (8 experts, 24 tokens x 4 routes, about 12 per expert), most
     workgroups without a tile, a down width that is not a multiple of 128 (96: the per-element down
@@ -428,6 +479,26 @@ def test_moe_grouped_many_routes_per_expert_and_fallback(gu_type, dn_type, ffn):
     got = _run_grouped(gu_type, dn_type, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
     ref = _moe_batch_ref(gu_type, dn_type, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
     assert normwise_rel_err(got, ref) <= 1e-4
+
+
+def test_moe_grouped_shared_experts_as_one_expert():
+    """C5's 2 shared experts (SharedExperts.cpp:21-49: swiglu over the concatenated [2816, 2048] Q4_K
+    gate/up, then a Q4_K [2048, 2816] down added into the MoE output) for 16 tokens, run as one
+    expert that every token takes with weight 1.0, on top of an output that already holds the routed
+    sum: the Q4_K streaming down kernel, 4 passes of 4 routes."""
+    E, ffn, hid, tokens, k = 1, 2816, 2048, 16, 1
+    wg, wu, grb, geb, wdn, drb, deb, x, _, _ = _moe_batch(Q4_K, Q4_K, E, ffn, hid, tokens, k, 351)
+    ids = np.zeros((tokens, 1), np.int32)
+    rw = np.ones((tokens, 1), np.float32)
+    out0 = np.random.default_rng(9).standard_normal((tokens, hid)).astype(np.float32)
+    banner("moe grouped shared experts")
+    got = _run_grouped(Q4_K, Q4_K, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+    ref = _moe_batch_ref(Q4_K, Q4_K, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(got - out0, ref - out0) <= 1e-4
+    # the reference's own two launches for one token: fused SwiGLU, then gemv_add into the output
+    act = orc.swiglu(Q4_K, wg, wu, grb, grb, x[0], ffn, hid)
+    ref0 = orc.gemv_add(Q4_K, wdn, drb, act, out0[0], hid, ffn)
+    assert normwise_rel_err(got[0] - out0[0], ref0 - out0[0]) <= 1e-4
 
 
 def test_moe_grouped_skewed_routing():
