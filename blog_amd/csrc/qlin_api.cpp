@@ -402,6 +402,83 @@ int qlin_launch_mla_absorb_v(int type, const uint8_t *w, size_t rb, const float 
                                        stream()));
 }
 
+// a Q8_1 latent cache: rows of at least ceil(kv_lora / 32) blocks, 4-aligned
+static int check_latent_cache(const uint8_t *cache, size_t crb, int kv_lora) {
+    if (crb < qlin_q8_1_row_bytes(kv_lora)) return QLIN_ERR_ROW_BYTES;
+    if (!cache) return QLIN_ERR_NULL;
+    if (!aligned(cache, 4) || crb % 4) return QLIN_ERR_ALIGN;
+    return QLIN_OK;
+}
+
+static int check_pos(const int *d_pos) {
+    if (!d_pos) return QLIN_ERR_NULL;
+    return aligned(d_pos, 4) ? QLIN_OK : QLIN_ERR_ALIGN;
+}
+
+int qlin_launch_mla_store_latent_q8_1_device_pos(const float *kv_cache, uint8_t *cache, int kv_lora, int qk_rope,
+                                                 size_t row_bytes, const int *d_pos) {
+    if (kv_lora <= 0 || qk_rope < 0) return QLIN_ERR_SHAPE;
+    int rc = check_latent_cache(cache, row_bytes, kv_lora);
+    if (rc || (rc = check_f32(kv_cache, true)) || (rc = check_pos(d_pos))) return rc;
+    return launched(qlin::mla_store_latent_q8_1(kv_cache, cache, kv_lora, qk_rope, row_bytes, d_pos, stream()));
+}
+
+int qlin_launch_mla_absorb_scores_device_pos(const float *q_abs, const float *q, const uint8_t *cache, size_t crb,
+                                             const float *q_abs_xsum_delta, const float *kv_cache, float *scores,
+                                             int n_heads, int qk_nope, int qk_rope, int kv_lora, const int *d_pos,
+                                             int max_seq_len, float softmax_scale) {
+    if (n_heads < 0 || qk_nope < 0 || qk_rope < 0 || kv_lora <= 0 || max_seq_len < 0) return QLIN_ERR_SHAPE;
+    if (n_heads == 0 || max_seq_len == 0) return QLIN_OK;
+    int rc = check_latent_cache(cache, crb, kv_lora);
+    if (rc || (rc = check_f32(q_abs, true)) || (rc = check_f32(q, qk_rope > 0)) ||
+        (rc = check_f32(q_abs_xsum_delta, true)) || (rc = check_f32(kv_cache, qk_rope > 0)) ||
+        (rc = check_f32(scores, true)) || (rc = check_pos(d_pos)))
+        return rc;
+    return launched(qlin::mla_absorb_scores(q_abs, q, cache, crb, q_abs_xsum_delta, kv_cache, scores, n_heads, qk_nope,
+                                            qk_rope, kv_lora, d_pos, max_seq_len, softmax_scale, stream()));
+}
+
+int qlin_launch_mla_absorb_context_device_pos(const float *scores, const uint8_t *cache, size_t crb,
+                                              float *attn_xsum_delta, float *attn_latent, int n_heads, int kv_lora,
+                                              const int *d_pos, int max_seq_len) {
+    if (n_heads < 0 || kv_lora <= 0 || max_seq_len <= 0) return QLIN_ERR_SHAPE;
+    if (n_heads == 0) return QLIN_OK;
+    int rc = check_latent_cache(cache, crb, kv_lora);
+    if (rc || (rc = check_f32(scores, true)) || (rc = check_f32(attn_xsum_delta, true)) ||
+        (rc = check_f32(attn_latent, true)) || (rc = check_pos(d_pos)))
+        return rc;
+    return launched(qlin::mla_absorb_context(scores, cache, crb, attn_xsum_delta, attn_latent, n_heads, kv_lora, d_pos,
+                                             max_seq_len, stream()));
+}
+
+int qlin_launch_mla_project_v_device_pos(int type, const uint8_t *w, size_t rb, const uint8_t *cache, size_t crb,
+                                         float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora,
+                                         const int *d_pos) {
+    int rc = check_kv_b(type, w, rb, n_heads, qk_nope, 0, v_head, kv_lora);
+    if (rc) return rc;
+    if (n_heads == 0 || v_head == 0) return QLIN_OK;
+    if (kv_lora == 0) return QLIN_ERR_SHAPE;
+    if (!w) return QLIN_ERR_NULL;
+    if ((rc = check_latent_cache(cache, crb, kv_lora)) || (rc = check_f32(kv_b_cache, true)) || (rc = check_pos(d_pos)))
+        return rc;
+    return launched(qlin::mla_project_v(type, w, rb, cache, crb, kv_b_cache, n_heads, qk_nope, v_head, kv_lora, d_pos,
+                                        stream()));
+}
+
+int qlin_launch_mla_absorb_context_v_device_pos(const float *scores, const float *kv_b_cache, float *attn,
+                                                int n_heads, int qk_nope, int v_head, const int *d_pos,
+                                                int max_seq_len) {
+    if (n_heads < 0 || qk_nope < 0 || v_head < 0 || max_seq_len <= 0) return QLIN_ERR_SHAPE;
+    if (v_head > 256) return QLIN_ERR_LIMIT;
+    if (n_heads == 0 || v_head == 0) return QLIN_OK;
+    int rc;
+    if ((rc = check_f32(scores, true)) || (rc = check_f32(kv_b_cache, true)) || (rc = check_f32(attn, true)) ||
+        (rc = check_pos(d_pos)))
+        return rc;
+    return launched(qlin::mla_absorb_context_v(scores, kv_b_cache, attn, n_heads, qk_nope, v_head, d_pos, max_seq_len,
+                                               stream()));
+}
+
 size_t qlin_moe_grouped_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size) {
     if (tokens < 0 || k < 0 || n_experts <= 0 || ffn_dim <= 0 || hidden_size <= 0) return 0;
     return qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden_size);

@@ -35,10 +35,6 @@ struct DenseArgs {
     int n, k, m;
 };
 
-__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
 // The raw bytes a lane needs of one Q4_K super-block: the header (d, dmin, 12 scale bytes) and,
 // for each pair c of sub-blocks, qs bytes 32c + 8g .. 32c + 8g + 7 (low nibbles: sub-block 2c,
 // high nibbles: sub-block 2c + 1).

@@ -45,6 +45,21 @@ bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, 
 hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, const float *x, float *y,
                         int out_dim, int in_dim, int m, int mode, hipStream_t s);
 
+// MLA over the Q8_1 latent cache (qlin_mla_latent.hip); pos is read from d_pos on the device.
+hipError_t mla_store_latent_q8_1(const float *kv_cache, uint8_t *cache, int kv_lora, int qk_rope, size_t row_bytes,
+                                 const int *d_pos, hipStream_t s);
+hipError_t mla_absorb_scores(const float *q_abs, const float *q, const uint8_t *cache, size_t cache_row_bytes,
+                             const float *delta, const float *kv_cache, float *scores, int n_heads, int qk_nope,
+                             int qk_rope, int kv_lora, const int *d_pos, int max_seq, float scale, hipStream_t s);
+hipError_t mla_absorb_context(const float *scores, const uint8_t *cache, size_t cache_row_bytes, float *delta_out,
+                              float *latent_out, int n_heads, int kv_lora, const int *d_pos, int max_seq,
+                              hipStream_t s);
+hipError_t mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_t *cache, size_t cache_row_bytes,
+                         float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora, const int *d_pos,
+                         hipStream_t s);
+hipError_t mla_absorb_context_v(const float *scores, const float *kv_b_cache, float *attn, int n_heads, int qk_nope,
+                                int v_head, const int *d_pos, int max_seq, hipStream_t s);
+
 // The per-element fallback used for any type / alignment (exposed for tests of the fast paths).
 hipError_t gemv_generic(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y,
                         int out_dim, int in_dim, int m, bool add, hipStream_t s);

@@ -81,4 +81,9 @@ __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x
                                                    0, 0, 0);
 }
 
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; D as above.
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 }  // namespace qlin

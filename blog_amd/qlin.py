@@ -64,6 +64,11 @@ SIGNATURES = {
     "qlin_launch_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
     "qlin_launch_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),
     "qlin_launch_mla_absorb_v": (I, [I, P, SZ, P, P, P, I, I, I, I]),
+    "qlin_launch_mla_store_latent_q8_1_device_pos": (I, [P, P, I, I, SZ, P]),
+    "qlin_launch_mla_absorb_scores_device_pos": (I, [P, P, P, SZ, P, P, P, I, I, I, I, P, I, F]),
+    "qlin_launch_mla_absorb_context_device_pos": (I, [P, P, SZ, P, P, I, I, P, I]),
+    "qlin_launch_mla_project_v_device_pos": (I, [I, P, SZ, P, SZ, P, I, I, I, I, P]),
+    "qlin_launch_mla_absorb_context_v_device_pos": (I, [P, P, P, I, I, I, P, I]),
     # include/qlin_gguf.h
     "qlin_gguf_open": (I, [S, PP]),
     "qlin_gguf_close": (None, [P]),

@@ -211,6 +211,47 @@ int qlin_launch_mla_absorb_v(int type, const uint8_t *kv_b_weight, size_t row_by
                              const float *attn_xsum_delta, float *attn, int n_heads, int qk_nope, int v_head,
                              int kv_lora);
 
+/* ---- MLA decode over the Q8_1 latent cache (kernel.cuh:297-327) -------------------------------
+ * The cache holds one Q8_1 row of latent_row_bytes (>= ceil(kv_lora / 32) * 36, a multiple of 4)
+ * per position; kv_cache rows are f32 [kv_lora + qk_rope] (latent, then k_rope).  pos = *d_pos is
+ * read on the device (d_pos a device int); the score / context entry points clamp it to
+ * max_seq_len - 1, and a negative pos means no positions. */
+
+/* cache[pos] = Q8_1 of kv_cache[pos, 0 .. kv_lora), zero-padded to row_bytes / 36 blocks, s = d * sum(q).
+ * Replaces launch_mla_store_latent_q8_1_device_pos (launch.cu:911-917). */
+int qlin_launch_mla_store_latent_q8_1_device_pos(const float *kv_cache, uint8_t *latent_q8_1_cache, int kv_lora,
+                                                 int qk_rope, size_t row_bytes, const int *d_pos);
+
+/* scores[h * max_seq_len + t] = softmax_scale * (q_abs[h] . latent(t) + q_rope[h] . k_rope(t)
+ *   + sum_b q_abs_xsum_delta[h, b] * (stored_sum(t, b) - dequantized_sum(t, b))) for t <= pos; q
+ * rows are [qk_nope + qk_rope] per head.  Replaces launch_mla_absorb_scores_device_pos (launch.cu:977-989). */
+int qlin_launch_mla_absorb_scores_device_pos(const float *q_abs, const float *q, const uint8_t *latent_q8_1_cache,
+                                             size_t latent_row_bytes, const float *q_abs_xsum_delta,
+                                             const float *kv_cache, float *scores, int n_heads, int qk_nope,
+                                             int qk_rope, int kv_lora, const int *d_pos, int max_seq_len,
+                                             float softmax_scale);
+
+/* p = softmax over t <= pos of scores[h] (denominator + 1e-9); attn_latent[h, k] = sum_t p_t latent(t, k),
+ * attn_xsum_delta[h, b] = sum_t p_t (stored_sum(t, b) - dequantized_sum(t, b)).
+ * Replaces launch_mla_absorb_context_device_pos (launch.cu:991-1000). */
+int qlin_launch_mla_absorb_context_device_pos(const float *scores, const uint8_t *latent_q8_1_cache,
+                                              size_t latent_row_bytes, float *attn_xsum_delta, float *attn_latent,
+                                              int n_heads, int kv_lora, const int *d_pos, int max_seq_len);
+
+/* kv_b_cache[pos, r] = W_kv_b[r] . cache[pos] (Q8_1 block-dot semantics of quant_matmul_q8_1) for the
+ * v rows r = h * (qk_nope + v_head) + qk_nope + v of every head.  Types Q4_K, Q6_K, Q5_0, Q8_0.
+ * Replaces launch_mla_project_v_device_pos (launch.cu:1015-1040). */
+int qlin_launch_mla_project_v_device_pos(int type, const uint8_t *kv_b_weight, size_t row_bytes,
+                                         const uint8_t *latent_q8_1_cache, size_t latent_row_bytes,
+                                         float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora,
+                                         const int *d_pos);
+
+/* attn[h, v] = sum_t p_t kv_b_cache[t, h * (qk_nope + v_head) + qk_nope + v], p the softmax of
+ * scores[h] as above; v_head <= 256.  Replaces launch_mla_absorb_context_v_device_pos (launch.cu:1042-1049). */
+int qlin_launch_mla_absorb_context_v_device_pos(const float *scores, const float *kv_b_cache, float *attn,
+                                                int n_heads, int qk_nope, int v_head, const int *d_pos,
+                                                int max_seq_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -167,4 +167,45 @@ inline void launch_mla_absorb_v(DType quant_type, const uint8_t *kv_b_weight, si
           "launch_mla_absorb_v");
 }
 
+// kernel.cuh:297-327 -- the Q8_1 latent cache
+inline void launch_mla_store_latent_q8_1_device_pos(const float *kv_cache, uint8_t *latent_q8_1_cache, int kv_lora,
+                                                    int qk_rope, size_t row_bytes, const int *d_pos) {
+    check(qlin_launch_mla_store_latent_q8_1_device_pos(kv_cache, latent_q8_1_cache, kv_lora, qk_rope, row_bytes, d_pos),
+          "launch_mla_store_latent_q8_1_device_pos");
+}
+inline void launch_mla_absorb_scores_device_pos(const float *q_abs, const float *q, const uint8_t *latent_q8_1_cache,
+                                                size_t latent_q8_1_row_bytes, const float *q_abs_xsum_delta,
+                                                const float *kv_cache, float *scores, int n_heads, int qk_nope,
+                                                int qk_rope, int kv_lora, const int *d_pos, int max_seq_len,
+                                                float softmax_scale) {
+    check(qlin_launch_mla_absorb_scores_device_pos(q_abs, q, latent_q8_1_cache, latent_q8_1_row_bytes, q_abs_xsum_delta,
+                                                   kv_cache, scores, n_heads, qk_nope, qk_rope, kv_lora, d_pos,
+                                                   max_seq_len, softmax_scale),
+          "launch_mla_absorb_scores_device_pos");
+}
+inline void launch_mla_absorb_context_device_pos(const float *scores, const uint8_t *latent_q8_1_cache,
+                                                 size_t latent_q8_1_row_bytes, float *attn_xsum_delta,
+                                                 float *attn_latent, int n_heads, int kv_lora, const int *d_pos,
+                                                 int max_seq_len) {
+    check(qlin_launch_mla_absorb_context_device_pos(scores, latent_q8_1_cache, latent_q8_1_row_bytes, attn_xsum_delta,
+                                                    attn_latent, n_heads, kv_lora, d_pos, max_seq_len),
+          "launch_mla_absorb_context_device_pos");
+}
+inline void launch_mla_project_v_device_pos(DType quant_type, const uint8_t *kv_b_weight, size_t row_bytes,
+                                            const uint8_t *latent_q8_1_cache, size_t latent_q8_1_row_bytes,
+                                            float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora,
+                                            const int *d_pos) {
+    check(qlin_launch_mla_project_v_device_pos(static_cast<int>(quant_type), kv_b_weight, row_bytes, latent_q8_1_cache,
+                                               latent_q8_1_row_bytes, kv_b_cache, n_heads, qk_nope, v_head, kv_lora,
+                                               d_pos),
+          "launch_mla_project_v_device_pos");
+}
+inline void launch_mla_absorb_context_v_device_pos(const float *scores, const float *kv_b_cache, float *attn,
+                                                   int n_heads, int qk_nope, int v_head, const int *d_pos,
+                                                   int max_seq_len) {
+    check(qlin_launch_mla_absorb_context_v_device_pos(scores, kv_b_cache, attn, n_heads, qk_nope, v_head, d_pos,
+                                                      max_seq_len),
+          "launch_mla_absorb_context_v_device_pos");
+}
+
 }  // namespace qlin_ref

@@ -71,6 +71,11 @@ def _declare(L: C.CDLL) -> None:
         "orc_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
         "orc_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),
         "orc_mla_absorb_v": (I, [I, P, SZ, P, P, P, I, I, I, I]),
+        "orc_mla_store_latent_q8_1": (I, [P, P, I, I, SZ, I]),
+        "orc_mla_absorb_scores": (I, [P, P, P, SZ, P, P, P, I, I, I, I, I, I, C.c_float]),
+        "orc_mla_absorb_context": (I, [P, P, SZ, P, P, I, I, I, I]),
+        "orc_mla_project_v": (I, [I, P, SZ, P, SZ, P, I, I, I, I, I]),
+        "orc_mla_absorb_context_v": (I, [P, P, P, I, I, I, I, I]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -255,4 +260,54 @@ def mla_absorb_v(qtype, w, rb, latent, delta, n_heads, qk_nope, v_head, kv_lora)
     out = np.zeros(n_heads * v_head, np.float64)
     _ok(lib().orc_mla_absorb_v(qtype, _p(w), rb, _p(latent), _p(delta), _p(out), n_heads, qk_nope, v_head, kv_lora),
         "orc_mla_absorb_v")
+    return out
+
+
+# ---- MLA over the Q8_1 latent cache --------------------------------------------------------------
+def mla_store_latent_q8_1(kv_cache, cache, kv_lora, qk_rope, row_bytes, pos) -> np.ndarray:
+    """cache (uint8 [rows, row_bytes]) with row pos rewritten; returns a new array."""
+    kv_cache = np.ascontiguousarray(kv_cache, np.float32)
+    out = np.array(cache, np.uint8, copy=True)
+    _ok(lib().orc_mla_store_latent_q8_1(_p(kv_cache), _p(out), kv_lora, qk_rope, row_bytes, pos),
+        "orc_mla_store_latent_q8_1")
+    return out
+
+
+def mla_absorb_scores(q_abs, q, cache, crb, delta, kv_cache, n_heads, qk_nope, qk_rope, kv_lora, pos, max_seq,
+                      scale) -> np.ndarray:
+    """[n_heads, max_seq] float64; entries past pos are NaN."""
+    args = [np.ascontiguousarray(a, np.float32) for a in (q_abs, q, delta, kv_cache)]
+    cache = np.ascontiguousarray(cache, np.uint8)
+    out = np.full((n_heads, max_seq), np.nan, np.float64)
+    _ok(lib().orc_mla_absorb_scores(_p(args[0]), _p(args[1]), _p(cache), crb, _p(args[2]), _p(args[3]), _p(out),
+                                    n_heads, qk_nope, qk_rope, kv_lora, pos, max_seq, scale), "orc_mla_absorb_scores")
+    return out
+
+
+def mla_absorb_context(scores, cache, crb, n_heads, kv_lora, pos, max_seq):
+    """(attn_latent [n_heads, kv_lora], attn_xsum_delta [n_heads, ceil(kv_lora / 32)]) in float64."""
+    scores = np.ascontiguousarray(scores, np.float32)
+    cache = np.ascontiguousarray(cache, np.uint8)
+    lat = np.zeros((n_heads, kv_lora), np.float64)
+    dl = np.zeros((n_heads, (kv_lora + 31) // 32), np.float64)
+    _ok(lib().orc_mla_absorb_context(_p(scores), _p(cache), crb, _p(dl), _p(lat), n_heads, kv_lora, pos, max_seq),
+        "orc_mla_absorb_context")
+    return lat, dl
+
+
+def mla_project_v(qtype, w, rb, cache, crb, kv_b_cache, n_heads, qk_nope, v_head, kv_lora, pos) -> np.ndarray:
+    """kv_b_cache (float64 copy) with the v rows of position pos written."""
+    cache = np.ascontiguousarray(cache, np.uint8)
+    out = np.array(kv_b_cache, np.float64, copy=True)
+    _ok(lib().orc_mla_project_v(qtype, _p(w), rb, _p(cache), crb, _p(out), n_heads, qk_nope, v_head, kv_lora, pos),
+        "orc_mla_project_v")
+    return out
+
+
+def mla_absorb_context_v(scores, kv_b_cache, n_heads, qk_nope, v_head, pos, max_seq) -> np.ndarray:
+    scores = np.ascontiguousarray(scores, np.float32)
+    kvb = np.ascontiguousarray(kv_b_cache, np.float32)
+    out = np.zeros((n_heads, v_head), np.float64)
+    _ok(lib().orc_mla_absorb_context_v(_p(scores), _p(kvb), _p(out), n_heads, qk_nope, v_head, pos, max_seq),
+        "orc_mla_absorb_context_v")
     return out

@@ -612,6 +612,128 @@ int orc_mla_absorb_v(int type, const uint8_t *w, size_t row_bytes, const float *
     return 0;
 }
 
+/* ------------------------------------------------------------------------------------------ */
+/* MLA over the Q8_1 latent cache -- kernel.cu:2945-3415                                       */
+
+int orc_mla_store_latent_q8_1(const float *kv_cache, uint8_t *cache, int kv_lora, int qk_rope, size_t row_bytes,
+                              int pos) {
+    /* kernel.cu:2945-2978: one block of 32 per warp, values past kv_lora are 0, s = d * sum(q) --
+     * the quantizer of kernel.cu:1679-1720 over the row zero-padded to row_bytes / 36 blocks */
+    const int nblk = (int)(row_bytes / 36);
+    if (kv_lora <= 0 || qk_rope < 0 || pos < 0) return -1;
+    float *row = (float *)calloc((size_t)nblk * 32 + 1, sizeof(float));
+    if (!row) return -1;
+    const int n = kv_lora < nblk * 32 ? kv_lora : nblk * 32;
+    memcpy(row, kv_cache + (size_t)pos * (kv_lora + qk_rope), sizeof(float) * (size_t)n);
+    orc_quantize_q8_1(row, cache + (size_t)pos * row_bytes, nblk * 32, 1, 0);
+    free(row);
+    return 0;
+}
+
+/* d * q of latent element k of a Q8_1 row (kernel.cu:2979-2987; exact in f32) */
+static float latent_at(const uint8_t *row, int k) {
+    const uint8_t *blk = row + (size_t)(k >> 5) * 36;
+    return orc_f16_to_f32(rd16(blk)) * (float)((const int8_t *)(blk + 4))[k & 31];
+}
+
+/* stored f16 sum minus the block's dequantized values added in order (kernel.cu:2989-3003) */
+static float latent_sum_delta(const uint8_t *row, int b, int kv_lora) {
+    const uint8_t *blk = row + (size_t)b * 36;
+    const float d = orc_f16_to_f32(rd16(blk));
+    float sum = 0.0f;
+    for (int l = 0; l < 32 && b * 32 + l < kv_lora; ++l) sum += d * (float)((const int8_t *)(blk + 4))[l];
+    return orc_f16_to_f32(rd16(blk + 2)) - sum;
+}
+
+int orc_mla_absorb_scores(const float *q_abs, const float *q, const uint8_t *cache, size_t crb, const float *delta,
+                          const float *kv_cache, double *scores, int n_heads, int qk_nope, int qk_rope, int kv_lora,
+                          int pos, int max_seq, float scale) {
+    /* kernel.cu:3157-3196 */
+    const int nb = (kv_lora + 31) / 32;
+    if (pos >= max_seq) pos = max_seq - 1;
+    for (int h = 0; h < n_heads; ++h)
+        for (int t = 0; t <= pos; ++t) {
+            const uint8_t *row = cache + (size_t)t * crb;
+            double dot = 0.0;
+            for (int k = 0; k < kv_lora; ++k) dot += (double)q_abs[(size_t)h * kv_lora + k] * latent_at(row, k);
+            const float *qr = q + (size_t)h * (qk_nope + qk_rope) + qk_nope;
+            const float *kr = kv_cache + (size_t)t * (kv_lora + qk_rope) + kv_lora;
+            for (int r = 0; r < qk_rope; ++r) dot += (double)qr[r] * kr[r];
+            for (int b = 0; b < nb; ++b) dot += (double)delta[(size_t)h * nb + b] * latent_sum_delta(row, b, kv_lora);
+            scores[(size_t)h * max_seq + t] = dot * scale;
+        }
+    return 0;
+}
+
+/* exp(s - max) / (sum + 1e-9) over t <= pos of one head's scores (kernel.cu:3211-3235) */
+static void softmax_probs(const float *s, int pos, double *p) {
+    double mx = -INFINITY, den = 0.0;
+    for (int t = 0; t <= pos; ++t) mx = s[t] > mx ? s[t] : mx;
+    for (int t = 0; t <= pos; ++t) den += (p[t] = exp((double)s[t] - mx));
+    for (int t = 0; t <= pos; ++t) p[t] /= den + 1e-9;
+}
+
+int orc_mla_absorb_context(const float *scores, const uint8_t *cache, size_t crb, double *delta_out,
+                           double *latent_out, int n_heads, int kv_lora, int pos, int max_seq) {
+    /* kernel.cu:3198-3257 */
+    const int nb = (kv_lora + 31) / 32;
+    if (pos >= max_seq) pos = max_seq - 1;
+    double *p = (double *)malloc(sizeof(double) * (size_t)(pos + 2));
+    if (!p) return -1;
+    for (int h = 0; h < n_heads; ++h) {
+        softmax_probs(scores + (size_t)h * max_seq, pos, p);
+        for (int k = 0; k < kv_lora; ++k) {
+            double acc = 0.0;
+            for (int t = 0; t <= pos; ++t) acc += p[t] * latent_at(cache + (size_t)t * crb, k);
+            latent_out[(size_t)h * kv_lora + k] = acc;
+        }
+        for (int b = 0; b < nb; ++b) {
+            double acc = 0.0;
+            for (int t = 0; t <= pos; ++t) acc += p[t] * latent_sum_delta(cache + (size_t)t * crb, b, kv_lora);
+            delta_out[(size_t)h * nb + b] = acc;
+        }
+    }
+    free(p);
+    return 0;
+}
+
+int orc_mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_t *cache, size_t crb,
+                      double *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora, int pos) {
+    /* kernel.cu:3259-3361: each v row of kv_b against the latent row, with the block-dot semantics
+     * of quant_matmul_q8_1 (kernel.cu:2305-2402) */
+    if (check_shape(type, kv_lora) || pos < 0) return -1;
+    const size_t stride = (size_t)n_heads * (qk_nope + v_head);
+    for (int h = 0; h < n_heads; ++h)
+        for (int v = 0; v < v_head; ++v) {
+            const size_t r = (size_t)h * (qk_nope + v_head) + qk_nope + v;
+            double y;
+            if (orc_matmul_q8_1(type, w + r * row_bytes, row_bytes, cache + (size_t)pos * crb, &y, 1, kv_lora, 1))
+                return -1;
+            kv_b_cache[(size_t)pos * stride + r] = y;
+        }
+    return 0;
+}
+
+int orc_mla_absorb_context_v(const float *scores, const float *kv_b_cache, double *attn, int n_heads, int qk_nope,
+                             int v_head, int pos, int max_seq) {
+    /* kernel.cu:3368-3415 */
+    if (pos >= max_seq) pos = max_seq - 1;
+    double *p = (double *)malloc(sizeof(double) * (size_t)(pos + 2));
+    if (!p) return -1;
+    const size_t stride = (size_t)n_heads * (qk_nope + v_head);
+    for (int h = 0; h < n_heads; ++h) {
+        softmax_probs(scores + (size_t)h * max_seq, pos, p);
+        for (int v = 0; v < v_head; ++v) {
+            double acc = 0.0;
+            for (int t = 0; t <= pos; ++t)
+                acc += p[t] * kv_b_cache[(size_t)t * stride + (size_t)h * (qk_nope + v_head) + qk_nope + v];
+            attn[(size_t)h * v_head + v] = acc;
+        }
+    }
+    free(p);
+    return 0;
+}
+
 int orc_argmax(const float *v, int n) {
     float best = -INFINITY;
     int idx = 0;

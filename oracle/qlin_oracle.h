@@ -148,6 +148,24 @@ int orc_mla_absorb_q4_xsum_delta(const float *q, const uint8_t *w, size_t row_by
 int orc_mla_absorb_v(int type, const uint8_t *w, size_t row_bytes, const float *latent, const float *delta,
                      double *attn, int n_heads, int qk_nope, int v_head, int kv_lora);
 
+/* MLA decode over the Q8_1 latent cache (kernel.cu:2945-3415) at position pos; sums in double.
+ * store: cache row pos from kv_cache row pos (row_bytes / 36 blocks, zero past kv_lora).
+ * scores: scores[h * max_seq + t] for t <= pos (other entries untouched).
+ * context: the softmax-weighted latent rows and block-sum corrections per head.
+ * project_v: kv_b_cache[pos * n_heads * (qk_nope + v_head) + r] for the v rows r of every head.
+ * context_v: the softmax-weighted v rows of kv_b_cache per head. */
+int orc_mla_store_latent_q8_1(const float *kv_cache, uint8_t *cache, int kv_lora, int qk_rope, size_t row_bytes,
+                              int pos);
+int orc_mla_absorb_scores(const float *q_abs, const float *q, const uint8_t *cache, size_t cache_row_bytes,
+                          const float *delta, const float *kv_cache, double *scores, int n_heads, int qk_nope,
+                          int qk_rope, int kv_lora, int pos, int max_seq, float scale);
+int orc_mla_absorb_context(const float *scores, const uint8_t *cache, size_t cache_row_bytes, double *delta_out,
+                           double *latent_out, int n_heads, int kv_lora, int pos, int max_seq);
+int orc_mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_t *cache, size_t cache_row_bytes,
+                      double *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora, int pos);
+int orc_mla_absorb_context_v(const float *scores, const float *kv_b_cache, double *attn, int n_heads, int qk_nope,
+                             int v_head, int pos, int max_seq);
+
 #ifdef __cplusplus
 }
 #endif

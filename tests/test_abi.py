@@ -202,6 +202,37 @@ def test_embedding_and_mla_validation():
     assert qlin.status(V, 14, FAKE, 420, FAKE, 0, FAKE, 16, 128, 0, 512) == OK
 
 
+def test_mla_latent_cache_validation():
+    """The Q8_1 latent-cache entry points (launch.cu:911-1049): cache rows shorter than the latent's
+    blocks, misaligned rows, null pointers and v_head beyond the kernel's limit are statuses; empty
+    head counts return before any launch."""
+    S = "qlin_launch_mla_store_latent_q8_1_device_pos"
+    assert qlin.status(S, FAKE, FAKE, 0, 64, 576, FAKE) == SHAPE
+    assert qlin.status(S, FAKE, FAKE, 512, 64, 540, FAKE) == ROWB           # 15 blocks for 16
+    assert qlin.status(S, FAKE, FAKE + 2, 512, 64, 576, FAKE) == ALIGN
+    assert qlin.status(S, FAKE, FAKE, 512, 64, 578, FAKE) == ALIGN          # rows not 4-aligned
+    assert qlin.status(S, FAKE, FAKE, 512, 64, 576, 0) == NULL              # d_pos
+    C_ = "qlin_launch_mla_absorb_scores_device_pos"
+    assert qlin.status(C_, FAKE, FAKE, FAKE, 576, FAKE, FAKE, FAKE, 16, 128, 64, 0, FAKE, 256, 0.1) == SHAPE
+    assert qlin.status(C_, FAKE, FAKE, 0, 576, FAKE, FAKE, FAKE, 16, 128, 64, 512, FAKE, 256, 0.1) == NULL
+    assert qlin.status(C_, FAKE, 0, FAKE, 576, FAKE, FAKE, FAKE, 16, 128, 64, 512, FAKE, 256, 0.1) == NULL
+    assert qlin.status(C_, 0, 0, 0, 0, 0, 0, 0, 0, 128, 64, 512, 0, 256, 0.1) == OK
+    X = "qlin_launch_mla_absorb_context_device_pos"
+    assert qlin.status(X, FAKE, FAKE, 576, FAKE, FAKE, 16, 512, FAKE, 0) == SHAPE
+    assert qlin.status(X, FAKE, FAKE, 500, FAKE, FAKE, 16, 512, FAKE, 256) == ROWB
+    assert qlin.status(X, FAKE, FAKE, 576, 0, FAKE, 16, 512, FAKE, 256) == NULL
+    P_ = "qlin_launch_mla_project_v_device_pos"
+    assert qlin.status(P_, 2, FAKE, 18, FAKE, 576, FAKE, 16, 128, 128, 512, FAKE) == UNSUP
+    assert qlin.status(P_, 12, FAKE, 288, FAKE, 576, FAKE, 16, 128, 128, 500, FAKE) == SHAPE
+    assert qlin.status(P_, 12, FAKE, 288, FAKE, 36, FAKE, 16, 128, 128, 512, FAKE) == ROWB
+    assert qlin.status(P_, 12, FAKE, 288, FAKE, 576, FAKE, 16, 128, 128, 512, 0) == NULL
+    V = "qlin_launch_mla_absorb_context_v_device_pos"
+    assert qlin.status(V, FAKE, FAKE, FAKE, 16, 128, 257, FAKE, 256) == LIMIT
+    assert qlin.status(V, FAKE, FAKE, FAKE, 16, 128, 128, FAKE, 0) == SHAPE
+    assert qlin.status(V, FAKE, 0, FAKE, 16, 128, 128, FAKE, 256) == NULL
+    assert qlin.status(V, 0, 0, 0, 0, 128, 128, 0, 256) == OK
+
+
 def test_cpp_shim_compiles():
     """The C++ shim with the reference's launcher names builds against the C ABI."""
     gxx = shutil.which("g++")
