@@ -451,6 +451,24 @@ int qlin_launch_mla_absorb_context_device_pos(const float *scores, const uint8_t
                                              max_seq_len, stream()));
 }
 
+int qlin_launch_mla_absorb_attend_device_pos(const float *q_abs, const float *q, const uint8_t *cache, size_t crb,
+                                             const float *q_abs_xsum_delta, float *attn_xsum_delta,
+                                             const float *kv_cache, float *attn_latent, int n_heads, int qk_nope,
+                                             int qk_rope, int kv_lora, const int *d_pos, int max_seq_len,
+                                             float softmax_scale) {
+    if (n_heads < 0 || qk_nope < 0 || qk_rope < 0 || kv_lora <= 0 || max_seq_len <= 0) return QLIN_ERR_SHAPE;
+    if (!qlin::mla_attend_ok(max_seq_len, kv_lora, qk_rope)) return QLIN_ERR_LIMIT;
+    if (n_heads == 0) return QLIN_OK;
+    int rc = check_latent_cache(cache, crb, kv_lora);
+    if (rc || (rc = check_f32(q_abs, true)) || (rc = check_f32(q, qk_rope > 0)) ||
+        (rc = check_f32(q_abs_xsum_delta, true)) || (rc = check_f32(attn_xsum_delta, true)) ||
+        (rc = check_f32(kv_cache, qk_rope > 0)) || (rc = check_f32(attn_latent, true)) || (rc = check_pos(d_pos)))
+        return rc;
+    return launched(qlin::mla_absorb_attend(q_abs, q, cache, crb, q_abs_xsum_delta, attn_xsum_delta, kv_cache,
+                                            attn_latent, n_heads, qk_nope, qk_rope, kv_lora, d_pos, max_seq_len,
+                                            softmax_scale, stream()));
+}
+
 int qlin_launch_mla_project_v_device_pos(int type, const uint8_t *w, size_t rb, const uint8_t *cache, size_t crb,
                                          float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora,
                                          const int *d_pos) {

@@ -54,6 +54,12 @@ hipError_t mla_absorb_scores(const float *q_abs, const float *q, const uint8_t *
 hipError_t mla_absorb_context(const float *scores, const uint8_t *cache, size_t cache_row_bytes, float *delta_out,
                               float *latent_out, int n_heads, int kv_lora, const int *d_pos, int max_seq,
                               hipStream_t s);
+// The fused scores + softmax + context of one head per workgroup (scores of every position in LDS).
+bool mla_attend_ok(int max_seq, int kv_lora, int qk_rope);
+hipError_t mla_absorb_attend(const float *q_abs, const float *q, const uint8_t *cache, size_t cache_row_bytes,
+                             const float *delta, float *delta_out, const float *kv_cache, float *latent_out,
+                             int n_heads, int qk_nope, int qk_rope, int kv_lora, const int *d_pos, int max_seq,
+                             float scale, hipStream_t s);
 hipError_t mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_t *cache, size_t cache_row_bytes,
                          float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora, const int *d_pos,
                          hipStream_t s);

@@ -11,6 +11,7 @@
 //   context    p[h, t] = exp(s[h, t] - max_t s[h]) / (sum_t exp(...) + 1e-9);
 //              latent[h, k] = sum_t p[h, t] L(t, k);  delta[h, b] = sum_t p[h, t] (S(t, b) - ...)
 //                                                                            (kernel.cu:3198-3257)
+//   attend     scores, softmax (fast exp, no 1e-9) and context in one launch   (kernel.cu:3078-3155)
 //   project_v  kv_b_cache[pos, v row r of head h] = W_kv_b[r] . cache[pos] with the Q8_1 block-dot
 //              semantics of quant_matmul_q8_1                               (kernel.cu:3259-3361)
 //   context_v  attn[h, v] = sum_t p[h, t] kv_b_cache[t, v row of head h]   (kernel.cu:3368-3415)
@@ -274,6 +275,93 @@ __global__ __launch_bounds__(kCThreads) void context_v_kernel(const float *__res
     }
 }
 
+constexpr int kAMaxSeq = 32768;  // attend: scores of every position in LDS
+constexpr size_t kMaxLds = 160 * 1024;
+
+// Scores, softmax and context of one head in one workgroup (the fused form): the scores of all
+// positions stay in LDS.  exp is the fast __expf and the denominator has no 1e-9 term, as in
+// kernel.cu:3078-3155.
+__global__ __launch_bounds__(kCThreads) void attend_kernel(const ScoreArgs a, float *delta_out, float *latent_out) {
+    extern __shared__ float s_sc[];  // [max_seq] scores, then q_abs [kv_lora], q_rope [qk_rope], delta [nb]
+    __shared__ float s_red[2][kCWaves];
+    __shared__ float s_out[kCWaves][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x;
+    const int pos = min(*a.d_pos, a.max_seq - 1);
+    const int nb = (a.kv_lora + 31) / 32;
+    float *s_qa = s_sc + a.max_seq, *s_qr = s_qa + a.kv_lora, *s_dl = s_qr + a.qk_rope;
+    for (int i = tid; i < a.kv_lora; i += kCThreads) s_qa[i] = a.q_abs[static_cast<size_t>(h) * a.kv_lora + i];
+    for (int i = tid; i < a.qk_rope; i += kCThreads)
+        s_qr[i] = a.q[static_cast<size_t>(h) * (a.qk_nope + a.qk_rope) + a.qk_nope + i];
+    for (int i = tid; i < nb; i += kCThreads) s_dl[i] = a.delta[static_cast<size_t>(h) * nb + i];
+    __syncthreads();
+
+    // scores: a wave per position, lanes over the latent values, the rope pair and the block sums
+    float m = -INFINITY;
+    for (int t = wave; t <= pos; t += kCWaves) {
+        const uint8_t *row = a.cache + static_cast<size_t>(t) * a.crb;
+        const float *kr = a.kv_cache + static_cast<size_t>(t) * (a.kv_lora + a.qk_rope) + a.kv_lora;
+        float dot = 0.0f;
+        for (int k = lane; k < a.kv_lora; k += 64) {
+            const uint8_t *blk = row + static_cast<size_t>(k >> 5) * 36;
+            dot = fmaf(s_qa[k], __fmul_rn(f16_bits_to_f32(ld_u16(blk)),
+                                          static_cast<float>(reinterpret_cast<const int8_t *>(blk + 4)[k & 31])), dot);
+        }
+        for (int r = lane; r < a.qk_rope; r += 64) dot = fmaf(s_qr[r], kr[r], dot);
+        for (int b = lane; b < nb; b += 64)
+            dot = fmaf(s_dl[b], block_sum_delta(row + static_cast<size_t>(b) * 36, a.kv_lora - 32 * b), dot);
+        dot = wave_sum(dot);
+        const float sc = __fmul_rn(dot, a.scale);
+        if (lane == 0) s_sc[t] = sc;
+        m = fmaxf(m, sc);
+    }
+    if (lane == 0) s_red[0][wave] = m;
+    __syncthreads();
+    m = -INFINITY;
+    for (int w = 0; w < kCWaves; ++w) m = fmaxf(m, s_red[0][w]);
+    float den = 0.0f;
+    for (int t = tid; t <= pos; t += kCThreads) {
+        const float e = __expf(s_sc[t] - m);
+        s_sc[t] = e;
+        den += e;
+    }
+    den = wave_sum(den);
+    if (lane == 0) s_red[1][wave] = den;
+    __syncthreads();
+    den = 0.0f;
+    for (int w = 0; w < kCWaves; ++w) den += s_red[1][w];
+
+    // context: a column per lane, the positions split over the waves, wave partials added in order
+    const int ncol = a.kv_lora + nb;
+    for (int c0 = 0; c0 < ncol; c0 += 64) {
+        const int c = c0 + lane;
+        float acc = 0.0f;
+        if (c < ncol)
+            for (int t = wave; t <= pos; t += kCWaves) {
+                const uint8_t *row = a.cache + static_cast<size_t>(t) * a.crb;
+                float v;
+                if (c < a.kv_lora) {
+                    const uint8_t *blk = row + static_cast<size_t>(c >> 5) * 36;
+                    v = __fmul_rn(f16_bits_to_f32(ld_u16(blk)),
+                                  static_cast<float>(reinterpret_cast<const int8_t *>(blk + 4)[c & 31]));
+                } else {
+                    const int b = c - a.kv_lora;
+                    v = block_sum_delta(row + static_cast<size_t>(b) * 36, a.kv_lora - 32 * b);
+                }
+                acc = fmaf(s_sc[t] / den, v, acc);
+            }
+        s_out[wave][lane] = acc;
+        __syncthreads();
+        if (tid < 64 && c < ncol) {
+            float o = 0.0f;
+            for (int w = 0; w < kCWaves; ++w) o += s_out[w][tid];
+            if (c < a.kv_lora) latent_out[static_cast<size_t>(h) * a.kv_lora + c] = o;
+            else delta_out[static_cast<size_t>(h) * nb + (c - a.kv_lora)] = o;
+        }
+        __syncthreads();
+    }
+}
+
 template <int T> struct ProjectV {
     static void run(const uint8_t *w, size_t rb, const uint8_t *cache, size_t crb, float *kvb, int nh, int qn, int vh,
                     int kl, const int *d_pos, hipStream_t s) {
@@ -311,6 +399,26 @@ hipError_t mla_absorb_context(const float *scores, const uint8_t *cache, size_t 
     const int nb = (kv_lora + 31) / 32;
     const dim3 grid((kv_lora + 15) / 16 + (nb + 15) / 16, (n_heads + 15) / 16);
     hipLaunchKernelGGL(context_kernel, grid, dim3(kCThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+size_t mla_attend_lds(int max_seq, int kv_lora, int qk_rope) {
+    return sizeof(float) * (static_cast<size_t>(max_seq) + kv_lora + qk_rope + (kv_lora + 31) / 32);
+}
+
+bool mla_attend_ok(int max_seq, int kv_lora, int qk_rope) {
+    return max_seq <= kAMaxSeq && mla_attend_lds(max_seq, kv_lora, qk_rope) + sizeof(float) * 2 * kCWaves +
+                                          sizeof(float) * kCWaves * 64 <= kMaxLds;
+}
+
+hipError_t mla_absorb_attend(const float *q_abs, const float *q, const uint8_t *cache, size_t crb, const float *delta,
+                             float *delta_out, const float *kv_cache, float *latent_out, int n_heads, int qk_nope,
+                             int qk_rope, int kv_lora, const int *d_pos, int max_seq, float scale, hipStream_t s) {
+    if (n_heads == 0) return hipSuccess;
+    const ScoreArgs a{q_abs, q, cache, crb, delta, kv_cache, nullptr, n_heads, qk_nope, qk_rope, kv_lora, max_seq,
+                      d_pos, scale};
+    hipLaunchKernelGGL(attend_kernel, dim3(n_heads), dim3(kCThreads), mla_attend_lds(max_seq, kv_lora, qk_rope), s, a,
+                       delta_out, latent_out);
     return hipGetLastError();
 }
 

@@ -67,6 +67,7 @@ SIGNATURES = {
     "qlin_launch_mla_store_latent_q8_1_device_pos": (I, [P, P, I, I, SZ, P]),
     "qlin_launch_mla_absorb_scores_device_pos": (I, [P, P, P, SZ, P, P, P, I, I, I, I, P, I, F]),
     "qlin_launch_mla_absorb_context_device_pos": (I, [P, P, SZ, P, P, I, I, P, I]),
+    "qlin_launch_mla_absorb_attend_device_pos": (I, [P, P, P, SZ, P, P, P, P, I, I, I, I, P, I, F]),
     "qlin_launch_mla_project_v_device_pos": (I, [I, P, SZ, P, SZ, P, I, I, I, I, P]),
     "qlin_launch_mla_absorb_context_v_device_pos": (I, [P, P, P, I, I, I, P, I]),
     # include/qlin_gguf.h

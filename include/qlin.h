@@ -238,6 +238,16 @@ int qlin_launch_mla_absorb_context_device_pos(const float *scores, const uint8_t
                                               size_t latent_row_bytes, float *attn_xsum_delta, float *attn_latent,
                                               int n_heads, int kv_lora, const int *d_pos, int max_seq_len);
 
+/* The scores, softmax and context above in one launch, with the fast exp (__expf) and no 1e-9 in the
+ * denominator; the scores of every position stay on chip, so max_seq_len <= 32768 (and the LDS of
+ * max_seq_len + kv_lora + qk_rope + ceil(kv_lora / 32) floats fits).
+ * Replaces launch_mla_absorb_attend_device_pos (launch.cu:964-975). */
+int qlin_launch_mla_absorb_attend_device_pos(const float *q_abs, const float *q, const uint8_t *latent_q8_1_cache,
+                                             size_t latent_row_bytes, const float *q_abs_xsum_delta,
+                                             float *attn_xsum_delta, const float *kv_cache, float *attn_latent,
+                                             int n_heads, int qk_nope, int qk_rope, int kv_lora, const int *d_pos,
+                                             int max_seq_len, float softmax_scale);
+
 /* kv_b_cache[pos, r] = W_kv_b[r] . cache[pos] (Q8_1 block-dot semantics of quant_matmul_q8_1) for the
  * v rows r = h * (qk_nope + v_head) + qk_nope + v of every head.  Types Q4_K, Q6_K, Q5_0, Q8_0.
  * Replaces launch_mla_project_v_device_pos (launch.cu:1015-1040). */

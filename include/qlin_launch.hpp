@@ -191,6 +191,16 @@ inline void launch_mla_absorb_context_device_pos(const float *scores, const uint
                                                     attn_latent, n_heads, kv_lora, d_pos, max_seq_len),
           "launch_mla_absorb_context_device_pos");
 }
+inline void launch_mla_absorb_attend_device_pos(const float *q_abs, const float *q, const uint8_t *latent_q8_1_cache,
+                                                size_t latent_q8_1_row_bytes, const float *q_abs_xsum_delta,
+                                                float *attn_xsum_delta, const float *kv_cache, float *attn_latent,
+                                                int n_heads, int qk_nope, int qk_rope, int kv_lora, const int *d_pos,
+                                                int max_seq_len, float softmax_scale) {
+    check(qlin_launch_mla_absorb_attend_device_pos(q_abs, q, latent_q8_1_cache, latent_q8_1_row_bytes,
+                                                   q_abs_xsum_delta, attn_xsum_delta, kv_cache, attn_latent, n_heads,
+                                                   qk_nope, qk_rope, kv_lora, d_pos, max_seq_len, softmax_scale),
+          "launch_mla_absorb_attend_device_pos");
+}
 inline void launch_mla_project_v_device_pos(DType quant_type, const uint8_t *kv_b_weight, size_t row_bytes,
                                             const uint8_t *latent_q8_1_cache, size_t latent_q8_1_row_bytes,
                                             float *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora,

@@ -74,6 +74,7 @@ def _declare(L: C.CDLL) -> None:
         "orc_mla_store_latent_q8_1": (I, [P, P, I, I, SZ, I]),
         "orc_mla_absorb_scores": (I, [P, P, P, SZ, P, P, P, I, I, I, I, I, I, C.c_float]),
         "orc_mla_absorb_context": (I, [P, P, SZ, P, P, I, I, I, I]),
+        "orc_mla_absorb_attend": (I, [P, P, P, SZ, P, P, P, P, I, I, I, I, I, I, C.c_float]),
         "orc_mla_project_v": (I, [I, P, SZ, P, SZ, P, I, I, I, I, I]),
         "orc_mla_absorb_context_v": (I, [P, P, P, I, I, I, I, I]),
     }
@@ -311,3 +312,15 @@ def mla_absorb_context_v(scores, kv_b_cache, n_heads, qk_nope, v_head, pos, max_
     _ok(lib().orc_mla_absorb_context_v(_p(scores), _p(kvb), _p(out), n_heads, qk_nope, v_head, pos, max_seq),
         "orc_mla_absorb_context_v")
     return out
+
+
+def mla_absorb_attend(q_abs, q, cache, crb, delta, kv_cache, n_heads, qk_nope, qk_rope, kv_lora, pos, max_seq, scale):
+    """(attn_latent, attn_xsum_delta) of the fused form (softmax without the 1e-9 term), float64."""
+    args = [np.ascontiguousarray(a, np.float32) for a in (q_abs, q, delta, kv_cache)]
+    cache = np.ascontiguousarray(cache, np.uint8)
+    lat = np.zeros((n_heads, kv_lora), np.float64)
+    dl = np.zeros((n_heads, (kv_lora + 31) // 32), np.float64)
+    _ok(lib().orc_mla_absorb_attend(_p(args[0]), _p(args[1]), _p(cache), crb, _p(args[2]), _p(dl), _p(args[3]),
+                                    _p(lat), n_heads, qk_nope, qk_rope, kv_lora, pos, max_seq, scale),
+        "orc_mla_absorb_attend")
+    return lat, dl

@@ -697,6 +697,35 @@ int orc_mla_absorb_context(const float *scores, const uint8_t *cache, size_t crb
     return 0;
 }
 
+int orc_mla_absorb_attend(const float *q_abs, const float *q, const uint8_t *cache, size_t crb, const float *delta,
+                          double *delta_out, const float *kv_cache, double *latent_out, int n_heads, int qk_nope,
+                          int qk_rope, int kv_lora, int pos, int max_seq, float scale) {
+    /* kernel.cu:3078-3155: the scores of kernel.cu:3157-3196, exp(s - max) / sum (no 1e-9), the context */
+    const int nb = (kv_lora + 31) / 32;
+    if (pos >= max_seq) pos = max_seq - 1;
+    double *sc = (double *)malloc(sizeof(double) * (size_t)n_heads * (size_t)max_seq + 1);
+    if (!sc) return -1;
+    orc_mla_absorb_scores(q_abs, q, cache, crb, delta, kv_cache, sc, n_heads, qk_nope, qk_rope, kv_lora, pos, max_seq,
+                          scale);
+    for (int h = 0; h < n_heads; ++h) {
+        double *p = sc + (size_t)h * max_seq, mx = -INFINITY, den = 0.0;
+        for (int t = 0; t <= pos; ++t) mx = p[t] > mx ? p[t] : mx;
+        for (int t = 0; t <= pos; ++t) den += (p[t] = exp(p[t] - mx));
+        for (int k = 0; k < kv_lora; ++k) {
+            double acc = 0.0;
+            for (int t = 0; t <= pos; ++t) acc += p[t] / den * latent_at(cache + (size_t)t * crb, k);
+            latent_out[(size_t)h * kv_lora + k] = acc;
+        }
+        for (int b = 0; b < nb; ++b) {
+            double acc = 0.0;
+            for (int t = 0; t <= pos; ++t) acc += p[t] / den * latent_sum_delta(cache + (size_t)t * crb, b, kv_lora);
+            delta_out[(size_t)h * nb + b] = acc;
+        }
+    }
+    free(sc);
+    return 0;
+}
+
 int orc_mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_t *cache, size_t crb,
                       double *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora, int pos) {
     /* kernel.cu:3259-3361: each v row of kv_b against the latent row, with the block-dot semantics

@@ -161,6 +161,10 @@ int orc_mla_absorb_scores(const float *q_abs, const float *q, const uint8_t *cac
                           int qk_rope, int kv_lora, int pos, int max_seq, float scale);
 int orc_mla_absorb_context(const float *scores, const uint8_t *cache, size_t cache_row_bytes, double *delta_out,
                            double *latent_out, int n_heads, int kv_lora, int pos, int max_seq);
+/* attend: scores, then the softmax without the 1e-9 term, then the context (kernel.cu:3078-3155). */
+int orc_mla_absorb_attend(const float *q_abs, const float *q, const uint8_t *cache, size_t cache_row_bytes,
+                          const float *delta, double *delta_out, const float *kv_cache, double *latent_out,
+                          int n_heads, int qk_nope, int qk_rope, int kv_lora, int pos, int max_seq, float scale);
 int orc_mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_t *cache, size_t cache_row_bytes,
                       double *kv_b_cache, int n_heads, int qk_nope, int v_head, int kv_lora, int pos);
 int orc_mla_absorb_context_v(const float *scores, const float *kv_b_cache, double *attn, int n_heads, int qk_nope,

@@ -221,6 +221,10 @@ def test_mla_latent_cache_validation():
     assert qlin.status(X, FAKE, FAKE, 576, FAKE, FAKE, 16, 512, FAKE, 0) == SHAPE
     assert qlin.status(X, FAKE, FAKE, 500, FAKE, FAKE, 16, 512, FAKE, 256) == ROWB
     assert qlin.status(X, FAKE, FAKE, 576, 0, FAKE, 16, 512, FAKE, 256) == NULL
+    A = "qlin_launch_mla_absorb_attend_device_pos"
+    assert qlin.status(A, FAKE, FAKE, FAKE, 576, FAKE, FAKE, FAKE, FAKE, 16, 128, 64, 512, FAKE, 32769, 0.1) == LIMIT
+    assert qlin.status(A, FAKE, FAKE, FAKE, 576, FAKE, 0, FAKE, FAKE, 16, 128, 64, 512, FAKE, 4096, 0.1) == NULL
+    assert qlin.status(A, 0, 0, 0, 0, 0, 0, 0, 0, 0, 128, 64, 512, 0, 4096, 0.1) == OK
     P_ = "qlin_launch_mla_project_v_device_pos"
     assert qlin.status(P_, 2, FAKE, 18, FAKE, 576, FAKE, 16, 128, 128, 512, FAKE) == UNSUP
     assert qlin.status(P_, 12, FAKE, 288, FAKE, 576, FAKE, 16, 128, 128, 500, FAKE) == SHAPE

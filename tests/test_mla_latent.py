@@ -105,6 +105,24 @@ def test_oracle_scores_context_against_numpy():
     assert np.allclose(lat_c, softmax64(s, T - 1) @ L.astype(np.float64), rtol=1e-9, atol=1e-12)
 
 
+def test_oracle_attend_against_numpy():
+    """The fused form: numpy scores, a softmax without the 1e-9 term, the weighted rows."""
+    T, pos = 24, 17
+    kv, cache, crb = make_cache(T, KL, QR, 13)
+    rng = np.random.default_rng(14)
+    q_abs = rng.standard_normal((NH, KL)).astype(np.float32) * 0.1
+    q = rng.standard_normal((NH, QN + QR)).astype(np.float32)
+    delta = rng.standard_normal((NH, KL // 32)).astype(np.float32)
+    L, C = decode_q8_1(cache, KL)
+    s = (q_abs.astype(np.float64) @ L.T.astype(np.float64) + q[:, QN:].astype(np.float64) @ kv[:, KL:].T
+         + delta.astype(np.float64) @ C.T.astype(np.float64))[:, :pos + 1] * np.float32(SCALE)
+    e = np.exp(s - s.max(axis=1, keepdims=True))
+    p = e / e.sum(axis=1, keepdims=True)
+    lat, dl = orc.mla_absorb_attend(q_abs, q, cache, crb, delta, kv, NH, QN, QR, KL, pos, T, SCALE)
+    assert np.allclose(lat, p @ L[:pos + 1].astype(np.float64), rtol=1e-9, atol=1e-12)
+    assert np.allclose(dl, p @ C[:pos + 1].astype(np.float64), rtol=1e-9, atol=1e-12)
+
+
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q5_0, Q8_0])
 def test_oracle_project_v(qtype):
     w, rb, vals = qgen.random_matrix(qtype, NH * (QN + VH), KL, seed=70 + qtype)
@@ -191,6 +209,25 @@ def test_scores_and_context(n_heads, T, pos):
     lat_d, dl_d = empty_f32(n_heads, KL), empty_f32(n_heads, KL // 32)
     qlin.call("qlin_launch_mla_absorb_context_device_pos", sd, cd, crb, dl_d, lat_d, n_heads, KL, _pos(pos), T)
     lat, dl = orc.mla_absorb_context(got, cache, crb, n_heads, KL, pos, T)
+    assert normwise_rel_err(host(lat_d), lat) <= 1e-5
+    assert normwise_rel_err(host(dl_d), dl) <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,pos", [(256, 0), (256, 255), (1024, 700)])
+def test_attend_fused(T, pos):
+    from gpu_util import banner, bind_stream, dev, empty_f32, host
+    kv, cache, crb = make_cache(T, KL, QR, 130 + pos)
+    rng = np.random.default_rng(131 + pos)
+    q_abs = rng.standard_normal((NH, KL)).astype(np.float32) * 0.05
+    q = rng.standard_normal((NH, QN + QR)).astype(np.float32) * 0.5
+    delta = rng.standard_normal((NH, KL // 32)).astype(np.float32)
+    banner(f"mla attend T={T} pos={pos}")
+    bind_stream()
+    lat_d, dl_d = empty_f32(NH, KL), empty_f32(NH, KL // 32)
+    qlin.call("qlin_launch_mla_absorb_attend_device_pos", dev(q_abs), dev(q), dev(cache), crb, dev(delta), dl_d,
+              dev(kv), lat_d, NH, QN, QR, KL, _pos(pos), T, SCALE)
+    lat, dl = orc.mla_absorb_attend(q_abs, q, cache, crb, delta, kv, NH, QN, QR, KL, pos, T, SCALE)
     assert normwise_rel_err(host(lat_d), lat) <= 1e-5
     assert normwise_rel_err(host(dl_d), dl) <= 1e-5
 
