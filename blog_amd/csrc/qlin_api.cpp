@@ -200,6 +200,34 @@ int qlin_launch_quant_matmul_q8_1(int type, const uint8_t *w, size_t rb, const u
     return launched(qlin::matmul_q8_1(type, w, rb, xq, y, out_dim, in_dim, m, stream()));
 }
 
+int qlin_launch_quant_gemv_q8_1(int type, const uint8_t *w, size_t rb, const uint8_t *xq, float *y, int out_dim,
+                                int in_dim) {
+    return qlin_launch_quant_matmul_q8_1(type, w, rb, xq, y, out_dim, in_dim, 1);
+}
+
+int qlin_launch_quantize_q8_1_mmq(const float *x, uint8_t *xq, int in_dim, int m, int store_raw_sum) {
+    if (in_dim <= 0 || m < 0) return QLIN_ERR_SHAPE;
+    if (m == 0) return QLIN_OK;
+    int rc = check_f32(x, true);
+    if (rc) return rc;
+    if (!xq) return QLIN_ERR_NULL;
+    if (!aligned(xq, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::quantize_q8_1_mmq(x, xq, in_dim, m, store_raw_sum != 0, stream()));
+}
+
+int qlin_launch_quant_matmul_q8_1_mmq(int type, const uint8_t *w, size_t rb, const uint8_t *xq, float *y,
+                                      int out_dim, int in_dim, int m) {
+    if (type != QLIN_TYPE_Q4_K && type != QLIN_TYPE_Q6_K) return QLIN_ERR_UNSUPPORTED_TYPE;
+    int rc = check_weight(type, w, rb, out_dim, in_dim);
+    if (rc) return rc;
+    if (m < 0) return QLIN_ERR_SHAPE;
+    if (out_dim == 0 || m == 0) return QLIN_OK;
+    if (!xq) return QLIN_ERR_NULL;
+    if (!aligned(xq, 4)) return QLIN_ERR_ALIGN;
+    if ((rc = check_f32(y, true))) return rc;
+    return launched(qlin::matmul_q8_1_mmq(type, w, rb, xq, y, out_dim, in_dim, m, stream()));
+}
+
 int qlin_launch_quant_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_rb, size_t u_rb,
                              const float *x, float *act, int ffn_dim, int in_dim) {
     int rc = check_weight(type, wg, g_rb, ffn_dim, in_dim);
@@ -243,6 +271,77 @@ int qlin_launch_quant_swiglu_indexed(int type, const uint8_t *wg, const uint8_t 
     if (!aligned(ids, 4)) return QLIN_ERR_ALIGN;
     return launched(qlin::swiglu_indexed(type, wg, wu, g_eb, u_eb, g_rb, u_rb, x, ids, act, k, ffn_dim, in_dim,
                                          stream()));
+}
+
+// gate/up of the experimental routed SwiGLU variants: Q4_K or Q6_K (launch.cu:262-318)
+static int check_swiglu_experts(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb, size_t g_rb,
+                                size_t u_rb, int k, int ffn_dim, int in_dim) {
+    if (type != QLIN_TYPE_Q4_K && type != QLIN_TYPE_Q6_K) return QLIN_ERR_UNSUPPORTED_TYPE;
+    int rc = check_weight(type, wg, g_rb, ffn_dim, in_dim);
+    if (rc || (rc = check_weight(type, wu, u_rb, ffn_dim, in_dim))) return rc;
+    if (k < 0) return QLIN_ERR_SHAPE;
+    if (g_eb < g_rb * static_cast<size_t>(ffn_dim) || u_eb < u_rb * static_cast<size_t>(ffn_dim))
+        return QLIN_ERR_ROW_BYTES;
+    return QLIN_OK;
+}
+
+int qlin_launch_quant_swiglu_indexed_block(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb,
+                                           size_t g_rb, size_t u_rb, const float *x, const int *ids, float *act, int k,
+                                           int ffn_dim, int in_dim, int fast_silu) {
+    (void)fast_silu;  // unused by the reference kernel as well (kernel.cu:1400)
+    int rc = check_swiglu_experts(type, wg, wu, g_eb, u_eb, g_rb, u_rb, k, ffn_dim, in_dim);
+    if (rc) return rc;
+    return qlin_launch_quant_swiglu_indexed(type, wg, wu, g_eb, u_eb, g_rb, u_rb, x, ids, act, k, ffn_dim, in_dim);
+}
+
+int qlin_launch_quant_swiglu_indexed_q8_1(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb,
+                                          size_t g_rb, size_t u_rb, const uint8_t *xq, const int *ids, float *act,
+                                          int k, int ffn_dim, int in_dim) {
+    int rc = check_swiglu_experts(type, wg, wu, g_eb, u_eb, g_rb, u_rb, k, ffn_dim, in_dim);
+    if (rc) return rc;
+    const bool work = ffn_dim > 0 && k > 0;
+    if ((rc = check_f32(act, work))) return rc;
+    if (!work) return QLIN_OK;
+    if (!xq || !ids) return QLIN_ERR_NULL;
+    if (!aligned(xq, 2) || !aligned(ids, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::swiglu_indexed_q8_1(type, wg, wu, g_eb, u_eb, g_rb, u_rb, xq, ids, act, k, ffn_dim, in_dim,
+                                              stream()));
+}
+
+static int down_q8_1_common(int type, bool f32_act, const uint8_t *wd, size_t d_eb, size_t d_rb, const void *act,
+                            const int *ids, const float *rw, float *out, int k, int hidden, int ffn_dim) {
+    if (type != QLIN_TYPE_Q4_K && type != QLIN_TYPE_Q6_K && type != QLIN_TYPE_Q5_0 && type != QLIN_TYPE_Q8_0)
+        return QLIN_ERR_UNSUPPORTED_TYPE;
+    int rc = check_weight(type, wd, d_rb, hidden, ffn_dim);
+    if (rc) return rc;
+    if (k < 0) return QLIN_ERR_SHAPE;
+    if (d_eb < d_rb * static_cast<size_t>(hidden)) return QLIN_ERR_ROW_BYTES;
+    if (f32_act && static_cast<size_t>(ffn_dim / 32) * 36 > 160 * 1024) return QLIN_ERR_LIMIT;
+    const bool work = hidden > 0 && k > 0;
+    if ((rc = check_f32(out, hidden > 0)) || (rc = check_f32(rw, work))) return rc;
+    if (!work) return QLIN_OK;
+    if (!act || !ids) return QLIN_ERR_NULL;
+    if (!aligned(act, f32_act ? 4 : 2) || !aligned(ids, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::down_q8_1_indexed_accum(type, f32_act, wd, d_eb, d_rb, act, ids, rw, out, k, hidden, ffn_dim,
+                                                  stream()));
+}
+
+int qlin_launch_quant_down_q8_1_indexed_accum(int type, const uint8_t *wd, size_t d_eb, size_t d_rb,
+                                              const uint8_t *act_q8_1, const int *ids, const float *rw, float *out,
+                                              int k, int hidden, int ffn_dim) {
+    return down_q8_1_common(type, false, wd, d_eb, d_rb, act_q8_1, ids, rw, out, k, hidden, ffn_dim);
+}
+
+int qlin_launch_quant_down_q8_1_indexed_accum_shared(int type, const uint8_t *wd, size_t d_eb, size_t d_rb,
+                                                     const uint8_t *act_q8_1, const int *ids, const float *rw,
+                                                     float *out, int k, int hidden, int ffn_dim) {
+    return down_q8_1_common(type, false, wd, d_eb, d_rb, act_q8_1, ids, rw, out, k, hidden, ffn_dim);
+}
+
+int qlin_launch_quant_down_f32_indexed_accum(int type, const uint8_t *wd, size_t d_eb, size_t d_rb, const float *act,
+                                             const int *ids, const float *rw, float *out, int k, int hidden,
+                                             int ffn_dim) {
+    return down_q8_1_common(type, true, wd, d_eb, d_rb, act, ids, rw, out, k, hidden, ffn_dim);
 }
 
 int qlin_launch_quant_down_f32_indexed_accum_ordered(int type, const uint8_t *wd, size_t d_eb, size_t d_rb,

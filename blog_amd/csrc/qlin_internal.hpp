@@ -82,6 +82,18 @@ hipError_t q4k_gemm_q8_1(const uint8_t *w, size_t row_bytes, const uint8_t *xq, 
 hipError_t matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y,
                        int out_dim, int in_dim, int m, hipStream_t s);
 
+// Q8_1-activation variants (qlin_q8_1_moe.hip): the MMQ layout, the MoE SwiGLU over one Q8_1 x and
+// the routed down projections over Q8_1 (or f32, quantized on the fly) activations.
+hipError_t quantize_q8_1_mmq(const float *x, uint8_t *xq, int in_dim, int m, bool raw_sum, hipStream_t s);
+hipError_t matmul_q8_1_mmq(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y, int out_dim,
+                           int in_dim, int m, hipStream_t s);
+hipError_t swiglu_indexed_q8_1(int type, const uint8_t *wg, const uint8_t *wu, size_t g_expert_bytes,
+                               size_t u_expert_bytes, size_t g_row_bytes, size_t u_row_bytes, const uint8_t *xq,
+                               const int *expert_ids, float *act, int k, int ffn_dim, int in_dim, hipStream_t s);
+hipError_t down_q8_1_indexed_accum(int type, bool f32_act, const uint8_t *wd, size_t d_expert_bytes,
+                                   size_t d_row_bytes, const void *act, const int *expert_ids, const float *route_w,
+                                   float *out, int k, int hidden, int ffn_dim, hipStream_t s);
+
 // MoE.
 hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts,
                        int k, float routed_scaling, hipStream_t s);

@@ -16,8 +16,11 @@
 
 namespace qlin {
 
-// One Q8_1 block from src[0 .. valid) (values past valid are 0) into the 36 bytes at dst (4-aligned).
-__device__ __forceinline__ void quantize_block_q8_1(const float *src, int valid, uint8_t *dst, bool raw) {
+// One Q8_1 block from src[0 .. valid) (values past valid are 0): (d, s) as two f16 into the dword at
+// ds, the 32 int8 q into the 8 dwords at q8 (the contiguous 36-byte block has q8 = ds + 1; the
+// group-major MMQ layout keeps them apart).
+__device__ __forceinline__ void quantize_block_q8_1(const float *src, int valid, uint32_t *ds, uint32_t *q8,
+                                                    bool raw) {
     float v[32], t[32];
     float amax = 0.0f;
 #pragma unroll
@@ -47,17 +50,20 @@ __device__ __forceinline__ void quantize_block_q8_1(const float *src, int valid,
         packed[w] = word;
     }
     const float sum = raw ? t[0] : __fmul_rn(d, static_cast<float>(qsum));
-    uint32_t *out = reinterpret_cast<uint32_t *>(dst);
-    out[0] = f32_to_f16_bits(d) | (f32_to_f16_bits(sum) << 16);
+    *ds = f32_to_f16_bits(d) | (f32_to_f16_bits(sum) << 16);
 #pragma unroll
-    for (int w = 0; w < 8; ++w) out[1 + w] = packed[w];
+    for (int w = 0; w < 8; ++w) q8[w] = packed[w];
 }
 
+// The same into a contiguous 36-byte block at dst (4-aligned).
+__device__ __forceinline__ void quantize_block_q8_1(const float *src, int valid, uint8_t *dst, bool raw) {
+    uint32_t *out = reinterpret_cast<uint32_t *>(dst);
+    quantize_block_q8_1(src, valid, out, out + 1, raw);
+}
+
+// Block qb of a weight row against activation block (dx, sx, qx[32]).
 template <int T>
-__device__ __forceinline__ float block_dot_q8_1(const uint8_t *row, int qb, const uint8_t *xb) {
-    const float dx = f16_bits_to_f32(ld_u16(xb));
-    const float sx = f16_bits_to_f32(ld_u16(xb + 2));
-    const int8_t *qx = reinterpret_cast<const int8_t *>(xb + 4);
+__device__ __forceinline__ float block_dot_q8_1(const uint8_t *row, int qb, float dx, float sx, const int8_t *qx) {
     if constexpr (T == T_Q4_K) {
         const uint8_t *sb = row + static_cast<size_t>(qb >> 3) * 144;
         const int j = qb & 7;
@@ -97,6 +103,13 @@ __device__ __forceinline__ float block_dot_q8_1(const uint8_t *row, int qb, cons
         for (int l = 0; l < 32; ++l) acc = fmaf(block_value<T>(b, l), dx * static_cast<float>(qx[l]), acc);
         return acc;
     }
+}
+
+// ... against the contiguous 36-byte block at xb.
+template <int T>
+__device__ __forceinline__ float block_dot_q8_1(const uint8_t *row, int qb, const uint8_t *xb) {
+    return block_dot_q8_1<T>(row, qb, f16_bits_to_f32(ld_u16(xb)), f16_bits_to_f32(ld_u16(xb + 2)),
+                             reinterpret_cast<const int8_t *>(xb + 4));
 }
 
 }  // namespace qlin

@@ -41,6 +41,14 @@ SIGNATURES = {
     "qlin_launch_quant_gemv_add": (I, [I, P, SZ, P, P, I, I]),
     "qlin_launch_quant_matmul": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_launch_quant_matmul_add": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_gemv_q8_1": (I, [I, P, SZ, P, P, I, I]),
+    "qlin_launch_quantize_q8_1_mmq": (I, [P, P, I, I, I]),
+    "qlin_launch_quant_matmul_q8_1_mmq": (I, [I, P, SZ, P, P, I, I, I]),
+    "qlin_launch_quant_swiglu_indexed_block": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I, I]),
+    "qlin_launch_quant_swiglu_indexed_q8_1": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
+    "qlin_launch_quant_down_q8_1_indexed_accum": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
+    "qlin_launch_quant_down_q8_1_indexed_accum_shared": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
+    "qlin_launch_quant_down_f32_indexed_accum": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
     "qlin_launch_quant_swiglu_rows": (I, [I, P, P, SZ, SZ, P, P, I, I, I]),
     "qlin_launch_quant_gemv_multi": (I, [I, I, P, SZ, P, P, P, I]),
     "qlin_q8_1_row_bytes": (SZ, [I]),

@@ -113,6 +113,20 @@ int qlin_launch_quantize_q8_1(const float *x, uint8_t *x_q8_1, int in_dim, int m
 int qlin_launch_quant_matmul_q8_1(int type, const uint8_t *weight, size_t row_bytes, const uint8_t *x_q8_1,
                                   float *y, int out_dim, int in_dim, int m);
 
+/* qlin_launch_quant_matmul_q8_1 for one row.  Replaces launch_quant_gemv_q8_1 (launch.cu:226-246). */
+int qlin_launch_quant_gemv_q8_1(int type, const uint8_t *weight, size_t row_bytes, const uint8_t *x_q8_1, float *y,
+                                int out_dim, int in_dim);
+
+/* Q8_1 blocks in the group-major MMQ layout: the ceil(in_dim / 128) groups of 128 values of row r
+ * at (g * m + r) * 144 bytes = 4 x (d f16, s f16) then 4 x 32 int8 (values past in_dim are 0).
+ * Replaces launch_quantize_q8_1_mmq (launch.cu:209-215). */
+int qlin_launch_quantize_q8_1_mmq(const float *x, uint8_t *x_q8_1, int in_dim, int m, int store_raw_sum);
+
+/* y[r, o] = W[o] . x_q8_1[r] from the MMQ layout, block-dot semantics; Q4_K and Q6_K.
+ * Replaces launch_quant_matmul_q8_1_mmq (launch.cu:546-560). */
+int qlin_launch_quant_matmul_q8_1_mmq(int type, const uint8_t *weight, size_t row_bytes, const uint8_t *x_q8_1,
+                                      float *y, int out_dim, int in_dim, int m);
+
 /* ---- MoE decode (kernel.cuh:62-129, 335-336) --------------------------------------------------- */
 
 /* act[o] = silu(Wg[o].x) * (Wu[o].x).  Replaces launch_quant_swiglu (launch.cu:132-154). */
@@ -133,6 +147,44 @@ int qlin_launch_quant_swiglu_indexed(int type, const uint8_t *gate_weight, const
                                      size_t gate_expert_bytes, size_t up_expert_bytes,
                                      size_t gate_row_bytes, size_t up_row_bytes, const float *x,
                                      const int *expert_ids, float *act, int k, int ffn_dim, int in_dim);
+
+/* The reference's block-factored form of qlin_launch_quant_swiglu_indexed (the same contraction,
+ * Q4_K and Q6_K; fast_silu is ignored, as the reference kernel ignores it).
+ * Replaces launch_quant_swiglu_indexed_block (launch.cu:262-283). */
+int qlin_launch_quant_swiglu_indexed_block(int type, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                           size_t gate_expert_bytes, size_t up_expert_bytes, size_t gate_row_bytes,
+                                           size_t up_row_bytes, const float *x, const int *expert_ids, float *act,
+                                           int k, int ffn_dim, int in_dim, int fast_silu);
+
+/* act[r, o] = silu(Wg[e_r][o] . x_q8_1) * (Wu[e_r][o] . x_q8_1) (block-dot semantics, one Q8_1 row
+ * x shared by the routes; id < 0 writes 0); Q4_K and Q6_K.
+ * Replaces launch_quant_swiglu_indexed_q8_1 (launch.cu:298-318). */
+int qlin_launch_quant_swiglu_indexed_q8_1(int type, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                          size_t gate_expert_bytes, size_t up_expert_bytes, size_t gate_row_bytes,
+                                          size_t up_row_bytes, const uint8_t *x_q8_1, const int *expert_ids,
+                                          float *act, int k, int ffn_dim, int in_dim);
+
+/* out[h] += route_weights[r] * (Wd[e_r][h] . act_q8_1[r]) for each route with e_r >= 0, act_q8_1 k
+ * Q8_1 rows of ffn_dim; the routes are added in route order (the reference adds them with atomics
+ * in any order, of which this is one).  Replaces launch_quant_down_q8_1_indexed_accum (launch.cu:333-364). */
+int qlin_launch_quant_down_q8_1_indexed_accum(int type, const uint8_t *down_weight, size_t down_expert_bytes,
+                                              size_t down_row_bytes, const uint8_t *act_q8_1, const int *expert_ids,
+                                              const float *route_weights, float *out, int k, int hidden_size,
+                                              int ffn_dim);
+
+/* The same contraction.  Replaces launch_quant_down_q8_1_indexed_accum_shared (launch.cu:379-409). */
+int qlin_launch_quant_down_q8_1_indexed_accum_shared(int type, const uint8_t *down_weight, size_t down_expert_bytes,
+                                                     size_t down_row_bytes, const uint8_t *act_q8_1,
+                                                     const int *expert_ids, const float *route_weights, float *out,
+                                                     int k, int hidden_size, int ffn_dim);
+
+/* The same from f32 act [k, ffn_dim]: each route's act is quantized to Q8_1 (s = d * sum(q)) and
+ * then dotted; (ffn_dim / 32) * 36 bytes must fit the 160 KiB of LDS.
+ * Replaces launch_quant_down_f32_indexed_accum (launch.cu:425-455). */
+int qlin_launch_quant_down_f32_indexed_accum(int type, const uint8_t *down_weight, size_t down_expert_bytes,
+                                             size_t down_row_bytes, const float *act, const int *expert_ids,
+                                             const float *route_weights, float *out, int k, int hidden_size,
+                                             int ffn_dim);
 
 /* out[h] += sum_r route_weights[r] * (Wd[e_r][h] . act[r]), routes in order, negative ids skipped.
  * Replaces launch_quant_down_f32_indexed_accum_ordered (launch.cu:469-498). */

@@ -87,6 +87,19 @@ inline void launch_quant_matmul_q8_1(DType t, const uint8_t *weight, size_t row_
     check(qlin_launch_quant_matmul_q8_1(static_cast<int>(t), weight, row_bytes, x_q8_1, y, out_dim, in_dim, m),
           "launch_quant_matmul_q8_1");
 }
+inline void launch_quant_gemv_q8_1(DType t, const uint8_t *weight, size_t row_bytes, const uint8_t *x_q8_1, float *y,
+                                   int out_dim, int in_dim) {
+    check(qlin_launch_quant_gemv_q8_1(static_cast<int>(t), weight, row_bytes, x_q8_1, y, out_dim, in_dim),
+          "launch_quant_gemv_q8_1");
+}
+inline void launch_quantize_q8_1_mmq(const float *x, uint8_t *x_q8_1, int in_dim, int m, bool store_raw_sum = false) {
+    check(qlin_launch_quantize_q8_1_mmq(x, x_q8_1, in_dim, m, store_raw_sum ? 1 : 0), "launch_quantize_q8_1_mmq");
+}
+inline void launch_quant_matmul_q8_1_mmq(DType t, const uint8_t *weight, size_t row_bytes, const uint8_t *x_q8_1,
+                                         float *y, int out_dim, int in_dim, int m) {
+    check(qlin_launch_quant_matmul_q8_1_mmq(static_cast<int>(t), weight, row_bytes, x_q8_1, y, out_dim, in_dim, m),
+          "launch_quant_matmul_q8_1_mmq");
+}
 
 // kernel.cuh:62-129
 inline void launch_quant_swiglu(DType t, const uint8_t *gate_weight, const uint8_t *up_weight,
@@ -114,6 +127,50 @@ inline void launch_quant_down_f32_indexed_accum_ordered(DType t, const uint8_t *
                                                            down_row_bytes, act, expert_ids, route_weights, out, k,
                                                            hidden_size, ffn_dim),
           "launch_quant_down_f32_indexed_accum_ordered");
+}
+inline void launch_quant_swiglu_indexed_block(DType t, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                              size_t gate_expert_bytes, size_t up_expert_bytes, size_t gate_row_bytes,
+                                              size_t up_row_bytes, const float *x, const int *expert_ids, float *act,
+                                              int k, int ffn_dim, int in_dim, bool fast_silu = false) {
+    check(qlin_launch_quant_swiglu_indexed_block(static_cast<int>(t), gate_weight, up_weight, gate_expert_bytes,
+                                                 up_expert_bytes, gate_row_bytes, up_row_bytes, x, expert_ids, act, k,
+                                                 ffn_dim, in_dim, fast_silu ? 1 : 0),
+          "launch_quant_swiglu_indexed_block");
+}
+inline void launch_quant_swiglu_indexed_q8_1(DType t, const uint8_t *gate_weight, const uint8_t *up_weight,
+                                             size_t gate_expert_bytes, size_t up_expert_bytes, size_t gate_row_bytes,
+                                             size_t up_row_bytes, const uint8_t *x_q8_1, const int *expert_ids,
+                                             float *act, int k, int ffn_dim, int in_dim) {
+    check(qlin_launch_quant_swiglu_indexed_q8_1(static_cast<int>(t), gate_weight, up_weight, gate_expert_bytes,
+                                                up_expert_bytes, gate_row_bytes, up_row_bytes, x_q8_1, expert_ids, act,
+                                                k, ffn_dim, in_dim),
+          "launch_quant_swiglu_indexed_q8_1");
+}
+inline void launch_quant_down_q8_1_indexed_accum(DType t, const uint8_t *down_weight, size_t down_expert_bytes,
+                                                 size_t down_row_bytes, const uint8_t *act_q8_1,
+                                                 const int *expert_ids, const float *route_weights, float *out, int k,
+                                                 int hidden_size, int ffn_dim) {
+    check(qlin_launch_quant_down_q8_1_indexed_accum(static_cast<int>(t), down_weight, down_expert_bytes,
+                                                    down_row_bytes, act_q8_1, expert_ids, route_weights, out, k,
+                                                    hidden_size, ffn_dim),
+          "launch_quant_down_q8_1_indexed_accum");
+}
+inline void launch_quant_down_q8_1_indexed_accum_shared(DType t, const uint8_t *down_weight, size_t down_expert_bytes,
+                                                        size_t down_row_bytes, const uint8_t *act_q8_1,
+                                                        const int *expert_ids, const float *route_weights, float *out,
+                                                        int k, int hidden_size, int ffn_dim) {
+    check(qlin_launch_quant_down_q8_1_indexed_accum_shared(static_cast<int>(t), down_weight, down_expert_bytes,
+                                                           down_row_bytes, act_q8_1, expert_ids, route_weights, out, k,
+                                                           hidden_size, ffn_dim),
+          "launch_quant_down_q8_1_indexed_accum_shared");
+}
+inline void launch_quant_down_f32_indexed_accum(DType t, const uint8_t *down_weight, size_t down_expert_bytes,
+                                                size_t down_row_bytes, const float *act, const int *expert_ids,
+                                                const float *route_weights, float *out, int k, int hidden_size,
+                                                int ffn_dim) {
+    check(qlin_launch_quant_down_f32_indexed_accum(static_cast<int>(t), down_weight, down_expert_bytes, down_row_bytes,
+                                                   act, expert_ids, route_weights, out, k, hidden_size, ffn_dim),
+          "launch_quant_down_f32_indexed_accum");
 }
 
 // kernel.cuh:335-336

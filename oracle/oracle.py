@@ -71,6 +71,11 @@ def _declare(L: C.CDLL) -> None:
         "orc_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
         "orc_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),
         "orc_mla_absorb_v": (I, [I, P, SZ, P, P, P, I, I, I, I]),
+        "orc_quantize_q8_1_mmq": (None, [P, P, I, I, I]),
+        "orc_matmul_q8_1_mmq": (I, [I, P, SZ, P, P, I, I, I]),
+        "orc_swiglu_indexed_q8_1": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
+        "orc_down_q8_1_indexed_accum": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
+        "orc_down_f32_indexed_accum": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
         "orc_mla_store_latent_q8_1": (I, [P, P, I, I, SZ, I]),
         "orc_mla_absorb_scores": (I, [P, P, P, SZ, P, P, P, I, I, I, I, I, I, C.c_float]),
         "orc_mla_absorb_context": (I, [P, P, SZ, P, P, I, I, I, I]),
@@ -324,3 +329,44 @@ def mla_absorb_attend(q_abs, q, cache, crb, delta, kv_cache, n_heads, qk_nope, q
                                     _p(lat), n_heads, qk_nope, qk_rope, kv_lora, pos, max_seq, scale),
         "orc_mla_absorb_attend")
     return lat, dl
+
+
+# ---- Q8_1-activation variants ----------------------------------------------------------------------
+def quantize_q8_1_mmq(x: np.ndarray, in_dim: int, store_raw_sum: bool = False) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    m = x.shape[0]
+    out = np.zeros(((in_dim + 127) // 128) * m * 144, np.uint8)
+    lib().orc_quantize_q8_1_mmq(_p(x), _p(out), in_dim, m, int(store_raw_sum))
+    return out
+
+
+def matmul_q8_1_mmq(qtype, w, rb, xq, out_dim, in_dim, m) -> np.ndarray:
+    xq = np.ascontiguousarray(xq, np.uint8)
+    y = np.empty((m, out_dim), np.float64)
+    _ok(lib().orc_matmul_q8_1_mmq(qtype, _p(w), rb, _p(xq), _p(y), out_dim, in_dim, m), "matmul_q8_1_mmq")
+    return y
+
+
+def swiglu_indexed_q8_1(qtype, wg, wu, g_eb, u_eb, g_rb, u_rb, xq, expert_ids, ffn_dim, in_dim) -> np.ndarray:
+    ids = np.ascontiguousarray(expert_ids, np.int32)
+    xq = np.ascontiguousarray(xq, np.uint8)
+    act = np.empty((ids.size, ffn_dim), np.float64)
+    _ok(lib().orc_swiglu_indexed_q8_1(qtype, _p(wg), _p(wu), g_eb, u_eb, g_rb, u_rb, _p(xq), _p(ids), _p(act),
+                                      ids.size, ffn_dim, in_dim), "swiglu_indexed_q8_1")
+    return act
+
+
+def down_q8_1_indexed_accum(qtype, wd, d_eb, d_rb, act, expert_ids, route_w, out, hidden, ffn_dim, f32_act=False):
+    """out (float64 copy) += the routed down products; act is Q8_1 bytes or, with f32_act, f32 rows."""
+    ids = np.ascontiguousarray(expert_ids, np.int32)
+    rw = np.ascontiguousarray(route_w, np.float32)
+    res = np.array(out, np.float64, copy=True)
+    if f32_act:
+        a = np.ascontiguousarray(act, np.float32)
+        fn = lib().orc_down_f32_indexed_accum
+    else:
+        a = np.ascontiguousarray(act, np.uint8)
+        fn = lib().orc_down_q8_1_indexed_accum
+    _ok(fn(qtype, _p(wd), d_eb, d_rb, _p(a), _p(ids), _p(rw), _p(res), ids.size, hidden, ffn_dim),
+        "down_q8_1_indexed_accum")
+    return res

@@ -613,6 +613,92 @@ int orc_mla_absorb_v(int type, const uint8_t *w, size_t row_bytes, const float *
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* Q8_1-activation variants -- kernel.cu:1532-1765, 1873-2242, 2405-2660                       */
+
+void orc_quantize_q8_1_mmq(const float *x, uint8_t *xq, int in_dim, int m, int store_raw_sum) {
+    /* the same blocks as orc_quantize_q8_1 over each row zero-padded to whole groups of 128 */
+    const int groups = (in_dim + 127) / 128, padded = groups * 128;
+    float *row = (float *)calloc((size_t)padded, sizeof(float));
+    uint8_t *blk = (uint8_t *)malloc((size_t)groups * 4 * 36);
+    if (!row || !blk) { free(row); free(blk); return; }
+    for (int r = 0; r < m; ++r) {
+        memcpy(row, x + (size_t)r * in_dim, sizeof(float) * (size_t)in_dim);
+        orc_quantize_q8_1(row, blk, padded, 1, store_raw_sum);
+        for (int g = 0; g < groups; ++g) {
+            uint8_t *dst = xq + ((size_t)g * m + r) * 144;
+            for (int sub = 0; sub < 4; ++sub) {
+                const uint8_t *b = blk + (size_t)(4 * g + sub) * 36;
+                memcpy(dst + 4 * sub, b, 4);
+                memcpy(dst + 16 + 32 * sub, b + 4, 32);
+            }
+        }
+    }
+    free(row);
+    free(blk);
+}
+
+int orc_matmul_q8_1_mmq(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y, int out_dim,
+                        int in_dim, int m) {
+    if (check_shape(type, in_dim) || m < 0) return -1;
+    const int bpr = in_dim / 32;
+    uint8_t *rows = (uint8_t *)malloc((size_t)(m > 0 ? m : 1) * bpr * 36);
+    if (!rows) return -1;
+    for (int r = 0; r < m; ++r)
+        for (int b = 0; b < bpr; ++b) {
+            const uint8_t *grp = xq + ((size_t)(b / 4) * m + r) * 144;
+            uint8_t *dst = rows + ((size_t)r * bpr + b) * 36;
+            memcpy(dst, grp + 4 * (b % 4), 4);
+            memcpy(dst + 4, grp + 16 + 32 * (b % 4), 32);
+        }
+    const int rc = orc_matmul_q8_1(type, w, row_bytes, rows, y, out_dim, in_dim, m);
+    free(rows);
+    return rc;
+}
+
+int orc_swiglu_indexed_q8_1(int type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t u_eb, size_t g_rb,
+                            size_t u_rb, const uint8_t *xq, const int *ids, double *act, int k, int ffn_dim,
+                            int in_dim) {
+    if (check_shape(type, in_dim)) return -1;
+    for (int r = 0; r < k; ++r)
+        for (int o = 0; o < ffn_dim; ++o) {
+            double g = 0.0, u = 0.0, *dst = act + (size_t)r * ffn_dim + o;
+            if (ids[r] < 0) { *dst = 0.0; continue; }
+            if (orc_matmul_q8_1(type, wg + (size_t)ids[r] * g_eb + (size_t)o * g_rb, g_rb, xq, &g, 1, in_dim, 1) ||
+                orc_matmul_q8_1(type, wu + (size_t)ids[r] * u_eb + (size_t)o * u_rb, u_rb, xq, &u, 1, in_dim, 1))
+                return -1;
+            *dst = g / (1.0 + exp(-g)) * u;
+        }
+    return 0;
+}
+
+int orc_down_q8_1_indexed_accum(int type, const uint8_t *wd, size_t d_eb, size_t d_rb, const uint8_t *act_q8_1,
+                                const int *ids, const float *rw, double *out, int k, int hidden, int ffn_dim) {
+    if (check_shape(type, ffn_dim)) return -1;
+    const size_t xrb = (size_t)(ffn_dim / 32) * 36;
+    for (int h = 0; h < hidden; ++h)
+        for (int r = 0; r < k; ++r) {
+            if (ids[r] < 0) continue;
+            double y;
+            if (orc_matmul_q8_1(type, wd + (size_t)ids[r] * d_eb + (size_t)h * d_rb, d_rb, act_q8_1 + (size_t)r * xrb,
+                                &y, 1, ffn_dim, 1))
+                return -1;
+            out[h] += (double)rw[r] * y;
+        }
+    return 0;
+}
+
+int orc_down_f32_indexed_accum(int type, const uint8_t *wd, size_t d_eb, size_t d_rb, const float *act,
+                               const int *ids, const float *rw, double *out, int k, int hidden, int ffn_dim) {
+    if (check_shape(type, ffn_dim) || k < 0) return -1;
+    uint8_t *q = (uint8_t *)malloc((size_t)(k > 0 ? k : 1) * (size_t)(ffn_dim / 32) * 36);
+    if (!q) return -1;
+    orc_quantize_q8_1(act, q, ffn_dim, k, 0);
+    const int rc = orc_down_q8_1_indexed_accum(type, wd, d_eb, d_rb, q, ids, rw, out, k, hidden, ffn_dim);
+    free(q);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* MLA over the Q8_1 latent cache -- kernel.cu:2945-3415                                       */
 
 int orc_mla_store_latent_q8_1(const float *kv_cache, uint8_t *cache, int kv_lora, int qk_rope, size_t row_bytes,

@@ -135,6 +135,26 @@ int orc_down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_bytes,
                              size_t d_row_bytes, const float *act, const int *expert_ids,
                              const float *route_w, float *out, int k, int hidden, int ffn_dim);
 
+/* Q8_1-activation variants, sums in double.
+ * quantize_q8_1_mmq: the group-major MMQ layout (kernel.cu:1724-1765): group g of row r at
+ *   (g * m + r) * 144 = 4 x (d f16, s f16), then 4 x 32 int8; the blocks are those of orc_quantize_q8_1.
+ * matmul_q8_1_mmq: orc_matmul_q8_1 over that layout (kernel.cu:2405-2660).
+ * swiglu_indexed_q8_1: silu(g) * u with g, u the block-dot rows against one Q8_1 x (kernel.cu:1532-1666).
+ * down_q8_1_indexed_accum: out[h] += sum_r rw_r * (Wd_e[h] . act_q8_1[r]) (kernel.cu:1873-2097);
+ * down_f32_indexed_accum: the same after orc_quantize_q8_1 of each route's act (kernel.cu:2112-2242). */
+void orc_quantize_q8_1_mmq(const float *x, uint8_t *xq, int in_dim, int m, int store_raw_sum);
+int orc_matmul_q8_1_mmq(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y, int out_dim,
+                        int in_dim, int m);
+int orc_swiglu_indexed_q8_1(int type, const uint8_t *wg, const uint8_t *wu, size_t g_expert_bytes,
+                            size_t u_expert_bytes, size_t g_row_bytes, size_t u_row_bytes, const uint8_t *xq,
+                            const int *expert_ids, double *act, int k, int ffn_dim, int in_dim);
+int orc_down_q8_1_indexed_accum(int type, const uint8_t *wd, size_t d_expert_bytes, size_t d_row_bytes,
+                                const uint8_t *act_q8_1, const int *expert_ids, const float *route_w, double *out,
+                                int k, int hidden, int ffn_dim);
+int orc_down_f32_indexed_accum(int type, const uint8_t *wd, size_t d_expert_bytes, size_t d_row_bytes,
+                               const float *act, const int *expert_ids, const float *route_w, double *out, int k,
+                               int hidden, int ffn_dim);
+
 /* Index of the maximum, lowest index on ties (kernel.cu:3531-3592). */
 int orc_argmax(const float *v, int n);
 

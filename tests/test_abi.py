@@ -202,6 +202,31 @@ def test_embedding_and_mla_validation():
     assert qlin.status(V, 14, FAKE, 420, FAKE, 0, FAKE, 16, 128, 0, 512) == OK
 
 
+def test_q8_1_variant_validation():
+    """The Q8_1-activation variants take the reference launchers' types (launch.cu:226-455, 546-560);
+    others, short strides and a down activation too long for LDS are statuses."""
+    assert qlin.status("qlin_launch_quant_matmul_q8_1_mmq", 8, FAKE, 34, FAKE, FAKE, 4, 32, 1) == UNSUP
+    assert qlin.status("qlin_launch_quant_matmul_q8_1_mmq", 12, FAKE, 144, 0, FAKE, 4, 256, 1) == NULL
+    assert qlin.status("qlin_launch_quantize_q8_1_mmq", FAKE, FAKE, 0, 1, 0) == SHAPE
+    assert qlin.status("qlin_launch_quantize_q8_1_mmq", FAKE, FAKE + 1, 32, 1, 0) == ALIGN
+    assert qlin.status("qlin_launch_quant_gemv_q8_1", 12, FAKE, 144, 0, FAKE, 4, 256) == NULL
+    for fn in ("qlin_launch_quant_swiglu_indexed_q8_1", "qlin_launch_quant_swiglu_indexed_block"):
+        extra = (0,) if fn.endswith("block") else ()
+        assert qlin.status(fn, 8, FAKE, FAKE, 34, 34, 34, 34, FAKE, FAKE, FAKE, 1, 1, 32, *extra) == UNSUP
+        assert qlin.status(fn, 12, FAKE, FAKE, 100, 144, 144, 144, FAKE, FAKE, FAKE, 1, 1, 256, *extra) == ROWB
+    assert qlin.status("qlin_launch_quant_swiglu_indexed_q8_1", 12, FAKE, FAKE, 144, 144, 144, 144, 0, FAKE, FAKE,
+                       1, 1, 256) == NULL
+    for fn in ("qlin_launch_quant_down_q8_1_indexed_accum", "qlin_launch_quant_down_q8_1_indexed_accum_shared",
+               "qlin_launch_quant_down_f32_indexed_accum"):
+        assert qlin.status(fn, 2, FAKE, 18, 18, FAKE, FAKE, FAKE, FAKE, 1, 1, 32) == UNSUP
+        assert qlin.status(fn, 6, FAKE, 10, 22, FAKE, FAKE, FAKE, FAKE, 1, 1, 32) == ROWB
+        assert qlin.status(fn, 6, FAKE, 22, 22, 0, FAKE, FAKE, FAKE, 1, 1, 32) == NULL
+        assert qlin.status(fn, 6, FAKE, 22, 22, FAKE, FAKE, FAKE, FAKE, 0, 1, 32) == OK
+    big = 160 * 1024 // 36 * 32 + 32   # one block more than fits
+    assert qlin.status("qlin_launch_quant_down_f32_indexed_accum", 8, FAKE, big // 32 * 34, big // 32 * 34, FAKE,
+                       FAKE, FAKE, FAKE, 1, 1, big) == LIMIT
+
+
 def test_mla_latent_cache_validation():
     """The Q8_1 latent-cache entry points (launch.cu:911-1049): cache rows shorter than the latent's
     blocks, misaligned rows, null pointers and v_head beyond the kernel's limit are statuses; empty
