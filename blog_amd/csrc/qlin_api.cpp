@@ -372,6 +372,31 @@ int qlin_launch_moe_router_topk(const float *logits, int *idx, float *w, int tok
     return launched(qlin::router_topk(logits, idx, w, tokens, n_experts, k, routed_scaling, stream()));
 }
 
+int qlin_launch_moe_accumulate(const float *expert_out, float weight, float *out, int n) {
+    if (n < 0) return QLIN_ERR_SHAPE;
+    if (n == 0) return QLIN_OK;
+    int rc;
+    if ((rc = check_f32(expert_out, true)) || (rc = check_f32(out, true))) return rc;
+    return launched(qlin::moe_accumulate(expert_out, weight, nullptr, out, n, stream()));
+}
+
+int qlin_launch_moe_accumulate_device(const float *expert_out, const float *weight, float *out, int n) {
+    if (n < 0) return QLIN_ERR_SHAPE;
+    if (n == 0) return QLIN_OK;
+    int rc;
+    if ((rc = check_f32(expert_out, true)) || (rc = check_f32(out, true)) || (rc = check_f32(weight, true))) return rc;
+    return launched(qlin::moe_accumulate(expert_out, 0.0f, weight, out, n, stream()));
+}
+
+int qlin_launch_argmax(const float *logits, int n, int *out_idx) {
+    if (n <= 0) return QLIN_ERR_SHAPE;
+    int rc = check_f32(logits, true);
+    if (rc) return rc;
+    if (!out_idx) return QLIN_ERR_NULL;
+    if (!aligned(out_idx, 4)) return QLIN_ERR_ALIGN;
+    return launched(qlin::argmax(logits, n, out_idx, stream()));
+}
+
 static int dequant_common(int type, const uint8_t *src, void *out, int64_t n, bool f16) {
     if (!known_weight_type(type)) return QLIN_ERR_UNSUPPORTED_TYPE;
     if (n < 0 || n % elems_of(type)) return QLIN_ERR_SHAPE;

@@ -95,6 +95,9 @@ hipError_t down_q8_1_indexed_accum(int type, bool f32_act, const uint8_t *wd, si
                                    float *out, int k, int hidden, int ffn_dim, hipStream_t s);
 
 // MoE.
+hipError_t moe_accumulate(const float *expert_out, float weight, const float *weight_dev, float *out, int n,
+                          hipStream_t s);
+hipError_t argmax(const float *logits, int n, int *out_idx, hipStream_t s);
 hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts,
                        int k, float routed_scaling, hipStream_t s);
 hipError_t swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t g_row_bytes,

@@ -133,7 +133,59 @@ __global__ __launch_bounds__(kBlock) void down_kernel(const uint8_t *__restrict_
     if (lane == 0) out[h] += total;
 }
 
+// out[i] += w * expert_out[i], w from the host or read on the device (kernel.cu:3514-3526).
+__global__ __launch_bounds__(256) void accumulate_kernel(const float *__restrict__ e, float w, const float *wp,
+                                                         float *__restrict__ out, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = fmaf(wp ? *wp : w, e[i], out[i]);
+}
+
+// Index of the largest logit, the lowest index among equals; NaN never wins and index 0 is the
+// answer when nothing beats -inf (kernel.cu:3531-3592).  One workgroup: strided scans, then the
+// (value, index) pairs are reduced across lanes and waves with the same rule.
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ void better(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits, int n,
+                                                            int *__restrict__ out_idx) {
+    __shared__ float s_v[kArgThreads / 64];
+    __shared__ int s_i[kArgThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float v = -INFINITY;
+    int idx = 0;
+    for (int i = tid; i < n; i += kArgThreads) better(v, idx, logits[i], i);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) better(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
+    if (lane == 0) {
+        s_v[wave] = v;
+        s_i[wave] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kArgThreads / 64; ++w) better(v, idx, s_v[w], s_i[w]);
+        *out_idx = idx;
+    }
+}
+
 }  // namespace
+
+hipError_t moe_accumulate(const float *expert_out, float weight, const float *weight_dev, float *out, int n,
+                          hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(accumulate_kernel, dim3((n + 255) / 256), dim3(256), 0, s, expert_out, weight, weight_dev, out, n);
+    return hipGetLastError();
+}
+
+hipError_t argmax(const float *logits, int n, int *out_idx, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgThreads), 0, s, logits, n, out_idx);
+    return hipGetLastError();
+}
 
 hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts, int k,
                        float routed_scaling, hipStream_t s) {

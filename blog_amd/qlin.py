@@ -42,6 +42,9 @@ SIGNATURES = {
     "qlin_launch_quant_matmul": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_launch_quant_matmul_add": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_launch_quant_gemv_q8_1": (I, [I, P, SZ, P, P, I, I]),
+    "qlin_launch_moe_accumulate": (I, [P, F, P, I]),
+    "qlin_launch_moe_accumulate_device": (I, [P, P, P, I]),
+    "qlin_launch_argmax": (I, [P, I, P]),
     "qlin_launch_quantize_q8_1_mmq": (I, [P, P, I, I, I]),
     "qlin_launch_quant_matmul_q8_1_mmq": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_launch_quant_swiglu_indexed_block": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I, I]),

@@ -199,6 +199,18 @@ int qlin_launch_quant_down_f32_indexed_accum_ordered(int type, const uint8_t *do
 int qlin_launch_moe_router_topk(const float *router_logits, int *top_idx, float *top_w, int tokens,
                                 int n_experts, int k, float routed_scaling);
 
+/* out[i] += weight * expert_out[i] (one expert's output into the MoE sum).
+ * Replaces launch_moe_accumulate (kernel.cuh:339, kernel.cu:3514-3518). */
+int qlin_launch_moe_accumulate(const float *expert_out, float weight, float *out, int n);
+
+/* The same with the weight read on the device (*weight), so routing weights need not come back to
+ * the host.  Replaces launch_moe_accumulate_device (kernel.cuh:342, kernel.cu:3522-3526). */
+int qlin_launch_moe_accumulate_device(const float *expert_out, const float *weight, float *out, int n);
+
+/* out_idx[0] = the index of the largest of logits[0 .. n), the lowest index on ties (greedy decode;
+ * the result stays on the device).  Replaces launch_argmax (kernel.cuh:347, kernel.cu:3531-3592). */
+int qlin_launch_argmax(const float *logits, int n, int *out_idx);
+
 /* ---- dequantization (kernel.cuh:237-252) -------------------------------------------------------- */
 
 /* num_elements values of a contiguous block stream to f16 bit patterns (RNE of the exact f32 value).

@@ -173,6 +173,17 @@ inline void launch_quant_down_f32_indexed_accum(DType t, const uint8_t *down_wei
           "launch_quant_down_f32_indexed_accum");
 }
 
+// kernel.cuh:339-347
+inline void launch_moe_accumulate(const float *expert_out, float weight, float *out, int n) {
+    check(qlin_launch_moe_accumulate(expert_out, weight, out, n), "launch_moe_accumulate");
+}
+inline void launch_moe_accumulate_device(const float *expert_out, const float *weight, float *out, int n) {
+    check(qlin_launch_moe_accumulate_device(expert_out, weight, out, n), "launch_moe_accumulate_device");
+}
+inline void launch_argmax(const float *logits, int n, int *out_idx) {
+    check(qlin_launch_argmax(logits, n, out_idx), "launch_argmax");
+}
+
 // kernel.cuh:335-336
 inline void launch_moe_router_topk(const float *router_logits, int *top_idx, float *top_w, int tokens,
                                    int n_experts, int k, float routed_scaling) {

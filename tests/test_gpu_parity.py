@@ -365,6 +365,38 @@ def _experts(qtype, E, rows, cols, seed):
     return w, rb, rows * rb
 
 
+@pytest.mark.parametrize("n", [151936, 1000, 1])
+def test_argmax(n):
+    """Greedy pick over a Qwen2.5 vocabulary (launch_argmax, kernel.cu:3531-3592): ties go to the
+    lowest index, NaN never wins, all -inf gives 0."""
+    rng = np.random.default_rng(n)
+    v = rng.standard_normal(n).astype(np.float32)
+    banner(f"argmax n={n}")
+    out = torch.empty(1, dtype=torch.int32, device="cuda")
+    cases = [v]
+    if n > 10:
+        t = v.copy()
+        t[[7, n - 3, n // 2]] = 50.0                 # a three-way tie
+        nan = v.copy()
+        nan[0] = np.nan
+        cases += [t, nan, np.full(n, -np.inf, np.float32)]
+    for c in cases:
+        qlin.call("qlin_launch_argmax", dev(c), n, out)
+        assert int(host(out)[0]) == orc.argmax(c)
+
+
+def test_moe_accumulate_host_and_device_weight():
+    e = np.random.default_rng(3).standard_normal(2048).astype(np.float32)
+    o0 = np.random.default_rng(4).standard_normal(2048).astype(np.float32)
+    banner("moe accumulate")
+    o = dev(o0)
+    qlin.call("qlin_launch_moe_accumulate", dev(e), 0.375, o, 2048)
+    ref = o0 + np.float64(0.375) * e
+    assert np.allclose(host(o), ref, rtol=0, atol=1e-6)
+    qlin.call("qlin_launch_moe_accumulate_device", dev(e), dev(np.array([-2.0], np.float32)), o, 2048)
+    assert np.allclose(host(o), ref - 2.0 * e, rtol=0, atol=1e-5)
+
+
 def test_swiglu_indexed_and_down_ordered():
     E, ffn, hid, k = 8, 96, 512, 4
     wg, grb, geb = _experts(Q4_K, E, ffn, hid, 81)
