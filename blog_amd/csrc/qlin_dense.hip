@@ -10,7 +10,7 @@
 // one warp per (r, o), with the same f32 operands and only the summation order changed.
 //
 // Layout.  A workgroup owns a tile of 16 output rows and all of K; its 8 waves take the 256-element
-// super-blocks of K in turn (wave w: w, w + 8, ...).  Lane l supplies output row l % 16 and token
+// chunks of K in turn (wave w: w, w + 8, ...; Q4_K super-blocks, eight 32-element blocks otherwise).  Lane l supplies output row l % 16 and token
 // l % 16 of the current 16-token tile, and k-slot g = l / 16 of each MFMA: the 8 MFMAs of 32-element
 // sub-block j cover its elements 8g .. 8g+7 in slot g, so a lane reads 8 consecutive weights and 8
 // consecutive activations per sub-block.  D holds tokens 4g .. 4g+3 of row l % 16.  The waves'
@@ -139,20 +139,111 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
     }
 }
 
+// The other formats (Q4_0, Q5_0, Q8_0, Q6_K): the same tiling over 32-element blocks, eight to a
+// chunk (a partial last chunk when K / 32 is not a multiple of 8), with each lane's 8 values taken
+// from the canonical per-element decoder (the 8 elements 8g .. 8g+7 of a block share its scales).
+template <int T, int MODE>
+__global__ __launch_bounds__(kDThreads) void dense_generic_kernel(const DenseArgs a) {
+    constexpr int NW = MODE == kSwiGLU ? 2 : 1;
+    constexpr int BE = Block<T>::elems, BB = Block<T>::bytes;
+    __shared__ f32x4 part[kDWaves][NW][4][64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int K = a.k, nb32 = K / 32, nch = (nb32 + 7) / 8;
+    const int row0 = blockIdx.x * 16;
+    const int row = min(row0 + n, a.n - 1);
+    const int t0 = blockIdx.y * kDTokens;
+    const int ntt = min(4, (a.m - t0 + 15) / 16);
+    const uint8_t *rp[2] = {a.w0 + static_cast<size_t>(row) * a.rb, a.w1 + static_cast<size_t>(row) * a.rb};
+
+    f32x4 D[NW][4];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) D[w][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int c = wave; c < nch; c += kDWaves) {
+        const int nj = min(8, nb32 - 8 * c);  // blocks of this chunk
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            if (tt >= ntt) break;  // uniform
+            const int tok = min(t0 + tt * 16 + n, a.m - 1);
+            const float *xr = a.x + static_cast<size_t>(tok) * K + c * 256 + 8 * g;
+            for (int j = 0; j < nj; ++j) {
+                const float4 x0 = *reinterpret_cast<const float4 *>(xr + 32 * j);
+                const float4 x1 = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const int k0 = c * 256 + 32 * j + 8 * g;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    const uint8_t *blk = rp[w] + static_cast<size_t>(k0 / BE) * BB;
+                    const int e0 = k0 % BE;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) D[w][tt] = mfma_f32(xv[i], block_value<T>(blk, e0 + i), D[w][tt]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+            if (tt < ntt) part[wave][w][tt][lane] = D[w][tt];
+    __syncthreads();
+    const int rows = min(16, a.n - row0);
+    for (int i = tid; i < ntt * 256; i += kDThreads) {
+        const int tl = i >> 4, o = i & 15;
+        const int t = t0 + tl;
+        if (o >= rows || t >= a.m) continue;
+        const int tt = tl >> 4, l = ((tl & 15) >> 2) * 16 + o, r = tl & 3;
+        float v0 = 0.0f, v1 = 0.0f;
+        for (int wv = 0; wv < kDWaves; ++wv) {
+            v0 += part[wv][0][tt][l][r];
+            if constexpr (NW == 2) v1 += part[wv][NW - 1][tt][l][r];
+        }
+        float *yo = a.y + static_cast<size_t>(t) * a.n + row0 + o;
+        if constexpr (MODE == kSwiGLU) *yo = v0 / (1.0f + expf(-v0)) * v1;
+        else if constexpr (MODE == kAdd) *yo += v0;
+        else *yo = v0;
+    }
+}
+
+template <int T>
+hipError_t launch_dense(const DenseArgs &a, int mode, dim3 grid, hipStream_t s) {
+    switch (mode) {
+        case kStore: hipLaunchKernelGGL((dense_generic_kernel<T, kStore>), grid, dim3(kDThreads), 0, s, a); break;
+        case kAdd: hipLaunchKernelGGL((dense_generic_kernel<T, kAdd>), grid, dim3(kDThreads), 0, s, a); break;
+        case kSwiGLU: hipLaunchKernelGGL((dense_generic_kernel<T, kSwiGLU>), grid, dim3(kDThreads), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t rb, const float *x, int k) {
     const auto al = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
-    if (type != T_Q4_K) return false;
-    return k % 256 == 0 && rb % 16 == 0 && al(w0, 16) && (!w1 || al(w1, 16)) && al(x, 16);
+    if (type == T_Q4_K) return k % 256 == 0 && rb % 16 == 0 && al(w0, 16) && (!w1 || al(w1, 16)) && al(x, 16);
+    if (type != T_Q4_0 && type != T_Q5_0 && type != T_Q8_0 && type != T_Q6_K) return false;
+    // the per-element decoder reads 16-bit fields: 2-byte aligned blocks
+    return k % 32 == 0 && rb % 2 == 0 && al(w0, 2) && (!w1 || al(w1, 2)) && al(x, 16);
 }
 
 hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t rb, const float *x, float *y, int n,
                         int k, int m, int mode, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
-    if (type != T_Q4_K) return hipErrorInvalidValue;
     const DenseArgs a{w0, w1 ? w1 : w0, rb, x, y, n, k, m};
     const dim3 grid((n + 15) / 16, (m + kDTokens - 1) / kDTokens);
+    switch (type) {
+        case T_Q4_K: break;
+        case T_Q4_0: return launch_dense<T_Q4_0>(a, mode, grid, s);
+        case T_Q5_0: return launch_dense<T_Q5_0>(a, mode, grid, s);
+        case T_Q8_0: return launch_dense<T_Q8_0>(a, mode, grid, s);
+        case T_Q6_K: return launch_dense<T_Q6_K>(a, mode, grid, s);
+        default: return hipErrorInvalidValue;
+    }
     switch (mode) {
         case kStore: hipLaunchKernelGGL(q4k_dense_kernel<kStore>, grid, dim3(kDThreads), 0, s, a); break;
         case kAdd: hipLaunchKernelGGL(q4k_dense_kernel<kAdd>, grid, dim3(kDThreads), 0, s, a); break;

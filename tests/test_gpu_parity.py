@@ -151,19 +151,22 @@ def test_gemv_several_rows(qtype, m):
     assert normwise_rel_err(host(yd), ref) <= FP32
 
 
-@pytest.mark.parametrize("out_dim,in_dim,m", [(200, 1024, 2), (1000, 3584, 16), (2816, 2048, 17), (96, 256, 64),
-                                           (40, 4608, 65), (33, 512, 130)])
-def test_matmul_rows_f32_matrix_cores(out_dim, in_dim, m):
-    """Q4_K over m > 1 rows (launch_quant_matmul, kernel.cu:1254-1279): the f32 matrix-core kernel
-    with row tails (out_dim % 16), fewer and more super-blocks than waves (in_dim 256 .. 4608), and
-    token tails within and across 64-token grid rows."""
-    w, rb, vals = qgen.random_matrix(Q4_K, out_dim, in_dim, seed=out_dim + m)
+@pytest.mark.parametrize("qtype,out_dim,in_dim,m", [
+    (Q4_K, 200, 1024, 2), (Q4_K, 1000, 3584, 16), (Q4_K, 2816, 2048, 17), (Q4_K, 96, 256, 64), (Q4_K, 40, 4608, 65),
+    (Q4_K, 33, 512, 130),
+    (Q8_0, 4864, 896, 32), (Q8_0, 896, 4864, 32), (Q8_0, 50, 96, 5),     # C3's prompt: K 896 = 3.5 chunks
+    (Q4_0, 300, 3584, 16), (Q5_0, 2048, 1408, 6), (Q6_K, 77, 2048, 20)])
+def test_matmul_rows_f32_matrix_cores(qtype, out_dim, in_dim, m):
+    """m > 1 rows (launch_quant_matmul, kernel.cu:1254-1279) on the f32 matrix cores: row tails
+    (out_dim % 16), fewer and more chunks than waves, a partial last chunk (K / 32 not a multiple of
+    8), token tails within and across 64-token grid rows, and every format."""
+    w, rb, vals = qgen.random_matrix(qtype, out_dim, in_dim, seed=out_dim + m + qtype)
     x = qgen.random_x(m, in_dim, seed=m + 7)
-    banner(f"dense matmul n={out_dim} k={in_dim} m={m}")
+    banner(f"dense matmul type={qtype} n={out_dim} k={in_dim} m={m}")
     yd = empty_f32(m, out_dim)
-    qlin.quant_matmul(Q4_K, dev(w), rb, dev(x), yd, out_dim, in_dim, m)
+    qlin.quant_matmul(qtype, dev(w), rb, dev(x), yd, out_dim, in_dim, m)
     y = host(yd)
-    ref = orc.matmul_f64(Q4_K, w, rb, x, out_dim, in_dim)
+    ref = orc.matmul_f64(qtype, w, rb, x, out_dim, in_dim)
     assert normwise_rel_err(y, ref) <= FP32
     assert cond_err(y, ref, vals, x) <= COND
 
@@ -186,11 +189,11 @@ def test_matmul_add_rows(qtype, m):
 
 
 @pytest.mark.parametrize("qtype,ffn,hid,m", [(Q4_K, 2816, 2048, 16), (Q4_K, 200, 768, 5), (Q4_K, 200, 768, 1),
-                                            (Q8_0, 96, 512, 3)])
+                                            (Q8_0, 96, 512, 3), (Q6_K, 2816, 2048, 16), (Q5_0, 100, 160, 4)])
 def test_swiglu_rows(qtype, ffn, hid, m):
     """act[r] = silu(Wg x[r]) * (Wu x[r]) for a batch: C5's shared experts ([2816, 2048] Q4_K gate/up,
-    16 tokens), a short batch, one row (the single-row kernel) and a type without the batched kernel
-    (one launch per row)."""
+    16 tokens), a short batch, one row (the single-row kernel) and the other formats on the f32
+    matrix-core kernel."""
     wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=ffn + m)
     wu, _, _ = qgen.random_matrix(qtype, ffn, hid, seed=ffn + m + 1)
     x = qgen.random_x(m, hid, seed=m + 3)
