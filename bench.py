@@ -392,7 +392,24 @@ def wl_c3(args, torch, qlin, gen):
     us_sw = graph_us(torch, qlin, lambda: [qlin.quant_swiglu(Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, x_h, act, F, H)
                                            for Lw in layers], reps) / L
     sw_bytes = 2 * F * rb_h + 4 * (H + F)
-    log(f"c3: {us:.2f} us/token ({1e6 / us:.0f} tok/s), gate/up SwiGLU {us_sw:.2f} us/launch")
+    # the 32-token prompt: every linear over 32 rows (f32 matrix-core matmul, batched SwiGLU), then
+    # the lm_head for the last row, whose logits start the greedy decode
+    P = 32
+    xp_h, xp_f = torch.randn(P, H, device="cuda", generator=gen), torch.randn(P, F, device="cuda", generator=gen)
+    yp = {nm: torch.empty(P, n, device="cuda") for nm, n, _ in shapes}
+    actp = torch.empty(P, F, device="cuda")
+
+    def prefill():
+        for Lw in layers:
+            for nm, n in (("q", H), ("k", KVD), ("v", KVD), ("o", H)):
+                qlin.quant_matmul(Q8_0, Lw[nm], rb_h, xp_h, yp[nm], n, H, P)
+            qlin.call("qlin_launch_quant_swiglu_rows", Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, xp_h, actp, F, H, P)
+            qlin.quant_matmul(Q8_0, Lw["down"], rb_f, xp_f, yp["down"], H, F, P)
+        qlin.quant_gemv(Q8_0, lm_head, rb_h, xp_h[P - 1], logits, V, H, 1)
+
+    us_pre = graph_us(torch, qlin, prefill, max(1, reps // 4))
+    log(f"c3: {us:.2f} us/token ({1e6 / us:.0f} tok/s), gate/up SwiGLU {us_sw:.2f} us/launch, "
+        f"32-token prefill {us_pre:.1f} us")
     result = {
         "metric": "decode GEMV HBM GB/s + tokens/s, Qwen2.5-0.5B-arch Q8_0 linear work per token, 1 GPU",
         "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
@@ -401,7 +418,9 @@ def wl_c3(args, torch, qlin, gen):
         "data": "synthetic (random Q8_0 blocks, f32 N(0,1) activations)",
         "config": {"workload": "c3-q8_0-decode-token", "layers": L, "hidden": H, "ffn": F, "kv_dim": KVD, "vocab": V,
                    "weight_format": "Q8_0", "batch": 1, "launches_per_step": 4 * L + 1,
-                   "algorithmic_bytes_per_step": nbytes, "execution": "hip graph replay"},
+                   "algorithmic_bytes_per_step": nbytes, "execution": "hip graph replay",
+                   "prefill_32_tokens_us": round(us_pre, 2),
+                   "prompt_32_plus_128_tokens_ms": round((us_pre + 128 * us) / 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": "mfma_gemv_kernel<8, true, *> (Q8_0 gate/up SwiGLU, 2 x [4864, 896])",

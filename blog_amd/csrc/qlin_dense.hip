@@ -139,49 +139,119 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
     }
 }
 
-// The other formats (Q4_0, Q5_0, Q8_0, Q6_K): the same tiling over 32-element blocks, eight to a
-// chunk (a partial last chunk when K / 32 is not a multiple of 8), with each lane's 8 values taken
-// from the canonical per-element decoder (the 8 elements 8g .. 8g+7 of a block share its scales).
+// 8 bytes at a 2-byte aligned address, as two dwords.
+__device__ __forceinline__ void ld8_a2(const uint8_t *p, uint32_t &lo, uint32_t &hi) {
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+    lo = h[0] | (static_cast<uint32_t>(h[1]) << 16);
+    hi = h[2] | (static_cast<uint32_t>(h[3]) << 16);
+}
+__device__ __forceinline__ uint32_t byte_of(uint32_t lo, uint32_t hi, int i) {
+    return ((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu;
+}
+
+// Elements k0 .. k0+7 of a row (k0 a multiple of 8: one block, one scale group), canonical values
+// as the per-element decoders give them (kernel.cu:1122-1185, ggml's Q4_0): the raw words first
+// (so that a wave can have several blocks' loads in flight), then the values.
+template <int T>
+__device__ __forceinline__ void raw8(const uint8_t *row, int k0, uint32_t (&w)[5]) {
+    if constexpr (T == T_Q8_0) {
+        const uint8_t *b = row + static_cast<size_t>(k0 >> 5) * 34;
+        w[0] = ld_u16(b);
+        ld8_a2(b + 2 + (k0 & 31), w[1], w[2]);
+    } else if constexpr (T == T_Q4_0 || T == T_Q5_0) {
+        constexpr int BB = T == T_Q4_0 ? 18 : 22, QS = T == T_Q4_0 ? 2 : 6;
+        const uint8_t *b = row + static_cast<size_t>(k0 >> 5) * BB;
+        w[0] = ld_u16(b);
+        ld8_a2(b + QS + (k0 & 15), w[1], w[2]);
+        if constexpr (T == T_Q5_0) w[3] = ld_u16(b + 2) | (ld_u16(b + 4) << 16);
+    } else {  // Q6_K: half h, group g of 32, lanes l0 .. l0+7 (one 16-element scale)
+        const uint8_t *b = row + static_cast<size_t>(k0 >> 8) * 210;
+        const int e = k0 & 255, half = e >> 7, grp = (e & 127) >> 5, l0 = e & 31;
+        ld8_a2(b + half * 64 + l0 + 32 * (grp & 1), w[0], w[1]);
+        ld8_a2(b + 128 + half * 32 + l0, w[2], w[3]);
+        w[4] = ld_u16(b + 208) | (static_cast<uint32_t>(b[192 + half * 8 + l0 / 16 + 2 * grp]) << 16);
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void values8(const uint32_t (&w)[5], int k0, float (&v)[8]) {
+    if constexpr (T == T_Q8_0) {
+        const float d = f16_bits_to_f32(w[0]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = mul_rn(d, static_cast<float>(static_cast<int8_t>(byte_of(w[1], w[2], i))));
+    } else if constexpr (T == T_Q4_0 || T == T_Q5_0) {
+        const int e0 = k0 & 31, sh = e0 >= 16 ? 4 : 0;
+        const float d = f16_bits_to_f32(w[0]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int q = static_cast<int>((byte_of(w[1], w[2], i) >> sh) & 15u);
+            if constexpr (T == T_Q5_0) q |= static_cast<int>(((w[3] >> (e0 + i)) & 1u) << 4);
+            v[i] = mul_rn(d, static_cast<float>(q - (T == T_Q4_0 ? 8 : 16)));
+        }
+    } else {
+        const int grp = ((k0 & 255) & 127) >> 5;
+        const int sc = static_cast<int8_t>(w[4] >> 16);
+        const float dsc = mul_rn(f16_bits_to_f32(w[4] & 0xffffu), static_cast<float>(sc));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lb = byte_of(w[0], w[1], i), hb = byte_of(w[2], w[3], i);
+            const int q = static_cast<int>(((grp < 2 ? lb : lb >> 4) & 15u) | (((hb >> (2 * grp)) & 3u) << 4)) - 32;
+            v[i] = mul_rn(dsc, static_cast<float>(q));
+        }
+    }
+}
+
+// The other formats (Q4_0, Q5_0, Q8_0, Q6_K): the waves take 32-element blocks in turn (wave w: w,
+// w + 8, ...); a lane's 8 values of a block are decoded once and serve every token tile.
 template <int T, int MODE>
 __global__ __launch_bounds__(kDThreads) void dense_generic_kernel(const DenseArgs a) {
     constexpr int NW = MODE == kSwiGLU ? 2 : 1;
-    constexpr int BE = Block<T>::elems, BB = Block<T>::bytes;
-    __shared__ f32x4 part[kDWaves][NW][4][64];
+    __shared__ f32x4 part[kDWaves][NW][1][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int K = a.k, nb32 = K / 32, nch = (nb32 + 7) / 8;
+    const int K = a.k, nb32 = K / 32;
     const int row0 = blockIdx.x * 16;
     const int row = min(row0 + n, a.n - 1);
-    const int t0 = blockIdx.y * kDTokens;
-    const int ntt = min(4, (a.m - t0 + 15) / 16);
+    const int t0 = blockIdx.y * 16;  // one 16-token tile per grid row
+    constexpr int ntt = 1;
     const uint8_t *rp[2] = {a.w0 + static_cast<size_t>(row) * a.rb, a.w1 + static_cast<size_t>(row) * a.rb};
+    const float *xrow = a.x + static_cast<size_t>(min(t0 + n, a.m - 1)) * K;  // past m: the last token
 
-    f32x4 D[NW][4];
+    f32x4 D[NW][1];
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) D[w][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int w = 0; w < NW; ++w) D[w][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int c = wave; c < nch; c += kDWaves) {
-        const int nj = min(8, nb32 - 8 * c);  // blocks of this chunk
+    // groups of U consecutive blocks, wave w: groups w, w + 8, ...; a group's weight words and
+    // activations are all requested before its first block is used
+    constexpr int U = 4;
+    for (int b0 = wave * U; b0 < nb32; b0 += kDWaves * U) {
+        uint32_t raw[NW][U][5];
+        float4 xq[U][2];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            if (tt >= ntt) break;  // uniform
-            const int tok = min(t0 + tt * 16 + n, a.m - 1);
-            const float *xr = a.x + static_cast<size_t>(tok) * K + c * 256 + 8 * g;
-            for (int j = 0; j < nj; ++j) {
-                const float4 x0 = *reinterpret_cast<const float4 *>(xr + 32 * j);
-                const float4 x1 = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
-                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                const int k0 = c * 256 + 32 * j + 8 * g;
+        for (int u = 0; u < U; ++u) {
+            const int k0 = 32 * min(b0 + u, nb32 - 1) + 8 * g;
 #pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    const uint8_t *blk = rp[w] + static_cast<size_t>(k0 / BE) * BB;
-                    const int e0 = k0 % BE;
+            for (int w = 0; w < NW; ++w) raw8<T>(rp[w], k0, raw[w][u]);
+            xq[u][0] = *reinterpret_cast<const float4 *>(xrow + k0);
+            xq[u][1] = *reinterpret_cast<const float4 *>(xrow + k0 + 4);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the group's loads ahead of its first use
+        // straight-line over the group (no branch lets the compiler sink a load to its use): a block
+        // past the end repeats the last one with zero activations
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) D[w][tt] = mfma_f32(xv[i], block_value<T>(blk, e0 + i), D[w][tt]);
-                }
+        for (int u = 0; u < U; ++u) {
+            const bool in = b0 + u < nb32;
+            const int k0 = 32 * min(b0 + u, nb32 - 1) + 8 * g;
+            const float xv[8] = {in ? xq[u][0].x : 0.0f, in ? xq[u][0].y : 0.0f, in ? xq[u][0].z : 0.0f,
+                                 in ? xq[u][0].w : 0.0f, in ? xq[u][1].x : 0.0f, in ? xq[u][1].y : 0.0f,
+                                 in ? xq[u][1].z : 0.0f, in ? xq[u][1].w : 0.0f};
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                float v[8];
+                values8<T>(raw[w][u], k0, v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) D[w][0] = mfma_f32(xv[i], v[i], D[w][0]);
             }
         }
     }
@@ -211,7 +281,8 @@ __global__ __launch_bounds__(kDThreads) void dense_generic_kernel(const DenseArg
 }
 
 template <int T>
-hipError_t launch_dense(const DenseArgs &a, int mode, dim3 grid, hipStream_t s) {
+hipError_t launch_dense(const DenseArgs &a, int mode, hipStream_t s) {
+    const dim3 grid((a.n + 15) / 16, (a.m + 15) / 16);
     switch (mode) {
         case kStore: hipLaunchKernelGGL((dense_generic_kernel<T, kStore>), grid, dim3(kDThreads), 0, s, a); break;
         case kAdd: hipLaunchKernelGGL((dense_generic_kernel<T, kAdd>), grid, dim3(kDThreads), 0, s, a); break;
@@ -238,10 +309,10 @@ hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t r
     const dim3 grid((n + 15) / 16, (m + kDTokens - 1) / kDTokens);
     switch (type) {
         case T_Q4_K: break;
-        case T_Q4_0: return launch_dense<T_Q4_0>(a, mode, grid, s);
-        case T_Q5_0: return launch_dense<T_Q5_0>(a, mode, grid, s);
-        case T_Q8_0: return launch_dense<T_Q8_0>(a, mode, grid, s);
-        case T_Q6_K: return launch_dense<T_Q6_K>(a, mode, grid, s);
+        case T_Q4_0: return launch_dense<T_Q4_0>(a, mode, s);
+        case T_Q5_0: return launch_dense<T_Q5_0>(a, mode, s);
+        case T_Q8_0: return launch_dense<T_Q8_0>(a, mode, s);
+        case T_Q6_K: return launch_dense<T_Q6_K>(a, mode, s);
         default: return hipErrorInvalidValue;
     }
     switch (mode) {
