@@ -744,11 +744,11 @@ void launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
 // The streaming down kernel reads Q5_0 / Q8_0 4-block chunks as aligned dwords (88 and 136 bytes,
 // multiples of 4, so every chunk starts 4-aligned once the weights do), and Q4_K super-blocks as
 // 16-byte pieces (144 bytes = 9 x 16).
-bool down_stream_ok(int type, const uint8_t *w, size_t eb, int ffn) {
+bool down_stream_ok(int type, const uint8_t *w, size_t eb, size_t rb, int ffn) {
     const auto al = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
-    if (type == T_Q4_K) return ffn % 256 == 0 && eb % 16 == 0 && al(w, 16);
+    if (type == T_Q4_K) return ffn % 256 == 0 && eb % 16 == 0 && rb % 16 == 0 && al(w, 16);
     if (type != T_Q5_0 && type != T_Q8_0) return false;
-    return ffn % 128 == 0 && al(w, 4);
+    return ffn % 128 == 0 && eb % 4 == 0 && rb % 4 == 0 && al(w, 4);
 }
 
 }  // namespace
@@ -806,7 +806,7 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
     }
 
     StreamPlan dn;
-    if (down_stream_ok(d_type, wd, d_eb, ffn)) {
+    if (down_stream_ok(d_type, wd, d_eb, d_rb, ffn)) {
         if (d_type == T_Q5_0) dn = stream_plan<T_Q5_0, false>(hidden, ffn, E, R);
         else if (d_type == T_Q8_0) dn = stream_plan<T_Q8_0, false>(hidden, ffn, E, R);
         else dn = stream_plan<T_Q4_K, false>(hidden, ffn, E, R);
