@@ -90,6 +90,13 @@ struct MfmaArgs {
     int nsb;      // chunks per row
     int total;    // concatenated rows (SwiGLU: rows of each of gate and up)
     int add;
+    // Workgroup b owns rows_q rows (+1 for b < rows_r), and a step index c splits as
+    // tile = mulhi(c, nsb_magic) with nsb_magic = ceil(2^32 / nsb), exact while c * nsb < 2^32
+    // (nsb = 1: tile = c, as 2^32 does not fit).  The host does these divisions, so the waves start
+    // their loads without a 64-bit division sequence on the scalar unit (several hundred cycles per
+    // wave, and the 16 waves of a CU share that unit).
+    int rows_q, rows_r;
+    uint32_t nsb_magic;
 };
 
 // The argument arrays, copied into registers once: indexing the kernel-argument struct with a
@@ -113,6 +120,7 @@ struct Mats {
         wp = w[0];
         yp = y[0];
         local = gr;
+        if (nmat == 1) return;  // uniform
 #pragma unroll
         for (int i = 1; i < kMaxStreamMats; ++i) {
             const bool past = i < nmat && gr >= end[i - 1];
@@ -145,9 +153,10 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
     float *partial = xsum + K / XS;                                // [rows][NW][nsb]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rb = static_cast<int>(static_cast<int64_t>(a.total) * blockIdx.x / gridDim.x);
-    const int re = static_cast<int>(static_cast<int64_t>(a.total) * (blockIdx.x + 1) / gridDim.x);
-    const int nrows = re - rb;
+    const int bid = blockIdx.x;
+    const int rb = bid * a.rows_q + min(bid, a.rows_r);
+    const int nrows = a.rows_q + (bid < a.rows_r ? 1 : 0);
+    const int re = rb + nrows;
     // The workgroup's work is the flat sequence of steps (16-row tile, matrix, super-block), which
     // is also the order of the bytes in memory; the waves claim them in that order, so that at any
     // time the workgroup reads one compact window of its rows.
@@ -186,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
         Pos p;
         p.s = s;
         const int c = min(s, nsteps - 1);
-        p.tw = c / nsb;
+        p.tw = nsb == 1 ? c : static_cast<int>(__umulhi(static_cast<uint32_t>(c), a.nsb_magic));
         p.sb = c - p.tw * nsb;
         int tile, which;
         split_tw(p.tw, tile, which);
@@ -442,12 +451,15 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
 struct Plan {
     int grid;
     size_t lds;
+    bool magic_exact;  // every step index c of a workgroup has c * nsb < 2^32
 };
 
 Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
     Plan p;
     p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
     const int rows = (total + p.grid - 1) / p.grid;
+    const uint64_t steps = static_cast<uint64_t>((rows + 15) / 16) * (swiglu ? 2 : 1) * nsb;
+    p.magic_exact = steps * static_cast<uint64_t>(nsb) < (uint64_t{1} << 32);
     const size_t K = static_cast<size_t>(k);
     p.lds = 4 * K + (K / sum_elems) * sizeof(float) +
             static_cast<size_t>(rows) * (swiglu ? 2 : 1) * nsb * sizeof(float);
@@ -482,6 +494,10 @@ int sum_elems(int type) { return type == T_Q6_K ? kSumElems<T_Q6_K> : kSumElems<
 
 hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
     const Plan p = plan(a.total, k, a.nsb, swiglu, sum_elems(type));
+    if (!p.magic_exact) return hipErrorInvalidValue;  // mfma_ok rejects these shapes first
+    a.rows_q = a.total / p.grid;
+    a.rows_r = a.total % p.grid;
+    a.nsb_magic = a.nsb > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + a.nsb - 1) / a.nsb) : 0u;
     switch (type) {
         case T_Q4_K: launch_fmt<T_Q4_K>(p, a, k, swiglu, s); break;
         case T_Q4_0: launch_fmt<T_Q4_0>(p, a, k, swiglu, s); break;
@@ -504,7 +520,8 @@ bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float
     if (k / 4 > kMaxXr * kThreads) return false;
     for (int i = 0; i < nmat; ++i)
         if (reinterpret_cast<uintptr_t>(w[i]) % wal) return false;
-    return plan(total, k, k / chunk_elems(type), swiglu, sum_elems(type)).lds <= kMaxLds;
+    const Plan p = plan(total, k, k / chunk_elems(type), swiglu, sum_elems(type));
+    return p.lds <= kMaxLds && p.magic_exact;
 }
 
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,
