@@ -19,6 +19,19 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 __device__ __forceinline__ float bf16_val(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+// value of the bf16 in the upper half of p
+__device__ __forceinline__ float bf16_hi_val(uint32_t p) { return __builtin_bit_cast(float, p & 0xffff0000u); }
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// hi = bf16(x), lo = bf16(x - hi) of two values, each as a packed pair (first value in the low half),
+// by v_cvt_pk_bf16_f32 (round to nearest even, as bf16_rne for finite values).
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    const f32x2 v = {a, b};
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    const f32x2 r = {a - bf16_val(hi & 0xffffu), b - bf16_hi_val(hi)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+}
 
 // Lane-constant (scale, min) decode of sub-blocks 2p and 2p+1 (kernel.cu:913-921), packed in bytes
 // 0 and 1 of the results.

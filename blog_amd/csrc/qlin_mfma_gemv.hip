@@ -64,10 +64,16 @@ namespace {
 #endif
 constexpr int kWaves = QLIN_MFMA_WAVES;
 constexpr int kThreads = kWaves * 64;
+#ifndef QLIN_MFMA_DEPTH
+// Steps in flight per wave while one is computed.  2 (a ring of three buffers) measured 9% slower
+// over the decode step than 1: more outstanding requests per CU serve worse on this memory system.
+#define QLIN_MFMA_DEPTH 1
+#endif
 #ifndef QLIN_MFMA_MATMAJOR
 #define QLIN_MFMA_MATMAJOR 1  // SwiGLU steps: 1 = all gate tiles, then all up tiles; 0 = tile-major
 #endif
 constexpr size_t kMaxLds = 160 * 1024;
+constexpr size_t kStaticLds = 256;      // the kernel's own __shared__ variables (claim counter, zeros)
 constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * kThreads
 
 // Weights per step chunk of one row, and its bytes.
@@ -170,6 +176,23 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
     const bool a_active = (n >> 2) == g;
     const bool a_high = (n >> 1) & 1;        // sub-block 2g+1: slots 4..7
     const int a_part = n & 1;
+    // Q4_K takes another slot order: in MFMAs 0..3 lane group g carries the low nibbles of its bytes
+    // 8t..8t+7 (elements 8t..8t+7 of sub-block 2g), in MFMAs 4..7 the high nibbles (sub-block 2g+1).
+    // Row n of A (part n & 1 of sub-block n >> 1) then holds x in all 8 slots of MFMAs 0..3 when
+    // n >> 1 == 2g, of MFMAs 4..7 when n >> 1 == 2g + 1, and zeros otherwise, so each A operand is
+    // 16 bytes read from the staged x or from a zero area (stride 0), with no selects.
+    __shared__ u32x4 s_zero[4];
+    const uint8_t *a_lo, *a_hi;
+    int a_lo_st, a_hi_st;
+    {
+        const int j = n >> 1;
+        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * K + j * 32);
+        const uint8_t *zb = reinterpret_cast<const uint8_t *>(s_zero);
+        a_lo = j == 2 * g ? xb : zb;
+        a_lo_st = j == 2 * g ? 2 * CE : 0;
+        a_hi = j == 2 * g + 1 ? xb : zb;
+        a_hi_st = j == 2 * g + 1 ? 2 * CE : 0;
+    }
 
     // A step: tw = tile * NW + matrix, sb = super-block; s = its index in the flat sequence.
     struct Pos {
@@ -254,13 +277,13 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
         for (int r = 0; r < XR; ++r) {
             const int i = tid + r * kThreads;
             const float xe[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
-            uint32_t hb[4], lb[4];
+            uint32_t hp[2], lp[2];  // (element 2e, element 2e + 1) as bf16 pairs
             float sm = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hb[e] = bf16_rne(xe[e]);
-                lb[e] = bf16_rne(xe[e] - bf16_val(hb[e]));
-                sm += bf16_val(hb[e]) + bf16_val(lb[e]);
+            for (int e = 0; e < 2; ++e) {
+                split_bf16x2(xe[2 * e], xe[2 * e + 1], hp[e], lp[e]);
+                sm += bf16_val(hp[e] & 0xffffu) + bf16_val(lp[e] & 0xffffu);
+                sm += bf16_hi_val(hp[e]) + bf16_hi_val(lp[e]);
             }
             // the threads of a 16- or 32-element group are consecutive lanes, and K is a multiple of
             // 128, so a group is entirely below K/4 or entirely above it
@@ -268,8 +291,8 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
             sm += __shfl_xor(sm, 2, 64);
             if constexpr (XS == 32) sm += __shfl_xor(sm, 4, 64);
             if (i < K / 4) {
-                reinterpret_cast<uint2 *>(xpart)[i] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-                reinterpret_cast<uint2 *>(xpart + K)[i] = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+                reinterpret_cast<uint2 *>(xpart)[i] = make_uint2(hp[0], hp[1]);
+                reinterpret_cast<uint2 *>(xpart + K)[i] = make_uint2(lp[0], lp[1]);
                 if ((i & (XS / 4 - 1)) == 0) xsum[i / (XS / 4)] = sm;
             }
         }
@@ -282,6 +305,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
     // of each other.
     __shared__ int next_step;
     if (tid == 0) next_step = kWaves;
+    if (tid < 4) s_zero[tid] = u32x4{0u, 0u, 0u, 0u};
     Pos cur = at(wave);
     Raw buf;
     load(buf, cur);
@@ -295,7 +319,15 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
     auto process = [&](const Raw &cur, const Pos &p) {
         // A operands of this chunk (x only): the lane's 32 values of its part / sub-block (Q8_0: the
         // block both nibble sub-blocks of the pair come from).
-        {
+        if constexpr (FMT == T_Q4_K) {
+            const u32x4 *pl = reinterpret_cast<const u32x4 *>(a_lo + p.sb * a_lo_st);
+            const u32x4 *ph = reinterpret_cast<const u32x4 *>(a_hi + p.sb * a_hi_st);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                aop[t] = pl[t];
+                aop[4 + t] = ph[t];
+            }
+        } else {
             uint32_t dw[16];
             if (a_active) {
                 // sub-block j = n >> 1; Q6_K: j is (half j/4, group (j/2)%2 + 2 (j%2)) of 32 elements
@@ -336,10 +368,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
         }
         // the 8 dwords of nibbles this lane feeds to the MFMAs
         uint32_t qv[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if constexpr (FMT == T_Q4_K) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) qv[k] = cur.w[4 + k];
-        } else if constexpr (FMT == T_Q4_0) {
+        if constexpr (FMT == T_Q4_0) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) qv[k] = __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2);
 #pragma unroll
@@ -364,6 +393,13 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
                 if (t < 4) d = mfma(aop[t], weights_operand2(lo, hi), d);
                 else d2 = mfma(aop[t], weights_operand2(lo, hi), d2);
             }
+        } else if constexpr (FMT == T_Q4_K) {
+            constexpr uint32_t M = 0x0f0f0f0fu;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) d = mfma(aop[t], weights_operand2(cur.w[4 + 2 * t] & M, cur.w[5 + 2 * t] & M), d);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                d = mfma(aop[4 + t], weights_operand2((cur.w[4 + 2 * t] >> 4) & M, (cur.w[5 + 2 * t] >> 4) & M), d);
         } else {
 #pragma unroll
             for (int t = 0; t < 8; ++t) d = mfma(aop[t], weights_operand(qv[t]), d);
@@ -407,25 +443,55 @@ __global__ __launch_bounds__(kThreads) void mfma_gemv_kernel(const MfmaArgs a) {
             const float dq = f16_bits_to_f32((cur.w[0] >> (16 * (g & 1))) & 0xffffu);
             r = dq * (((d[0] + d[1]) + 16.0f * (d[2] + d[3])) - 2304.0f * xs);
         }
-        // add the four lane-groups (sub-block pairs)
-        r += __shfl_xor(r, 16, 64);
-        r += __shfl_xor(r, 32, 64);
+        // add the four lane-groups (sub-block pairs), into lanes 0..15
+        r = sum_lane_groups(r);
         int tile, which;
         split_tw(p.tw, tile, which);
         const int lr = tile * 16 + n;
         if (g == 0 && lr < nrows) partial[(lr * NW + which) * nsb + p.sb] = r;
     };
 
+    auto claim = [&]() {
+        int c = 0;
+        if (lane == 0) c = atomicAdd(&next_step, 1);
+        return at(__builtin_amdgcn_readfirstlane(c));
+    };
+#if QLIN_MFMA_DEPTH == 2
+    // Two steps in flight while one is computed: a ring of three buffers, unrolled so that no
+    // buffer is copied (a loop-carried copy of loaded registers waits for every outstanding load).
+    // Claims are monotonic per wave, so once a claimed step is past the end, so are the later ones.
+    Pos pa = cur, pb = claim();
+    Raw bb;
+    load(bb, pb);
+    for (;;) {
+        if (pa.s >= nsteps) break;
+        const Pos pc = claim();
+        Raw bc;
+        load(bc, pc);
+        __builtin_amdgcn_sched_barrier(0);
+        process(buf, pa);
+        if (pb.s >= nsteps) break;
+        pa = claim();
+        load(buf, pa);
+        __builtin_amdgcn_sched_barrier(0);
+        process(bb, pb);
+        if (pc.s >= nsteps) break;
+        pb = claim();
+        load(bb, pb);
+        __builtin_amdgcn_sched_barrier(0);
+        process(bc, pc);
+    }
+#else
     while (cur.s < nsteps) {
-        int claimed = 0;
-        if (lane == 0) claimed = atomicAdd(&next_step, 1);
-        const Pos nxt = at(__builtin_amdgcn_readfirstlane(claimed));
+        const Pos nxt = claim();
         Raw nb;
         load(nb, nxt);
+        __builtin_amdgcn_sched_barrier(0);
         process(buf, cur);
         buf = nb;
         cur = nxt;
     }
+#endif
 
     __syncthreads();
     for (int r = tid; r < nrows; r += kThreads) {
@@ -521,7 +587,7 @@ bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float
     for (int i = 0; i < nmat; ++i)
         if (reinterpret_cast<uintptr_t>(w[i]) % wal) return false;
     const Plan p = plan(total, k, k / chunk_elems(type), swiglu, sum_elems(type));
-    return p.lds <= kMaxLds && p.magic_exact;
+    return p.lds + kStaticLds <= kMaxLds && p.magic_exact;
 }
 
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,

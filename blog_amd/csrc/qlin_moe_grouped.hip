@@ -153,7 +153,21 @@ struct StreamArgs {
     int piece;                 // tiles whose step partials fit in LDS at once
 };
 
-__device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
+// shared by the 16 waves of a CU: both helpers take 32-bit arithmetic when the operands allow
+// (wave-uniform branches), which covers every realistic cost total.
+__device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) {
+    constexpr int64_t lim = int64_t{1} << 30;
+    if (a > -lim && a < lim && b < lim)
+        return (static_cast<int>(a) + static_cast<int>(b) - 1) / static_cast<int>(b);
+    return (a + b - 1) / b;
+}
+// floor(C * b / G) for workgroup b of G
+__device__ __forceinline__ int64_t share_bound(int64_t C, int b, int G) {
+    if (C < (int64_t{1} << 23) && G <= 256)
+        return static_cast<int64_t>(static_cast<uint32_t>(C) * static_cast<uint32_t>(b) / static_cast<uint32_t>(G));
+    return C * b / G;
+}
 
 // A value the whole wave holds alike, moved to scalar registers (LDS and vector loads give VGPRs).
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -219,7 +233,8 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
         __syncthreads();
     }
     const int64_t C = uni(s_pref[nsel]);
-    const int64_t c0 = C * blockIdx.x / gridDim.x, c1 = C * (blockIdx.x + 1) / gridDim.x;
+    const int bid = blockIdx.x, nwg = gridDim.x;
+    const int64_t c0 = share_bound(C, bid, nwg), c1 = share_bound(C, bid + 1, nwg);
     if (c0 >= c1) return;  // uniform
     int s_first = 0;
     for (int hi = nsel - 1; s_first < hi;) {  // first expert whose range ends after c0
