@@ -185,17 +185,24 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     const bool a_active = (n >> 2) == g;
     const bool a_high = (n >> 1) & 1;        // sub-block 2g+1: slots 4..7
     const int a_part = n & 1;
-    // Q4_K takes another slot order: in MFMAs 0..3 lane group g carries the low nibbles of its bytes
-    // 8t..8t+7 (elements 8t..8t+7 of sub-block 2g), in MFMAs 4..7 the high nibbles (sub-block 2g+1).
-    // Row n of A (part n & 1 of sub-block n >> 1) then holds x in all 8 slots of MFMAs 0..3 when
+    // Q4_K, Q4_0 and Q8_0 take another slot order: every MFMA gives lane group g's 8 slots to 8
+    // consecutive weights of one 32-weight unit ("sub-block" j of the D rows).  MFMAs 0..3 carry
+    // unit 2g, 4..7 unit 2g+1:
+    //   Q4_K: the low / high nibbles of the pair's bytes 8t..8t+7 (sub-blocks 2g, 2g+1);
+    //   Q4_0: blocks 2g, 2g+1, each as low nibbles of bytes 0..7, 8..15, then high nibbles of the same;
+    //   Q8_0: block g's bytes 8t..8t+7 as the l (units 2g) and h (unit 2g+1) nibbles of q + 128.
+    // Row n of A (part n & 1 of unit n >> 1) then holds x in all 8 slots of MFMAs 0..3 when
     // n >> 1 == 2g, of MFMAs 4..7 when n >> 1 == 2g + 1, and zeros otherwise, so each A operand is
     // 16 bytes read from the staged x or from a zero area (stride 0), with no selects.
+    constexpr bool kDirectA = FMT != T_Q6_K;
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
     int a_lo_st, a_hi_st;
     {
         const int j = n >> 1;
-        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * K + j * 32);
+        // the unit's 32 x values: Q8_0 units 2b and 2b+1 are both block b
+        const int xo = FMT == T_Q8_0 ? (j >> 1) * 32 : j * 32;
+        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * K + xo);
         const uint8_t *zb = reinterpret_cast<const uint8_t *>(s_zero);
         a_lo = j == 2 * g ? xb : zb;
         a_lo_st = j == 2 * g ? 2 * CE : 0;
@@ -328,7 +335,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     auto process = [&](const Raw &cur, const Pos &p) {
         // A operands of this chunk (x only): the lane's 32 values of its part / sub-block (Q8_0: the
         // block both nibble sub-blocks of the pair come from).
-        if constexpr (FMT == T_Q4_K) {
+        if constexpr (kDirectA) {
             const u32x4 *pl = reinterpret_cast<const u32x4 *>(a_lo + p.sb * a_lo_st);
             const u32x4 *ph = reinterpret_cast<const u32x4 *>(a_hi + p.sb * a_hi_st);
 #pragma unroll
@@ -339,11 +346,9 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         } else {
             uint32_t dw[16];
             if (a_active) {
-                // sub-block j = n >> 1; Q6_K: j is (half j/4, group (j/2)%2 + 2 (j%2)) of 32 elements
+                // Q6_K sub-block j = n >> 1 is (half j/4, group (j/2)%2 + 2 (j%2)) of 32 elements
                 const int j = n >> 1;
-                const int xo = FMT == T_Q8_0   ? p.sb * CE + (n >> 2) * 32
-                               : FMT == T_Q6_K ? p.sb * CE + (j >> 2) * 128 + (((j >> 1) & 1) + 2 * (j & 1)) * 32
-                                               : p.sb * CE + j * 32;
+                const int xo = p.sb * CE + (j >> 2) * 128 + (((j >> 1) & 1) + 2 * (j & 1)) * 32;
                 const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * K + xo);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -354,25 +359,12 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 #pragma unroll
                 for (int q = 0; q < 16; ++q) dw[q] = 0u;
             }
-            if constexpr (FMT == T_Q4_0) {
-                // a block's x fills both halves of the 4 MFMAs that carry it
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int tt = t & 3;
-                    const bool on = (t >> 2) == static_cast<int>(a_high);
-                    aop[t].x = on ? dw[2 * tt] : 0u;
-                    aop[t].y = on ? dw[2 * tt + 1] : 0u;
-                    aop[t].z = on ? dw[8 + 2 * tt] : 0u;
-                    aop[t].w = on ? dw[8 + 2 * tt + 1] : 0u;
-                }
-            } else {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    aop[t].x = a_high ? 0u : dw[2 * t];
-                    aop[t].y = a_high ? 0u : dw[2 * t + 1];
-                    aop[t].z = a_high ? dw[2 * t] : 0u;
-                    aop[t].w = a_high ? dw[2 * t + 1] : 0u;
-                }
+            for (int t = 0; t < 8; ++t) {
+                aop[t].x = a_high ? 0u : dw[2 * t];
+                aop[t].y = a_high ? 0u : dw[2 * t + 1];
+                aop[t].z = a_high ? dw[2 * t] : 0u;
+                aop[t].w = a_high ? dw[2 * t + 1] : 0u;
             }
         }
         // the 8 dwords of nibbles this lane feeds to the MFMAs
@@ -402,16 +394,25 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
                 if (t < 4) d = mfma(aop[t], weights_operand2(lo, hi), d);
                 else d2 = mfma(aop[t], weights_operand2(lo, hi), d2);
             }
-        } else if constexpr (FMT == T_Q4_K) {
+        } else if constexpr (FMT == T_Q4_0) {
+            // block 2g + (t >> 2): low nibbles of bytes 0..7, 8..15 (elements 0..15), then high nibbles
             constexpr uint32_t M = 0x0f0f0f0fu;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) d = mfma(aop[t], weights_operand2(cur.w[4 + 2 * t] & M, cur.w[5 + 2 * t] & M), d);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                d = mfma(aop[4 + t], weights_operand2((cur.w[4 + 2 * t] >> 4) & M, (cur.w[5 + 2 * t] >> 4) & M), d);
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t a0 = qv[4 * (t >> 2) + 2 * (t & 1)], a1 = qv[4 * (t >> 2) + 2 * (t & 1) + 1];
+                const int sh = 4 * ((t >> 1) & 1);
+                d = mfma(aop[t], weights_operand2((a0 >> sh) & M, (a1 >> sh) & M), d);
+            }
         } else {
+            // Q4_K: the pair's bytes 8t..8t+7 (cur.w[4..11]); Q8_0: block g's (qv): low nibbles, then high
+            constexpr uint32_t M = 0x0f0f0f0fu;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) d = mfma(aop[t], weights_operand(qv[t]), d);
+            for (int t = 0; t < 8; ++t) {
+                const int k = 2 * (t & 3), sh = 4 * (t >> 2);
+                const uint32_t a0 = FMT == T_Q4_K ? cur.w[4 + k] : qv[k];
+                const uint32_t a1 = FMT == T_Q4_K ? cur.w[5 + k] : qv[k + 1];
+                d = mfma(aop[t], weights_operand2((a0 >> sh) & M, (a1 >> sh) & M), d);
+            }
         }
         float r;
         if constexpr (FMT == T_Q6_K) {
