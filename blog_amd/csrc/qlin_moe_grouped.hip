@@ -246,8 +246,20 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     // A-operand role of this lane (row n of A, k-slots of lane-group g)
     const bool a_active = (n >> 2) == g;
     const int a_part = n & 1;
-    const bool a_high = (n >> 1) & 1;       // Q4_K: sub-block 2g+1 uses slots 4..7
-    const int a_pair = (n >> 1) & 1;        // others: route of the pair
+    const int a_pair = (n >> 1) & 1;        // Q5_0 / Q8_0: route of the pair
+    // Q4_K x operands, in the decode GEMV's slot order (MFMAs 0..3 carry the low nibbles of lane
+    // group g's bytes 8t..8t+7, sub-block 2g; MFMAs 4..7 the high nibbles, sub-block 2g+1): for
+    // route q, operand t is the 16 bytes at a_lo (t < 4) or a_hi (t >= 4) + 16 (t & 3), offset by
+    // the route and chunk where the lane's row (part n & 1 of sub-block n >> 1) belongs to that
+    // sub-block, and a zero area otherwise -- LDS reads with no selects.
+    const bool on_lo = (n >> 1) == 2 * g, on_hi = (n >> 1) == 2 * g + 1;
+    const uint8_t *a_lo, *a_hi;
+    {
+        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * K + (n >> 1) * 32);
+        const uint8_t *zb = reinterpret_cast<const uint8_t *>(s_zero);
+        a_lo = on_lo ? xb : zb;
+        a_hi = on_hi ? xb : zb;
+    }
     const ScaleDecoder dec(g);
     // others: lane-group g's block starts bb*g bytes into the chunk; its payload (after d) is read
     // from the dword at or 2 bytes before it
@@ -319,8 +331,12 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             const bool store = g == 0 && p.tile * 16 + n < nrows;
             if constexpr (K4) {
                 u32x4 B[8];
+                constexpr uint32_t M = 0x0f0f0f0fu;
 #pragma unroll
-                for (int t = 0; t < 8; ++t) B[t] = weights_operand(cur.w[4 + t]);
+                for (int t = 0; t < 8; ++t) {
+                    const int k = 2 * (t & 3), sh = 4 * (t >> 2);
+                    B[t] = weights_operand2((cur.w[4 + k] >> sh) & M, (cur.w[5 + k] >> sh) & M);
+                }
                 uint32_t scp, mp;
                 dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
                 const float dd = f16_bits_to_f32(cur.w[0] & 0xffffu);
@@ -332,30 +348,15 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
                     if (q >= nq) break;  // uniform
-                    // this lane's A row: part a_part of sub-block n >> 1 (block-diagonal, as the decode GEMV)
-                    uint32_t dw[16];
-                    if (a_active) {
-                        const uint4 *src = reinterpret_cast<const uint4 *>(xpart + (2 * q + a_part) * K + p.ch * 256 +
-                                                                           (n >> 1) * 32);
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            const uint4 v = src[c];
-                            dw[4 * c] = v.x; dw[4 * c + 1] = v.y; dw[4 * c + 2] = v.z; dw[4 * c + 3] = v.w;
-                        }
-                    } else {
-#pragma unroll
-                        for (int c = 0; c < 16; ++c) dw[c] = 0u;
-                    }
+                    // route q's planes start 4K bytes after route q-1's; a chunk is 512 bytes of a plane
+                    const int off = q * 4 * K + p.ch * 512;
+                    const u32x4 *pl = reinterpret_cast<const u32x4 *>(a_lo + (on_lo ? off : 0));
+                    const u32x4 *ph = reinterpret_cast<const u32x4 *>(a_hi + (on_hi ? off : 0));
                     f32x4 D = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        u32x4 ao;
-                        ao.x = a_high ? 0u : dw[2 * t];
-                        ao.y = a_high ? 0u : dw[2 * t + 1];
-                        ao.z = a_high ? dw[2 * t] : 0u;
-                        ao.w = a_high ? dw[2 * t + 1] : 0u;
-                        D = mfma(ao, B[t], D);
-                    }
+                    for (int t = 0; t < 4; ++t) D = mfma(pl[t], B[t], D);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) D = mfma(ph[t], B[4 + t], D);
                     const float2 xs = *reinterpret_cast<const float2 *>(xsum + q * nblk + p.ch * 8 + 2 * g);
                     float r = dsc0 * ((D[0] + D[1]) - 128.0f * xs.x);
                     r = fmaf(dsc1, (D[2] + D[3]) - 128.0f * xs.y, r);
@@ -418,21 +419,21 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                     const int q = it / per, c = it - q * per;
                     const int route = a.list[beg + q0 + q];
                     const float4 v = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(route / a.x_div) * K)[c];
-                    const float xe[4] = {v.x, v.y, v.z, v.w};
-                    uint32_t hb[4], lb[4];
+                    uint32_t hp[2], lp[2];  // (element 2i, 2i + 1) as bf16 pairs
                     float sm = 0.0f;
+                    split_bf16x2(v.x, v.y, hp[0], lp[0]);
+                    split_bf16x2(v.z, v.w, hp[1], lp[1]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        hb[i] = bf16_rne(xe[i]);
-                        lb[i] = bf16_rne(xe[i] - bf16_val(hb[i]));
-                        sm += bf16_val(hb[i]) + bf16_val(lb[i]);
+                    for (int i = 0; i < 2; ++i) {
+                        sm += bf16_val(hp[i] & 0xffffu) + bf16_val(lp[i] & 0xffffu);
+                        sm += bf16_hi_val(hp[i]) + bf16_hi_val(lp[i]);
                     }
                     sm += __shfl_xor(sm, 1, 64);
                     sm += __shfl_xor(sm, 2, 64);
                     sm += __shfl_xor(sm, 4, 64);
                     uint16_t *xp = xpart + static_cast<size_t>(q) * 2 * K;
-                    reinterpret_cast<uint2 *>(xp)[c] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-                    reinterpret_cast<uint2 *>(xp + K)[c] = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+                    reinterpret_cast<uint2 *>(xp)[c] = make_uint2(hp[0], hp[1]);
+                    reinterpret_cast<uint2 *>(xp + K)[c] = make_uint2(lp[0], lp[1]);
                     if ((c & 7) == 0) xsum[q * nblk + (c >> 3)] = sm;
                 }
             } else {
