@@ -713,7 +713,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 constexpr size_t kMaxLds = 160 * 1024;
-// the streaming kernel's static LDS (cost prefix, scan totals, step counter), with some margin
+// the streaming kernel's static LDS (cost prefix, scan totals, zero operands, step counter), with
+// some margin; launch_stream checks the compiled size against it
 constexpr size_t kStreamStaticLds = (kMaxExperts + 1 + kSWaves) * sizeof(int64_t) + 256;
 
 // A streaming launch: one workgroup per CU, routes per pass, and the tiles whose partials fit in
@@ -751,10 +752,22 @@ StreamPlan stream_plan(int rows, int K, int E, int R) {
     return p;
 }
 
+// Refuses (rather than dispatches) a launch whose dynamic plus static LDS would exceed the CU's.
+template <int FMT, int NQ, bool SW>
+hipError_t launch_stream_nq(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
+    static const size_t static_lds = [] {
+        hipFuncAttributes fa{};
+        return hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&stream_kernel<FMT, NQ, SW>)) == hipSuccess
+                   ? fa.sharedSizeBytes
+                   : kMaxLds;
+    }();
+    if (p.lds + static_lds > kMaxLds) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((stream_kernel<FMT, NQ, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+    return hipGetLastError();
+}
 template <int FMT, bool SW>
-void launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
-    if (p.nq == 4) hipLaunchKernelGGL((stream_kernel<FMT, 4, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
-    else hipLaunchKernelGGL((stream_kernel<FMT, 2, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+hipError_t launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
+    return p.nq == 4 ? launch_stream_nq<FMT, 4, SW>(p, a, s) : launch_stream_nq<FMT, 2, SW>(p, a, s);
 }
 
 // The streaming down kernel reads Q5_0 / Q8_0 4-block chunks as aligned dwords (88 and 136 bytes,
@@ -814,7 +827,8 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
     if (up.ok) {
         const StreamArgs ua{wg,  wu,  g_eb, g_rb,   x,         k,          gr.list, gr.seg,
                             gr.nsel, act, ffn, K, K / 256, (ffn + 15) / 16, up.piece};
-        launch_stream<T_Q4_K, true>(up, ua, s);
+        const hipError_t e = launch_stream<T_Q4_K, true>(up, ua, s);
+        if (e != hipSuccess) return e;
     } else {
         const UpArgs ua{wg, wu, g_eb, g_rb, x, gr, act, ffn, K, k};
         const size_t lds = static_cast<size_t>(kGroup) * (4 * K + K / 8);
@@ -831,9 +845,10 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
         const int nchunk = ffn / (d_type == T_Q4_K ? 256 : 128);
         const StreamArgs da{wd,      wd, d_eb,   d_rb, act,    1,                  gr.list, gr.seg,
                             gr.nsel, yr, hidden, ffn,  nchunk, (hidden + 15) / 16, dn.piece};
-        if (d_type == T_Q5_0) launch_stream<T_Q5_0, false>(dn, da, s);
-        else if (d_type == T_Q8_0) launch_stream<T_Q8_0, false>(dn, da, s);
-        else launch_stream<T_Q4_K, false>(dn, da, s);
+        const hipError_t e = d_type == T_Q5_0   ? launch_stream<T_Q5_0, false>(dn, da, s)
+                             : d_type == T_Q8_0 ? launch_stream<T_Q8_0, false>(dn, da, s)
+                                                : launch_stream<T_Q4_K, false>(dn, da, s);
+        if (e != hipSuccess) return e;
     } else {
         const DownArgs da{wd, d_eb, d_rb, act, gr, yr, hidden, ffn};
         const dim3 dgrid(E, (hidden + 63) / 64);

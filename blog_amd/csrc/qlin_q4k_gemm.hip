@@ -30,11 +30,23 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
+#ifndef QLIN_GEMM_WAVES
+#define QLIN_GEMM_WAVES 8
+#endif
+#ifndef QLIN_GEMM_NT
+#define QLIN_GEMM_NT 2
+#endif
+constexpr int kWaves = QLIN_GEMM_WAVES;
 constexpr int kThreads = kWaves * 64;
-constexpr int kNT = 2;                    // 16-row weight tiles per wave
+constexpr int kNT = QLIN_GEMM_NT;         // 16-row weight tiles per wave
 constexpr int kBN = kWaves * kNT * 16;    // weight rows per workgroup (256)
-constexpr int kMT = 4;                    // 16-token tiles per workgroup
+#ifndef QLIN_GEMM_SB
+#define QLIN_GEMM_SB 1
+#endif
+#ifndef QLIN_GEMM_MT
+#define QLIN_GEMM_MT 4
+#endif
+constexpr int kMT = QLIN_GEMM_MT;         // 16-token tiles per workgroup
 constexpr int kBM = kMT * 16;             // tokens per workgroup (64)
 constexpr int kPlane = 2 * kMT * 8 * 64;  // uint4s of one buffer's A planes (hi, lo): 64 KB
 constexpr int kBuf = kPlane + kMT * 64;   // plus the min-term operands [mt][lane] (lanes >= 16 stay zero)
@@ -222,7 +234,9 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
                 }
             // no hoisting of the next sub-block's LDS reads above these MFMAs: the registers they
             // would hold push the kernel past its 256 VGPRs (measured 3% faster)
+#if QLIN_GEMM_SB
             __builtin_amdgcn_sched_barrier(0);
+#endif
         };
         sub_block(std::integral_constant<int, 0>{});
         sub_block(std::integral_constant<int, 1>{});
