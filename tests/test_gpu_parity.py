@@ -614,6 +614,25 @@ def test_gemv_multi_c3_qkv():
         assert normwise_rel_err(host(y), orc.matmul_f64(Q8_0, w, rb, x, n, 896)[0]) <= FP32
 
 
+@pytest.mark.parametrize("qtype,in_dim", [(Q4_K, 256), (Q4_K, 768), (Q4_0, 256), (Q4_0, 512), (Q8_0, 128),
+                                          (Q8_0, 384), (Q6_K, 256)])
+def test_gemv_multi_four_ragged(qtype, in_dim):
+    """Four matrices of ragged row counts (1, 17, 33, 300) in one launch: the per-row matrix lookup,
+    row slices that end mid-tile, and a single chunk per row at the smallest in_dim."""
+    shapes = [17, 1, 33, 300]
+    mats = [qgen.random_matrix(qtype, n, in_dim, seed=700 + 13 * i + qtype) for i, n in enumerate(shapes)]
+    x = qgen.random_x(1, in_dim, seed=710 + in_dim)
+    ys = [empty_f32(n) for n in shapes]
+    banner(f"gemv multi four ragged type={qtype} K={in_dim}")
+    qlin.quant_gemv_multi(qtype, [dev(w) for w, _, _ in mats], mats[0][1], dev(x), ys, shapes, in_dim)
+    for (w, rb, vals), y, n in zip(mats, ys, shapes):
+        # a 1-row matrix is a single dot product: judged, as test_gemv_parity does, against its
+        # conditioning (sum |w x|) as well as normwise
+        yh, ref = host(y), orc.matmul_f64(qtype, w, rb, x, n, in_dim)[0]
+        assert normwise_rel_err(yh, ref) <= GATE
+        assert cond_err(yh, ref, vals, x) <= COND
+
+
 def test_gemv_multi_generic_types():
     """Non-Q4_K types take one launch per matrix behind the same entry point."""
     mats = [qgen.random_matrix(Q8_0, n, 512, seed=500 + n) for n in (33, 64)]
