@@ -44,11 +44,12 @@
 //   Their blocks are only 2-byte aligned, so each lane loads aligned dwords and realigns them
 //     with v_alignbyte_b32.
 //
-// Work decomposition.  One workgroup per CU owns a contiguous slice of the rows.  Its work is the
-// flat sequence of steps (16-row tile, matrix, super-block), in memory order; the waves claim the
-// steps one at a time from an LDS counter, so the workgroup reads one compact window that slides
-// along its slice (waves with separate contiguous ranges each open their own window, and HBM
-// serves many scattered windows measurably slower), and no wave is left with a backlog at the end.
+// Work decomposition.  One workgroup per CU; workgroup b of G owns the 16-row tiles b, b + G, ...,
+// so that the workgroups sweep one region of the weights together.  Its work is the flat sequence
+// of steps (tile, matrix, super-block), in memory order; the waves claim the steps one at a time
+// from an LDS counter, so the workgroup reads one compact window that slides along its tiles
+// (waves with separate contiguous ranges each open their own window, and HBM serves many scattered
+// windows measurably slower), and no wave is left with a backlog at the end.
 // A wave loads the step it will compute next while it computes the current one, and parks each
 // step's 16 row sums in LDS; they are added in super-block order at the end (deterministic) and
 // only then is y written.
@@ -73,6 +74,12 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 // Steps in flight per wave while one is computed.  2 (a ring of three buffers) measured 9% slower
 // over the decode step than 1: more outstanding requests per CU serve worse on this memory system.
 #define QLIN_MFMA_DEPTH 1
+#endif
+// Workgroup b of G takes 16-row tiles b, b + G, b + 2G, ... (1), so that all workgroups sweep one
+// region of the weights together, rather than a contiguous slice each (0): 1.6% faster over the
+// decode step (gate/up and lm_head, the launches with several tiles per workgroup).
+#ifndef QLIN_MFMA_INTERLEAVE
+#define QLIN_MFMA_INTERLEAVE 1
 #endif
 #ifndef QLIN_MFMA_FINAL_UNROLL
 #define QLIN_MFMA_FINAL_UNROLL 4  // batches the final per-row sum's LDS reads (same order of adds)
@@ -169,9 +176,18 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int bid = blockIdx.x;
+#if QLIN_MFMA_INTERLEAVE
+    // 16-row tiles bid, bid + G, bid + 2G, ... (G workgroups): all workgroups sweep one region
+    // (rows_q, rows_r here count tiles: tiles / G and tiles % G, from the host)
+    const int G = gridDim.x;
+    const int ntl = a.rows_q + (bid < a.rows_r ? 1 : 0);
+    const int nrows = ntl ? (ntl - 1) * 16 + min(16, a.total - 16 * (bid + (ntl - 1) * G)) : 0;
+    auto grow = [&](int lr) { return 16 * (bid + (lr >> 4) * G) + (lr & 15); };  // global row of local row lr
+#else
     const int rb = bid * a.rows_q + min(bid, a.rows_r);
     const int nrows = a.rows_q + (bid < a.rows_r ? 1 : 0);
-    const int re = rb + nrows;
+    auto grow = [&](int lr) { return rb + lr; };
+#endif
     // The workgroup's work is the flat sequence of steps (16-row tile, matrix, super-block), which
     // is also the order of the bytes in memory; the waves claim them in that order, so that at any
     // time the workgroup reads one compact window of its rows.
@@ -238,7 +254,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         p.sb = c - p.tw * nsb;
         int tile, which;
         split_tw(p.tw, tile, which);
-        const int gr = min(rb + tile * 16 + n, re - 1);
+        const int gr = grow(min(tile * 16 + n, nrows - 1));
         if constexpr (SWIGLU) {
             p.rp = (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes;
         } else {
@@ -514,7 +530,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 #endif
             for (int sb = 0; sb < nsb; ++sb) tot[q] += partial[(r * NW + q) * nsb + sb];
         }
-        const int gr = rb + r;
+        const int gr = grow(r);
         if constexpr (SWIGLU) {
             mats.y[0][gr] = tot[0] / (1.0f + expf(-tot[0])) * tot[1];
         } else {
@@ -536,7 +552,7 @@ struct Plan {
 Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
     Plan p;
     p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
-    const int rows = (total + p.grid - 1) / p.grid;
+    const int rows = QLIN_MFMA_INTERLEAVE ? ((total + 15) / 16 + p.grid - 1) / p.grid * 16 : (total + p.grid - 1) / p.grid;
     const uint64_t steps = static_cast<uint64_t>((rows + 15) / 16) * (swiglu ? 2 : 1) * nsb;
     p.magic_exact = steps * static_cast<uint64_t>(nsb) < (uint64_t{1} << 32);
     const size_t K = static_cast<size_t>(k);
@@ -575,8 +591,9 @@ int sum_elems(int type) { return type == T_Q6_K ? kSumElems<T_Q6_K> : kSumElems<
 hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
     const Plan p = plan(a.total, k, a.nsb, swiglu, sum_elems(type));
     if (!p.magic_exact) return hipErrorInvalidValue;  // mfma_ok rejects these shapes first
-    a.rows_q = a.total / p.grid;
-    a.rows_r = a.total % p.grid;
+    const int units = QLIN_MFMA_INTERLEAVE ? (a.total + 15) / 16 : a.total;  // tiles or rows per workgroup
+    a.rows_q = units / p.grid;
+    a.rows_r = units % p.grid;
     a.nsb_magic = a.nsb > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + a.nsb - 1) / a.nsb) : 0u;
     switch (type) {
         case T_Q4_K: launch_fmt<T_Q4_K>(p, a, k, swiglu, s); break;
