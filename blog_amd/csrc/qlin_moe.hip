@@ -47,16 +47,27 @@ __global__ __launch_bounds__(64) void router_kernel(const float *__restrict__ lo
     }
     float maxv = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
     maxv = wave_max(maxv);
-    __shared__ float ex[256];
+    __shared__ __attribute__((aligned(16))) float ex[256];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         if (lane + 64 * j < ne) ex[lane + 64 * j] = isfinite(maxv) ? expf(v[j] - maxv) : 0.0f;
     __syncthreads();
     __shared__ float denom_s;
     if (lane == 0) {
+        // summed in expert order, as the reference's one thread per token does; the reads go 4 at a
+        // time, so that the adds wait on few LDS round trips
         float denom = 0.0f;
-        if (isfinite(maxv))
-            for (int e = 0; e < ne; ++e) denom += ex[e];
+        if (isfinite(maxv)) {
+            const int n4 = ne >> 2;
+            for (int i = 0; i < n4; ++i) {
+                const float4 q = reinterpret_cast<const float4 *>(ex)[i];
+                denom += q.x;
+                denom += q.y;
+                denom += q.z;
+                denom += q.w;
+            }
+            for (int e = 4 * n4; e < ne; ++e) denom += ex[e];
+        }
         denom_s = denom;
     }
     __syncthreads();
