@@ -94,6 +94,12 @@ __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x
                                                    0, 0, 0);
 }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+// v_mfma_i32_16x16x64_i8: 16 int8 k-slots per lane in A and B alike, exact int32 accumulation.
+__device__ __forceinline__ i32x4 mfma_i8(const i32x4 &a, const i32x4 &b, const i32x4 &c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; D as above.
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);

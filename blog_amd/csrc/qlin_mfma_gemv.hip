@@ -16,6 +16,13 @@
 // to within 2^-18 |x|; products are exact and accumulate in f32.  The 128 offset is removed in the
 // epilogue with the sub-block sums X = sum(hi + lo).
 //
+// Q4_K with a short x (at most 2 float4s per thread, e.g. K = 3584) runs on the int8 matrix cores
+// instead (v_mfma_i32_16x16x64_i8, half the MFMAs and about a third less VALU per step): per 32
+// elements x = 2^e (d1 + d2/128 + d3/16384) with int8 digits in [-64, 64] and max|x| < 2^(e+6), so
+// each element is represented to within 2^(e-15) < 2^-21 of its block's largest |x|; the nibbles
+// are the int8 B operand as they are, and every digit's dot is exact in int32.  A long x (the down
+// projection) keeps the bf16 form, whose staging costs about half.
+//
 // Operands of one MFMA (16 weight rows n, K = 32; lane l supplies row or column l % 16 and the
 // eight k-slots 8*(l/16) .. 8*(l/16)+7, the same slots in A and B):
 //   B (weights): lane (n, g = l/16) takes dword t of sub-block pair g of its row -- 4 low nibbles
@@ -80,6 +87,12 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 // decode step (gate/up and lm_head, the launches with several tiles per workgroup).
 #ifndef QLIN_MFMA_INTERLEAVE
 #define QLIN_MFMA_INTERLEAVE 1
+#endif
+// Q4_K on the int8 matrix cores: 0 never, 1 the SwiGLU pair, 2 every launch, 3 launches whose
+// threads stage at most 2 float4s of x.  3 is the fastest: the digit staging costs about twice the
+// bf16 one, which the long x of a down projection (K = 18944) does not repay.
+#ifndef QLIN_MFMA_I8
+#define QLIN_MFMA_I8 3
 #endif
 #ifndef QLIN_MFMA_FINAL_UNROLL
 #define QLIN_MFMA_FINAL_UNROLL 4  // batches the final per-row sum's LDS reads (same order of adds)
@@ -170,9 +183,15 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int XS = kSumElems<FMT>;
     const int nsb = a.nsb, K = nsb * CE;
+    // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
+    // per 32 elements, in no more LDS than the bf16 layout takes (3K + K/4 against 4K + K/8 bytes)
+    constexpr bool I8 = FMT == T_Q4_K && (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) ||
+                                          (QLIN_MFMA_I8 == 3 && XR <= 2));
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
     float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/XS] sum(hi + lo) per XS elements
     float *partial = xsum + K / XS;                                // [rows][NW][nsb]
+    int8_t *planes = reinterpret_cast<int8_t *>(smem);                    // I8: [3][K]
+    float *sxp = reinterpret_cast<float *>(smem + 3 * static_cast<size_t>(K));  // I8: [K/32][2] (scale, sum)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int bid = blockIdx.x;
@@ -211,6 +230,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // n >> 1 == 2g, of MFMAs 4..7 when n >> 1 == 2g + 1, and zeros otherwise, so each A operand is
     // 16 bytes read from the staged x or from a zero area (stride 0), with no selects.
     constexpr bool kDirectA = FMT != T_Q6_K;
+    // I8 A operand: row n is digit n & 3 (3: none) of sub-block 2g (MFMAs 0, 1) and 2g + 1 (2, 3)
+    // of lane group g = n >> 2; its 4 x 16 bytes are the pair's 64 consecutive plane bytes
+    const bool i8_on = (n >> 2) == g && (n & 3) < 3;
+    const int8_t *a8 = planes + (n & 3) * K + 64 * g;  // read only when i8_on (else the zero area)
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
     int a_lo_st, a_hi_st;
@@ -303,7 +326,58 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 #pragma unroll
     for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
 
+    auto stage_x_i8 = [&]() {
+        // per 32 elements: e with max|x| < 2^(e+6), so t = x / 2^e is below 64 in magnitude; digits
+        // d1 = rint(t), d2 = rint(128 (t - d1)), d3 = rint(128 (128 (t - d1) - d2)), each in
+        // [-64, 64]; x = 2^e (d1 + d2 / 128 + d3 / 16384) to within 2^(e-15).  rint is the low byte
+        // of t + 1.5 * 2^23 (round to nearest even, exact for |t| < 2^22).
+        constexpr float kMagic = 12582912.0f;
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int i = tid + r * kThreads;
+            const float xe[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+            float mx = fmaxf(fmaxf(fabsf(xe[0]), fabsf(xe[1])), fmaxf(fabsf(xe[2]), fabsf(xe[3])));
+            float sm = ((xe[0] + xe[1]) + xe[2]) + xe[3];
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+            sm += __shfl_xor(sm, 1, 64);
+            sm += __shfl_xor(sm, 2, 64);
+            sm += __shfl_xor(sm, 4, 64);
+            int ex;
+            (void)frexpf(mx, &ex);
+            const int e = ex - 6;
+            uint32_t b[3][4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float t = ldexpf(xe[k], -e);
+                const float f1 = t + kMagic, r1 = t - (f1 - kMagic);
+                const float u = r1 * 128.0f;
+                const float f2 = u + kMagic, r2 = u - (f2 - kMagic);
+                const float f3 = r2 * 128.0f + kMagic;
+                b[0][k] = __builtin_bit_cast(uint32_t, f1);
+                b[1][k] = __builtin_bit_cast(uint32_t, f2);
+                b[2][k] = __builtin_bit_cast(uint32_t, f3);
+            }
+            if (i < K / 4) {
+#pragma unroll
+                for (int d = 0; d < 3; ++d) {
+                    const uint32_t lo = __builtin_amdgcn_perm(b[d][1], b[d][0], 0x0c0c0400u);
+                    const uint32_t hi = __builtin_amdgcn_perm(b[d][3], b[d][2], 0x04000c0cu);
+                    reinterpret_cast<uint32_t *>(planes + d * K)[i] = lo | hi;
+                }
+                // a non-finite x makes the block's scale NaN, so that the dot is NaN as in f32
+                if ((i & 7) == 0)
+                    reinterpret_cast<float2 *>(sxp)[i >> 3] =
+                        make_float2(isfinite(sm) && isfinite(mx) ? ldexpf(1.0f, e) : __builtin_nanf(""), sm);
+            }
+        }
+    };
     auto stage_x = [&]() {
+        if constexpr (I8) {
+            stage_x_i8();
+            return;
+        }
         // bf16 hi / lo parts and the per-sub-block sums of hi + lo
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
@@ -349,6 +423,44 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // One step: the 16 rows' dots with super-block sb, parked in LDS (each (row, matrix, sb) slot is
     // written by exactly one step; a global store here would share vmcnt with the weight stream).
     auto process = [&](const Raw &cur, const Pos &p) {
+        if constexpr (I8) {
+            // Q4_K on the int8 matrix cores: B takes the nibbles themselves (MFMAs 0, 1: low
+            // nibbles of the pair's bytes 0..15, 16..31 = sub-block 2g; 2, 3: the high nibbles =
+            // sub-block 2g + 1), A the x digits; D rows 4g + r are digit r's dots, exact in int32.
+            const i32x4 *pa = reinterpret_cast<const i32x4 *>(i8_on ? a8 + p.sb * CE : reinterpret_cast<const int8_t *>(s_zero));
+            constexpr uint32_t M = 0x0f0f0f0fu;
+            const i32x4 b0 = {static_cast<int>(cur.w[4] & M), static_cast<int>(cur.w[5] & M),
+                              static_cast<int>(cur.w[6] & M), static_cast<int>(cur.w[7] & M)};
+            const i32x4 b1 = {static_cast<int>(cur.w[8] & M), static_cast<int>(cur.w[9] & M),
+                              static_cast<int>(cur.w[10] & M), static_cast<int>(cur.w[11] & M)};
+            const i32x4 b2 = {static_cast<int>((cur.w[4] >> 4) & M), static_cast<int>((cur.w[5] >> 4) & M),
+                              static_cast<int>((cur.w[6] >> 4) & M), static_cast<int>((cur.w[7] >> 4) & M)};
+            const i32x4 b3 = {static_cast<int>((cur.w[8] >> 4) & M), static_cast<int>((cur.w[9] >> 4) & M),
+                              static_cast<int>((cur.w[10] >> 4) & M), static_cast<int>((cur.w[11] >> 4) & M)};
+            i32x4 de = mfma_i8(pa[0], b0, i32x4{0, 0, 0, 0});
+            de = mfma_i8(pa[1], b1, de);
+            i32x4 dq = mfma_i8(pa[2], b2, i32x4{0, 0, 0, 0});
+            dq = mfma_i8(pa[3], b3, dq);
+            const float4 sx = *reinterpret_cast<const float4 *>(sxp + p.sb * 16 + 4 * g);  // s, X of 2g, 2g + 1
+            const float dote = sx.x * (static_cast<float>(de[0]) + (static_cast<float>(de[1]) * 0.0078125f +
+                                                                    static_cast<float>(de[2]) * 6.103515625e-05f));
+            const float doto = sx.z * (static_cast<float>(dq[0]) + (static_cast<float>(dq[1]) * 0.0078125f +
+                                                                    static_cast<float>(dq[2]) * 6.103515625e-05f));
+            uint32_t scp, mp;
+            dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
+            const float dd = f16_bits_to_f32(cur.w[0] & 0xffffu);
+            const float dmin = f16_bits_to_f32(cur.w[0] >> 16);
+            float r = dd * static_cast<float>(scp & 0xffu) * dote;
+            r = fmaf(dd * static_cast<float>((scp >> 8) & 0xffu), doto, r);
+            r = fmaf(-dmin * static_cast<float>(mp & 0xffu), sx.y, r);
+            r = fmaf(-dmin * static_cast<float>((mp >> 8) & 0xffu), sx.w, r);
+            r = sum_lane_groups(r);
+            int tile, which;
+            split_tw(p.tw, tile, which);
+            const int lr = tile * 16 + n;
+            if (g == 0 && lr < nrows) partial[(lr * NW + which) * nsb + p.sb] = r;
+            return;
+        }
         // A operands of this chunk (x only): the lane's 32 values of its part / sub-block (Q8_0: the
         // block both nibble sub-blocks of the pair come from).
         if constexpr (kDirectA) {
