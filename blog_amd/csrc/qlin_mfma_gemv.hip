@@ -16,11 +16,12 @@
 // to within 2^-18 |x|; products are exact and accumulate in f32.  The 128 offset is removed in the
 // epilogue with the sub-block sums X = sum(hi + lo).
 //
-// Q4_K with a short x (at most 2 float4s per thread, e.g. K = 3584) runs on the int8 matrix cores
-// instead (v_mfma_i32_16x16x64_i8, half the MFMAs and about a third less VALU per step): per 32
+// Q4_K, Q4_0 and Q8_0 with a short x (at most 2 float4s per thread, e.g. K = 3584) run on the int8
+// matrix cores instead (v_mfma_i32_16x16x64_i8, half the MFMAs and about a third less VALU per step): per 32
 // elements x = 2^e (d1 + d2/128 + d3/16384) with int8 digits in [-64, 64] and max|x| < 2^(e+6), so
-// each element is represented to within 2^(e-15) < 2^-21 of its block's largest |x|; the nibbles
-// are the int8 B operand as they are, and every digit's dot is exact in int32.  A long x (the down
+// each element is represented to within 2^(e-15) < 2^-21 of its block's largest |x|; the stored
+// integers (nibbles, Q8_0 bytes) are the int8 B operand as they are, and every digit's dot is exact
+// in int32 (Q4_0's q - 8 leaves with the block sums, as the bf16 form's 128 offset does).  A long x (the down
 // projection) keeps the bf16 form, whose staging costs about half.
 //
 // Operands of one MFMA (16 weight rows n, K = 32; lane l supplies row or column l % 16 and the
@@ -185,8 +186,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     const int nsb = a.nsb, K = nsb * CE;
     // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
     // per 32 elements, in no more LDS than the bf16 layout takes (3K + K/4 against 4K + K/8 bytes)
-    constexpr bool I8 = FMT == T_Q4_K && (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) ||
-                                          (QLIN_MFMA_I8 == 3 && XR <= 2));
+    constexpr bool I8 = (FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0) &&
+                        (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) || (QLIN_MFMA_I8 == 3 && XR <= 2));
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
     float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/XS] sum(hi + lo) per XS elements
     float *partial = xsum + K / XS;                                // [rows][NW][nsb]
@@ -230,10 +231,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // n >> 1 == 2g, of MFMAs 4..7 when n >> 1 == 2g + 1, and zeros otherwise, so each A operand is
     // 16 bytes read from the staged x or from a zero area (stride 0), with no selects.
     constexpr bool kDirectA = FMT != T_Q6_K;
-    // I8 A operand: row n is digit n & 3 (3: none) of sub-block 2g (MFMAs 0, 1) and 2g + 1 (2, 3)
-    // of lane group g = n >> 2; its 4 x 16 bytes are the pair's 64 consecutive plane bytes
+    // I8 A operand: row n is digit n & 3 (3: none) of the 32-element units of lane group g = n >> 2:
+    // Q4_K sub-blocks 2g (MFMAs 0, 1) and 2g + 1 (2, 3), Q4_0 blocks 2g and 2g + 1 likewise (their 4
+    // x 16 bytes are 64 consecutive plane bytes), Q8_0 block g (MFMAs 0, 1: 32 bytes)
     const bool i8_on = (n >> 2) == g && (n & 3) < 3;
-    const int8_t *a8 = planes + (n & 3) * K + 64 * g;  // read only when i8_on (else the zero area)
+    const int8_t *a8 = planes + (n & 3) * K + (FMT == T_Q8_0 ? 32 : 64) * g;  // read only when i8_on
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
     int a_lo_st, a_hi_st;
@@ -424,36 +426,74 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // written by exactly one step; a global store here would share vmcnt with the weight stream).
     auto process = [&](const Raw &cur, const Pos &p) {
         if constexpr (I8) {
-            // Q4_K on the int8 matrix cores: B takes the nibbles themselves (MFMAs 0, 1: low
-            // nibbles of the pair's bytes 0..15, 16..31 = sub-block 2g; 2, 3: the high nibbles =
-            // sub-block 2g + 1), A the x digits; D rows 4g + r are digit r's dots, exact in int32.
+            // The int8 matrix cores: B takes the stored integers themselves (Q4_K / Q4_0 nibbles, Q8_0
+            // bytes), A the x digits; D rows 4g + r are digit r's dots of a unit, exact in int32.
             const i32x4 *pa = reinterpret_cast<const i32x4 *>(i8_on ? a8 + p.sb * CE : reinterpret_cast<const int8_t *>(s_zero));
             constexpr uint32_t M = 0x0f0f0f0fu;
-            const i32x4 b0 = {static_cast<int>(cur.w[4] & M), static_cast<int>(cur.w[5] & M),
-                              static_cast<int>(cur.w[6] & M), static_cast<int>(cur.w[7] & M)};
-            const i32x4 b1 = {static_cast<int>(cur.w[8] & M), static_cast<int>(cur.w[9] & M),
-                              static_cast<int>(cur.w[10] & M), static_cast<int>(cur.w[11] & M)};
-            const i32x4 b2 = {static_cast<int>((cur.w[4] >> 4) & M), static_cast<int>((cur.w[5] >> 4) & M),
-                              static_cast<int>((cur.w[6] >> 4) & M), static_cast<int>((cur.w[7] >> 4) & M)};
-            const i32x4 b3 = {static_cast<int>((cur.w[8] >> 4) & M), static_cast<int>((cur.w[9] >> 4) & M),
-                              static_cast<int>((cur.w[10] >> 4) & M), static_cast<int>((cur.w[11] >> 4) & M)};
-            i32x4 de = mfma_i8(pa[0], b0, i32x4{0, 0, 0, 0});
-            de = mfma_i8(pa[1], b1, de);
-            i32x4 dq = mfma_i8(pa[2], b2, i32x4{0, 0, 0, 0});
-            dq = mfma_i8(pa[3], b3, dq);
-            const float4 sx = *reinterpret_cast<const float4 *>(sxp + p.sb * 16 + 4 * g);  // s, X of 2g, 2g + 1
-            const float dote = sx.x * (static_cast<float>(de[0]) + (static_cast<float>(de[1]) * 0.0078125f +
-                                                                    static_cast<float>(de[2]) * 6.103515625e-05f));
-            const float doto = sx.z * (static_cast<float>(dq[0]) + (static_cast<float>(dq[1]) * 0.0078125f +
-                                                                    static_cast<float>(dq[2]) * 6.103515625e-05f));
-            uint32_t scp, mp;
-            dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
-            const float dd = f16_bits_to_f32(cur.w[0] & 0xffffu);
-            const float dmin = f16_bits_to_f32(cur.w[0] >> 16);
-            float r = dd * static_cast<float>(scp & 0xffu) * dote;
-            r = fmaf(dd * static_cast<float>((scp >> 8) & 0xffu), doto, r);
-            r = fmaf(-dmin * static_cast<float>(mp & 0xffu), sx.y, r);
-            r = fmaf(-dmin * static_cast<float>((mp >> 8) & 0xffu), sx.w, r);
+            // the 8 dwords of this lane's stored integers: Q4_K the pair's 32 bytes; Q4_0 blocks 2g,
+            // 2g + 1 (16 bytes each); Q8_0 block g's 32 bytes
+            uint32_t src[8];
+            if constexpr (FMT == T_Q4_K) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) src[k] = cur.w[4 + k];
+            } else if constexpr (FMT == T_Q4_0) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) src[k] = __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) src[4 + k] = cur.w[5 + k];
+            } else {
+                const bool odd = g & 1;  // odd blocks start 2 bytes into the first dword
+#pragma unroll
+                for (int k = 0; k < 8; ++k) src[k] = odd ? cur.w[k + 1] : __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2);
+            }
+            auto nib = [&](int k0, int sh) {
+                return i32x4{static_cast<int>((src[k0] >> sh) & M), static_cast<int>((src[k0 + 1] >> sh) & M),
+                             static_cast<int>((src[k0 + 2] >> sh) & M), static_cast<int>((src[k0 + 3] >> sh) & M)};
+            };
+            auto digits = [](const i32x4 &d) {
+                return static_cast<float>(d[0]) + (static_cast<float>(d[1]) * 0.0078125f +
+                                                   static_cast<float>(d[2]) * 6.103515625e-05f);
+            };
+            float r;
+            if constexpr (FMT == T_Q8_0) {
+                const i32x4 b0 = {static_cast<int>(src[0]), static_cast<int>(src[1]), static_cast<int>(src[2]),
+                                  static_cast<int>(src[3])};
+                const i32x4 b1 = {static_cast<int>(src[4]), static_cast<int>(src[5]), static_cast<int>(src[6]),
+                                  static_cast<int>(src[7])};
+                i32x4 de = mfma_i8(pa[0], b0, i32x4{0, 0, 0, 0});
+                de = mfma_i8(pa[1], b1, de);
+                const float2 sx = *reinterpret_cast<const float2 *>(sxp + 2 * (p.sb * 4 + g));  // s of block g
+                const float dq = f16_bits_to_f32((cur.w[0] >> (16 * (g & 1))) & 0xffffu);
+                r = dq * (sx.x * digits(de));
+            } else {
+                // MFMAs 0, 1 carry unit 2g (Q4_K: low nibbles of bytes 0..15, 16..31; Q4_0: block 2g's
+                // low, then high nibbles), 2, 3 unit 2g + 1
+                const i32x4 b0 = nib(0, 0);
+                const i32x4 b1 = FMT == T_Q4_K ? nib(4, 0) : nib(0, 4);
+                const i32x4 b2 = FMT == T_Q4_K ? nib(0, 4) : nib(4, 0);
+                const i32x4 b3 = nib(4, 4);
+                i32x4 de = mfma_i8(pa[0], b0, i32x4{0, 0, 0, 0});
+                de = mfma_i8(pa[1], b1, de);
+                i32x4 dq = mfma_i8(pa[2], b2, i32x4{0, 0, 0, 0});
+                dq = mfma_i8(pa[3], b3, dq);
+                const float4 sx = *reinterpret_cast<const float4 *>(sxp + p.sb * 16 + 4 * g);  // s, X of 2g, 2g + 1
+                const float dote = sx.x * digits(de), doto = sx.z * digits(dq);
+                if constexpr (FMT == T_Q4_K) {
+                    uint32_t scp, mp;
+                    dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
+                    const float dd = f16_bits_to_f32(cur.w[0] & 0xffffu);
+                    const float dmin = f16_bits_to_f32(cur.w[0] >> 16);
+                    r = dd * static_cast<float>(scp & 0xffu) * dote;
+                    r = fmaf(dd * static_cast<float>((scp >> 8) & 0xffu), doto, r);
+                    r = fmaf(-dmin * static_cast<float>(mp & 0xffu), sx.y, r);
+                    r = fmaf(-dmin * static_cast<float>((mp >> 8) & 0xffu), sx.w, r);
+                } else {
+                    // q - 8: the offset leaves with the block sums
+                    const float d0 = f16_bits_to_f32(cur.w[0] & 0xffffu), d1 = f16_bits_to_f32(cur.w[4] >> 16);
+                    r = d0 * (dote - 8.0f * sx.y);
+                    r = fmaf(d1, doto - 8.0f * sx.w, r);
+                }
+            }
             r = sum_lane_groups(r);
             int tile, which;
             split_tw(p.tw, tile, which);
