@@ -165,7 +165,7 @@ def main() -> int:
                    "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "mfma_gemv_kernel<12, true, 2> (Q4_K gate/up SwiGLU, 2 x [18944, 3584])",
+                     "kernel": "mfma_gemv_kernel<12, true, 1> (Q4_K gate/up SwiGLU, 2 x [18944, 3584])",
                      "avg_launch_us": round(launch_us, 3),
                      "algorithmic_bytes_per_launch": gate_bytes},
     }

@@ -71,10 +71,10 @@ namespace {
 #ifndef QLIN_MFMA_WAVES
 #define QLIN_MFMA_WAVES 16
 #endif
-// The SwiGLU pair runs 12 waves per workgroup: 6% faster than 16 on the 2 x [18944, 3584] pair,
-// while the single-matrix launches (down above all) are fastest with 16.
+// Waves per workgroup of the SwiGLU pair.  With bf16 operands 12 was 3-6% faster than 16 on the
+// 2 x [18944, 3584] pair; with the int8 operands 16 is (15.6 against 16.1 us).
 #ifndef QLIN_MFMA_SW_WAVES
-#define QLIN_MFMA_SW_WAVES 12
+#define QLIN_MFMA_SW_WAVES 16
 #endif
 constexpr int waves_for(bool swiglu) { return swiglu ? QLIN_MFMA_SW_WAVES : QLIN_MFMA_WAVES; }
 constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
