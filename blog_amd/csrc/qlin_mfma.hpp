@@ -95,6 +95,55 @@ __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// x as int8 digits, for the int8 matrix cores.  Called by the 8 consecutive lanes that hold the 4
+// elements each of one 32-element block: with e such that max|x| < 2^(e+6), t = x / 2^e is below 64
+// in magnitude and x = 2^e (d1 + d2 / 128 + d3 / 16384) to within 2^(e-15), the digits
+//   d1 = rint(t), d2 = rint(128 (t - d1)), d3 = rint(128 (128 (t - d1) - d2))
+// each in [-64, 64] (rint is the low byte of t + 1.5 * 2^23: round to nearest even, exact for
+// |t| < 2^22; every residual above is exact).  Gives the lane's 4 digits of each kind packed in a
+// dword, and the block's scale 2^e (NaN if any of its x is not finite) and sum of x.
+__device__ __forceinline__ void x_digits4(const float4 &v, uint32_t &p1, uint32_t &p2, uint32_t &p3, float &scale,
+                                          float &sum) {
+    constexpr float kMagic = 12582912.0f;
+    const float xe[4] = {v.x, v.y, v.z, v.w};
+    float mx = fmaxf(fmaxf(fabsf(xe[0]), fabsf(xe[1])), fmaxf(fabsf(xe[2]), fabsf(xe[3])));
+    float sm = ((xe[0] + xe[1]) + xe[2]) + xe[3];
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    sm += __shfl_xor(sm, 4, 64);
+    int ex;
+    (void)frexpf(mx, &ex);
+    const int e = ex - 6;
+    uint32_t b[3][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float t = ldexpf(xe[k], -e);
+        const float f1 = t + kMagic, r1 = t - (f1 - kMagic);
+        const float u = r1 * 128.0f;
+        const float f2 = u + kMagic, r2 = u - (f2 - kMagic);
+        const float f3 = r2 * 128.0f + kMagic;
+        b[0][k] = __builtin_bit_cast(uint32_t, f1);
+        b[1][k] = __builtin_bit_cast(uint32_t, f2);
+        b[2][k] = __builtin_bit_cast(uint32_t, f3);
+    }
+    uint32_t pk[3];
+#pragma unroll
+    for (int d = 0; d < 3; ++d)
+        pk[d] = __builtin_amdgcn_perm(b[d][1], b[d][0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[d][3], b[d][2], 0x04000c0cu);
+    p1 = pk[0];
+    p2 = pk[1];
+    p3 = pk[2];
+    scale = isfinite(sm) && isfinite(mx) ? ldexpf(1.0f, e) : __builtin_nanf("");
+    sum = sm;
+}
+// the value of a unit's three digit dots (exact integers) in units of its scale
+__device__ __forceinline__ float digits_value(const i32x4 &d) {
+    return static_cast<float>(d[0]) + (static_cast<float>(d[1]) * 0.0078125f + static_cast<float>(d[2]) * 6.103515625e-05f);
+}
 // v_mfma_i32_16x16x64_i8: 16 int8 k-slots per lane in A and B alike, exact int32 accumulation.
 __device__ __forceinline__ i32x4 mfma_i8(const i32x4 &a, const i32x4 &b, const i32x4 &c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);

@@ -329,49 +329,18 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
 
     auto stage_x_i8 = [&]() {
-        // per 32 elements: e with max|x| < 2^(e+6), so t = x / 2^e is below 64 in magnitude; digits
-        // d1 = rint(t), d2 = rint(128 (t - d1)), d3 = rint(128 (128 (t - d1) - d2)), each in
-        // [-64, 64]; x = 2^e (d1 + d2 / 128 + d3 / 16384) to within 2^(e-15).  rint is the low byte
-        // of t + 1.5 * 2^23 (round to nearest even, exact for |t| < 2^22).
-        constexpr float kMagic = 12582912.0f;
+        // x as three int8 digit planes and (scale, sum) per 32 elements (x_digits4)
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
             const int i = tid + r * kThreads;
-            const float xe[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
-            float mx = fmaxf(fmaxf(fabsf(xe[0]), fabsf(xe[1])), fmaxf(fabsf(xe[2]), fabsf(xe[3])));
-            float sm = ((xe[0] + xe[1]) + xe[2]) + xe[3];
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-            sm += __shfl_xor(sm, 1, 64);
-            sm += __shfl_xor(sm, 2, 64);
-            sm += __shfl_xor(sm, 4, 64);
-            int ex;
-            (void)frexpf(mx, &ex);
-            const int e = ex - 6;
-            uint32_t b[3][4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float t = ldexpf(xe[k], -e);
-                const float f1 = t + kMagic, r1 = t - (f1 - kMagic);
-                const float u = r1 * 128.0f;
-                const float f2 = u + kMagic, r2 = u - (f2 - kMagic);
-                const float f3 = r2 * 128.0f + kMagic;
-                b[0][k] = __builtin_bit_cast(uint32_t, f1);
-                b[1][k] = __builtin_bit_cast(uint32_t, f2);
-                b[2][k] = __builtin_bit_cast(uint32_t, f3);
-            }
+            uint32_t p1, p2, p3;
+            float sc, sm;
+            x_digits4(xv[r], p1, p2, p3, sc, sm);
             if (i < K / 4) {
-#pragma unroll
-                for (int d = 0; d < 3; ++d) {
-                    const uint32_t lo = __builtin_amdgcn_perm(b[d][1], b[d][0], 0x0c0c0400u);
-                    const uint32_t hi = __builtin_amdgcn_perm(b[d][3], b[d][2], 0x04000c0cu);
-                    reinterpret_cast<uint32_t *>(planes + d * K)[i] = lo | hi;
-                }
-                // a non-finite x makes the block's scale NaN, so that the dot is NaN as in f32
-                if ((i & 7) == 0)
-                    reinterpret_cast<float2 *>(sxp)[i >> 3] =
-                        make_float2(isfinite(sm) && isfinite(mx) ? ldexpf(1.0f, e) : __builtin_nanf(""), sm);
+                reinterpret_cast<uint32_t *>(planes)[i] = p1;
+                reinterpret_cast<uint32_t *>(planes + K)[i] = p2;
+                reinterpret_cast<uint32_t *>(planes + 2 * K)[i] = p3;
+                if ((i & 7) == 0) reinterpret_cast<float2 *>(sxp)[i >> 3] = make_float2(sc, sm);
             }
         }
     };
@@ -450,10 +419,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
                 return i32x4{static_cast<int>((src[k0] >> sh) & M), static_cast<int>((src[k0 + 1] >> sh) & M),
                              static_cast<int>((src[k0 + 2] >> sh) & M), static_cast<int>((src[k0 + 3] >> sh) & M)};
             };
-            auto digits = [](const i32x4 &d) {
-                return static_cast<float>(d[0]) + (static_cast<float>(d[1]) * 0.0078125f +
-                                                   static_cast<float>(d[2]) * 6.103515625e-05f);
-            };
+            auto digits = [](const i32x4 &d) { return digits_value(d); };
             float r;
             if constexpr (FMT == T_Q8_0) {
                 const i32x4 b0 = {static_cast<int>(src[0]), static_cast<int>(src[1]), static_cast<int>(src[2]),
