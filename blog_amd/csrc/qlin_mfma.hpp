@@ -102,9 +102,10 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 //   d1 = rint(t), d2 = rint(128 (t - d1)), d3 = rint(128 (128 (t - d1) - d2))
 // each in [-64, 64] (rint is the low byte of t + 1.5 * 2^23: round to nearest even, exact for
 // |t| < 2^22; every residual above is exact).  Gives the lane's 4 digits of each kind packed in a
-// dword, and the block's scale 2^e (NaN if any of its x is not finite) and sum of x.
+// dword, and the block's scale 2^e (NaN if any of its x is not finite), sum of x and the sum of
+// the lane's 16-element half.
 __device__ __forceinline__ void x_digits4(const float4 &v, uint32_t &p1, uint32_t &p2, uint32_t &p3, float &scale,
-                                          float &sum) {
+                                          float &sum, float &sum16) {
     constexpr float kMagic = 12582912.0f;
     const float xe[4] = {v.x, v.y, v.z, v.w};
     float mx = fmaxf(fmaxf(fabsf(xe[0]), fabsf(xe[1])), fmaxf(fabsf(xe[2]), fabsf(xe[3])));
@@ -114,6 +115,7 @@ __device__ __forceinline__ void x_digits4(const float4 &v, uint32_t &p1, uint32_
     mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
     sm += __shfl_xor(sm, 1, 64);
     sm += __shfl_xor(sm, 2, 64);
+    sum16 = sm;  // the sum of the lane's 16-element half of the block
     sm += __shfl_xor(sm, 4, 64);
     int ex;
     (void)frexpf(mx, &ex);

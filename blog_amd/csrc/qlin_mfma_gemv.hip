@@ -95,6 +95,9 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #ifndef QLIN_MFMA_I8
 #define QLIN_MFMA_I8 3
 #endif
+#ifndef QLIN_MFMA_I8_Q6K
+#define QLIN_MFMA_I8_Q6K 1
+#endif
 #ifndef QLIN_MFMA_FINAL_UNROLL
 #define QLIN_MFMA_FINAL_UNROLL 4  // batches the final per-row sum's LDS reads (same order of adds)
 #endif
@@ -170,13 +173,15 @@ struct Mats {
 // A lane's raw bytes of one step: Q4_K the 16-byte header and 32 bytes of nibbles; the 32-weight
 // formats 9 aligned dwords covering the lane's blocks.
 struct Raw {
-    uint32_t w[21];
+    uint32_t w[27];
 };
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
 
-// XR: float4 loads of x per thread (K/4 <= XR * kThreads).
-template <int FMT, bool SWIGLU, int XR>
+// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  WIDE (Q6_K): every super-block lies in
+// whole 16-byte units of its row (16-aligned rows of 8k super-blocks), so its ql and qh are read as
+// three aligned 16-byte pieces each.
+template <int FMT, bool SWIGLU, int XR, bool WIDE = false>
 __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const MfmaArgs a) {
     constexpr int kWaves = waves_for(SWIGLU), kThreads = threads_for(SWIGLU);
     constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     const int nsb = a.nsb, K = nsb * CE;
     // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
     // per 32 elements, in no more LDS than the bf16 layout takes (3K + K/4 against 4K + K/8 bytes)
-    constexpr bool I8 = (FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0) &&
+    constexpr bool I8 = (FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0 || (FMT == T_Q6_K && QLIN_MFMA_I8_Q6K)) &&
                         (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) || (QLIN_MFMA_I8 == 3 && XR <= 2));
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
     float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/XS] sum(hi + lo) per XS elements
@@ -235,7 +240,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // Q4_K sub-blocks 2g (MFMAs 0, 1) and 2g + 1 (2, 3), Q4_0 blocks 2g and 2g + 1 likewise (their 4
     // x 16 bytes are 64 consecutive plane bytes), Q8_0 block g (MFMAs 0, 1: 32 bytes)
     const bool i8_on = (n >> 2) == g && (n & 3) < 3;
-    const int8_t *a8 = planes + (n & 3) * K + (FMT == T_Q8_0 ? 32 : 64) * g;  // read only when i8_on
+    // (Q6_K: lane group g's low-nibble group starts (g >> 1) * 128 + (g & 1) * 32 into the chunk, its
+    // high-nibble group 64 further)
+    const int8_t *a8 = planes + (n & 3) * K +
+                       (FMT == T_Q8_0 ? 32 * g : FMT == T_Q6_K ? (g >> 1) * 128 + (g & 1) * 32 : 64 * g);  // when i8_on
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
     int a_lo_st, a_hi_st;
@@ -302,14 +310,35 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             // ql bytes [32g, 32g+32) and qh bytes [128+32h, +32) from the dwords at or 2 bytes before
             // them (rows are a multiple of 4 bytes, so odd super-blocks start 2 bytes in), then the
             // lane's 4 scales and d as 16-bit loads
-            const int h = g >> 1, sh = static_cast<int>(reinterpret_cast<uintptr_t>(q) & 3u);
+            // (wide rows: the 48 bytes from the 16-byte unit holding the first byte, w[0..11] and
+            // w[12..23], with the offset into that unit, 0..14)
+            const int h = g >> 1;
+            const int sh = static_cast<int>(reinterpret_cast<uintptr_t>(q) & (WIDE ? 15u : 3u));
+            if constexpr (WIDE) {
 #pragma unroll
-            for (int k = 0; k < 9; ++k) st.w[k] = ld4(q - sh + 32 * g + 4 * k);
+                for (int k = 0; k < 3; ++k) {
+                    const u32x4 l = ld16(q - sh + 32 * g + 16 * k), m = ld16(q - sh + 128 + 32 * h + 16 * k);
+                    st.w[4 * k] = l.x; st.w[4 * k + 1] = l.y; st.w[4 * k + 2] = l.z; st.w[4 * k + 3] = l.w;
+                    st.w[12 + 4 * k] = m.x; st.w[13 + 4 * k] = m.y; st.w[14 + 4 * k] = m.z; st.w[15 + 4 * k] = m.w;
+                }
+            } else {
 #pragma unroll
-            for (int k = 0; k < 9; ++k) st.w[9 + k] = ld4(q - sh + 128 + 32 * h + 4 * k);
-            st.w[18] = *reinterpret_cast<const uint16_t *>(q + 192 + 8 * h + 2 * (g & 1));
-            st.w[19] = *reinterpret_cast<const uint16_t *>(q + 196 + 8 * h + 2 * (g & 1));
-            st.w[20] = *reinterpret_cast<const uint16_t *>(q + 208) | (static_cast<uint32_t>(sh) << 16);
+                for (int k = 0; k < 9; ++k) st.w[k] = ld4(q - sh + 32 * g + 4 * k);
+#pragma unroll
+                for (int k = 0; k < 9; ++k) st.w[9 + k] = ld4(q - sh + 128 + 32 * h + 4 * k);
+            }
+            if constexpr (WIDE) {
+                // the 32 bytes from the 16-byte unit holding scale byte 0 (inside the row, as rows
+                // end on a unit boundary), 8 per lane group; the lanes gather theirs in process
+                const uint2 sv = *reinterpret_cast<const uint2 *>(q - sh + 192 + 8 * g);
+                st.w[24] = sv.x;
+                st.w[25] = sv.y;
+                st.w[26] = static_cast<uint32_t>(sh) << 16;
+            } else {
+                st.w[24] = *reinterpret_cast<const uint16_t *>(q + 192 + 8 * h + 2 * (g & 1));
+                st.w[25] = *reinterpret_cast<const uint16_t *>(q + 196 + 8 * h + 2 * (g & 1));
+                st.w[26] = *reinterpret_cast<const uint16_t *>(q + 208) | (static_cast<uint32_t>(sh) << 16);
+            }
         } else {
             // Q4_0: blocks 2g, 2g+1 = bytes [36g, 36g+36).  Q8_0: block g = bytes [34g, 34g+34), read
             // from the dword at or 2 bytes before it.
@@ -334,13 +363,19 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         for (int r = 0; r < XR; ++r) {
             const int i = tid + r * kThreads;
             uint32_t p1, p2, p3;
-            float sc, sm;
-            x_digits4(xv[r], p1, p2, p3, sc, sm);
+            float sc, sm, sm16;
+            x_digits4(xv[r], p1, p2, p3, sc, sm, sm16);
             if (i < K / 4) {
                 reinterpret_cast<uint32_t *>(planes)[i] = p1;
                 reinterpret_cast<uint32_t *>(planes + K)[i] = p2;
                 reinterpret_cast<uint32_t *>(planes + 2 * K)[i] = p3;
-                if ((i & 7) == 0) reinterpret_cast<float2 *>(sxp)[i >> 3] = make_float2(sc, sm);
+                if constexpr (FMT == T_Q6_K) {
+                    // scales per 32 [K/32], then x sums per 16 [K/16]
+                    if ((i & 7) == 0) sxp[i >> 3] = sc;
+                    if ((i & 3) == 0) sxp[K / 32 + (i >> 2)] = sm16;
+                } else {
+                    if ((i & 7) == 0) reinterpret_cast<float2 *>(sxp)[i >> 3] = make_float2(sc, sm);
+                }
             }
         }
     };
@@ -391,6 +426,69 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 
     u32x4 aop[8];
 
+    // Q6_K: dword t of this lane's ql and qh bytes (elements 4t..4t+3 of its low- and high-nibble
+    // groups): from the 36 bytes at or 2 before them, or (wide rows) from the 48-byte window, first
+    // shifting by whole dwords (offset bits 3 and 2, uniform per step), then by bytes
+    auto q6_words = [&](const Raw &cur, uint32_t (&ql)[8], uint32_t (&qh)[8]) {
+        const uint32_t off = cur.w[26] >> 16;
+        if constexpr (WIDE) {
+            // (the dword shifts as bit-field merges under an all-ones or all-zero mask the compiler
+            // cannot see through: as selects between neighbouring elements they would become an
+            // element chosen by a computed index, which keeps the arrays in scratch)
+            uint32_t m8 = 0u - ((off >> 3) & 1u), m4 = 0u - ((off >> 2) & 1u);
+            asm("" : "+v"(m8));
+            asm("" : "+v"(m4));
+            uint32_t c[10], e[10];
+#pragma unroll
+            for (int j = 0; j < 10; ++j) {
+                c[j] = (cur.w[j + 2] & m8) | (cur.w[j] & ~m8);
+                e[j] = (cur.w[14 + j] & m8) | (cur.w[12 + j] & ~m8);
+            }
+#pragma unroll
+            for (int j = 0; j < 9; ++j) {
+                c[j] = (c[j + 1] & m4) | (c[j] & ~m4);
+                e[j] = (e[j + 1] & m4) | (e[j] & ~m4);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                ql[t] = __builtin_amdgcn_alignbyte(c[t + 1], c[t], off & 3u);
+                qh[t] = __builtin_amdgcn_alignbyte(e[t + 1], e[t], off & 3u);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                ql[t] = __builtin_amdgcn_alignbyte(cur.w[t + 1], cur.w[t], off);
+                qh[t] = __builtin_amdgcn_alignbyte(cur.w[10 + t], cur.w[9 + t], off);
+            }
+        }
+    };
+    // Q6_K: this lane's four 16-element scales (sc[8h + 2(g & 1)], +1, +4, +5) and d.  Wide rows: the
+    // 8-byte pieces of the 32-byte window hold the scale pairs at window offsets o = off + 8h + 2(g & 1)
+    // and o + 4, d at off + 16; dword j of the window is in lane group j >> 1 (element j & 1)
+    auto q6_scales = [&](const Raw &cur, float &s0, float &s1, float &s2, float &s3, float &dd) {
+        uint32_t sa, sb, dw;
+        if constexpr (WIDE) {
+            const int off = static_cast<int>(cur.w[26] >> 16);
+            const int o = off + 8 * (g >> 1) + 2 * (g & 1), j = o >> 2;
+            const int la = 16 * (j >> 1) + n, lb = 16 * ((j + 1) >> 1) + n;
+            const uint32_t ax = __shfl(cur.w[24], la), ay = __shfl(cur.w[25], la);
+            const uint32_t bx = __shfl(cur.w[24], lb), by = __shfl(cur.w[25], lb);
+            sa = ((j & 1) ? ay : ax) >> (8 * (o & 3));
+            sb = ((j & 1) ? bx : by) >> (8 * (o & 3));
+            const int jd = (off + 16) >> 2;
+            dw = __shfl((jd & 1) ? cur.w[25] : cur.w[24], 16 * (jd >> 1) + n) >> (8 * (off & 3));
+        } else {
+            sa = cur.w[24];
+            sb = cur.w[25];
+            dw = cur.w[26];
+        }
+        s0 = static_cast<float>(static_cast<int8_t>(sa & 0xffu));
+        s1 = static_cast<float>(static_cast<int8_t>((sa >> 8) & 0xffu));
+        s2 = static_cast<float>(static_cast<int8_t>(sb & 0xffu));
+        s3 = static_cast<float>(static_cast<int8_t>((sb >> 8) & 0xffu));
+        dd = f16_bits_to_f32(dw & 0xffffu);
+    };
+
     // One step: the 16 rows' dots with super-block sb, parked in LDS (each (row, matrix, sb) slot is
     // written by exactly one step; a global store here would share vmcnt with the weight stream).
     auto process = [&](const Raw &cur, const Pos &p) {
@@ -401,8 +499,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             constexpr uint32_t M = 0x0f0f0f0fu;
             // the 8 dwords of this lane's stored integers: Q4_K the pair's 32 bytes; Q4_0 blocks 2g,
             // 2g + 1 (16 bytes each); Q8_0 block g's 32 bytes
-            uint32_t src[8];
-            if constexpr (FMT == T_Q4_K) {
+            uint32_t src[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+            if constexpr (FMT == T_Q6_K) {
+                // decoded below
+            } else if constexpr (FMT == T_Q4_K) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) src[k] = cur.w[4 + k];
             } else if constexpr (FMT == T_Q4_0) {
@@ -421,7 +521,43 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             };
             auto digits = [](const i32x4 &d) { return digits_value(d); };
             float r;
-            if constexpr (FMT == T_Q8_0) {
+            if constexpr (FMT == T_Q6_K) {
+                // 6-bit values u of the low-nibble group (elements 4t..4t+3 from ql/qh dword t) and of the
+                // high-nibble group; MFMA u carries one 16-element scale group: the low group's
+                // elements 0..15, 16..31, then the high group's
+                const int hs = 2 * (g & 1);
+                uint32_t lo[8], hi[8], wl[8], wh[8];
+                q6_words(cur, wl, wh);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    lo[t] = (wl[t] & 0x0f0f0f0fu) | (((wh[t] >> hs) & 0x03030303u) << 4);
+                    hi[t] = ((wl[t] >> 4) & 0x0f0f0f0fu) | (((wh[t] >> (hs + 4)) & 0x03030303u) << 4);
+                }
+                auto vec = [](const uint32_t *v) {
+                    return i32x4{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]),
+                                 static_cast<int>(v[3])};
+                };
+                const i32x4 *pq = reinterpret_cast<const i32x4 *>(
+                    i8_on ? a8 + p.sb * CE : reinterpret_cast<const int8_t *>(s_zero));
+                // A: the low group at +0, +16 bytes, the high group at +64, +80 (zero area: 64 bytes,
+                // so its lanes read it at +0, +16 twice)
+                const int hoff = i8_on ? 4 : 0;
+                const i32x4 d0 = mfma_i8(pq[0], vec(lo), i32x4{0, 0, 0, 0});
+                const i32x4 d1 = mfma_i8(pq[1], vec(lo + 4), i32x4{0, 0, 0, 0});
+                const i32x4 d2 = mfma_i8(pq[hoff], vec(hi), i32x4{0, 0, 0, 0});
+                const i32x4 d3 = mfma_i8(pq[hoff + 1], vec(hi + 4), i32x4{0, 0, 0, 0});
+                const int blo = p.sb * 8 + (g >> 1) * 4 + (g & 1), bhi = blo + 2;  // 32-element blocks
+                const float scl = sxp[blo], sch = sxp[bhi];
+                const float *x16 = sxp + K / 32;
+                float s0, s1, s2, s3, dd;
+                q6_scales(cur, s0, s1, s2, s3, dd);
+                // u - 32: the offset leaves with the 16-element x sums
+                r = s0 * (scl * digits(d0) - 32.0f * x16[2 * blo]);
+                r = fmaf(s1, scl * digits(d1) - 32.0f * x16[2 * blo + 1], r);
+                r = fmaf(s2, sch * digits(d2) - 32.0f * x16[2 * bhi], r);
+                r = fmaf(s3, sch * digits(d3) - 32.0f * x16[2 * bhi + 1], r);
+                r *= dd;
+            } else if constexpr (FMT == T_Q8_0) {
                 const i32x4 b0 = {static_cast<int>(src[0]), static_cast<int>(src[1]), static_cast<int>(src[2]),
                                   static_cast<int>(src[3])};
                 const i32x4 b1 = {static_cast<int>(src[4]), static_cast<int>(src[5]), static_cast<int>(src[6]),
@@ -517,12 +653,12 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
         f32x4 d2 = {0.0f, 0.0f, 0.0f, 0.0f};  // Q6_K: elements 16..31 of each group
         if constexpr (FMT == T_Q6_K) {
-            const uint32_t sh = 8 * (cur.w[20] >> 16);
             const int hs = 2 * (g & 1);  // qh bit pair of the low-nibble group; +4 for the high one
+            uint32_t wl[8], wh[8];
+            q6_words(cur, wl, wh);
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const uint32_t ql = __builtin_amdgcn_alignbyte(cur.w[t + 1], cur.w[t], sh >> 3);
-                const uint32_t qh = __builtin_amdgcn_alignbyte(cur.w[10 + t], cur.w[9 + t], sh >> 3);
+                const uint32_t ql = wl[t], qh = wh[t];
                 const uint32_t lo = (ql & 0x0f0f0f0fu) | (((qh >> hs) & 0x03030303u) << 4);
                 const uint32_t hi = ((ql >> 4) & 0x0f0f0f0fu) | (((qh >> (hs + 4)) & 0x03030303u) << 4);
                 if (t < 4) d = mfma(aop[t], weights_operand2(lo, hi), d);
@@ -553,11 +689,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             // groups of this lane: low nibbles (half h, group p), high nibbles (h, p + 2); x sums per 16
             const int gl = 8 * (g >> 1) + 2 * (g & 1), gh = gl + 4;  // 16-element unit index in the chunk
             const float *xs = xsum + p.sb * 16;
-            const float dd = f16_bits_to_f32(cur.w[20] & 0xffffu);
-            const float s0 = static_cast<float>(static_cast<int8_t>(cur.w[18] & 0xffu));
-            const float s1 = static_cast<float>(static_cast<int8_t>((cur.w[18] >> 8) & 0xffu));
-            const float s2 = static_cast<float>(static_cast<int8_t>(cur.w[19] & 0xffu));
-            const float s3 = static_cast<float>(static_cast<int8_t>((cur.w[19] >> 8) & 0xffu));
+            float s0, s1, s2, s3, dd;
+            q6_scales(cur, s0, s1, s2, s3, dd);
             r = s0 * ((d[0] + d[1]) - 160.0f * xs[gl]);
             r = fmaf(s1, (d2[0] + d2[1]) - 160.0f * xs[gl + 1], r);
             r = fmaf(s2, (d[2] + d[3]) - 160.0f * xs[gh], r);
@@ -681,26 +814,27 @@ Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int FMT, bool SWIGLU, int XR>
+template <int FMT, bool SWIGLU, int XR, bool WIDE>
 void launch_xr(const Plan &p, const MfmaArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((mfma_gemv_kernel<FMT, SWIGLU, XR>), dim3(p.grid), dim3(threads_for(SWIGLU)), p.lds, s, a);
+    hipLaunchKernelGGL((mfma_gemv_kernel<FMT, SWIGLU, XR, WIDE>), dim3(p.grid), dim3(threads_for(SWIGLU)), p.lds, s,
+                       a);
 }
 
-template <int FMT, bool SWIGLU>
+template <int FMT, bool SWIGLU, bool WIDE>
 void launch_sw(const Plan &p, const MfmaArgs &a, int k, hipStream_t s) {
     constexpr int kThreads = threads_for(SWIGLU);
     const int need = (k / 4 + kThreads - 1) / kThreads;  // float4 loads of x per thread
-    if (need <= 1) launch_xr<FMT, SWIGLU, 1>(p, a, s);
-    else if (need <= 2) launch_xr<FMT, SWIGLU, 2>(p, a, s);
-    else if (need <= 4) launch_xr<FMT, SWIGLU, 4>(p, a, s);
-    else if (need <= 6) launch_xr<FMT, SWIGLU, 6>(p, a, s);
-    else launch_xr<FMT, SWIGLU, kMaxXr>(p, a, s);
+    if (need <= 1) launch_xr<FMT, SWIGLU, 1, WIDE>(p, a, s);
+    else if (need <= 2) launch_xr<FMT, SWIGLU, 2, WIDE>(p, a, s);
+    else if (need <= 4) launch_xr<FMT, SWIGLU, 4, WIDE>(p, a, s);
+    else if (need <= 6) launch_xr<FMT, SWIGLU, 6, WIDE>(p, a, s);
+    else launch_xr<FMT, SWIGLU, kMaxXr, WIDE>(p, a, s);
 }
 
-template <int FMT>
+template <int FMT, bool WIDE = false>
 void launch_fmt(const Plan &p, const MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
-    if (swiglu) launch_sw<FMT, true>(p, a, k, s);
-    else launch_sw<FMT, false>(p, a, k, s);
+    if (swiglu) launch_sw<FMT, true, WIDE>(p, a, k, s);
+    else launch_sw<FMT, false, WIDE>(p, a, k, s);
 }
 
 int chunk_elems(int type) { return type == T_Q8_0 ? Chunk<T_Q8_0>::elems : Chunk<T_Q4_K>::elems; }
@@ -713,11 +847,16 @@ hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
     a.rows_q = units / p.grid;
     a.rows_r = units % p.grid;
     a.nsb_magic = a.nsb > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + a.nsb - 1) / a.nsb) : 0u;
+    bool q6_wide = type == T_Q6_K && a.row_bytes % 16 == 0;
+    for (int i = 0; i < (swiglu ? 2 : a.nmat); ++i) q6_wide = q6_wide && aligned16(a.w[i]);
     switch (type) {
         case T_Q4_K: launch_fmt<T_Q4_K>(p, a, k, swiglu, s); break;
         case T_Q4_0: launch_fmt<T_Q4_0>(p, a, k, swiglu, s); break;
         case T_Q8_0: launch_fmt<T_Q8_0>(p, a, k, swiglu, s); break;
-        case T_Q6_K: launch_fmt<T_Q6_K>(p, a, k, swiglu, s); break;
+        case T_Q6_K:
+            if (q6_wide) launch_fmt<T_Q6_K, true>(p, a, k, swiglu, s);
+            else launch_fmt<T_Q6_K>(p, a, k, swiglu, s);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

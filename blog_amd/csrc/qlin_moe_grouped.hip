@@ -467,8 +467,8 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                     const int route = a.list[beg + q0 + q];
                     const float4 v = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(route / a.x_div) * K)[c];
                     uint32_t p1, p2, p3;
-                    float sc, sm;
-                    x_digits4(v, p1, p2, p3, sc, sm);
+                    float sc, sm, sm16;
+                    x_digits4(v, p1, p2, p3, sc, sm, sm16);
                     uint32_t *pq = reinterpret_cast<uint32_t *>(planes + static_cast<size_t>(q) * 3 * K);
                     pq[c] = p1;
                     pq[K / 4 + c] = p2;

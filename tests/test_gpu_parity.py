@@ -136,6 +136,22 @@ def test_gemv_generic_path_agrees(qtype, out_dim, in_dim):
     assert normwise_rel_err(y_gen, ref) <= FP32
 
 
+@pytest.mark.parametrize("out_dim,in_dim", [(300, 2048), (70, 4096)])
+def test_q6k_rows_of_16_byte_units_and_offset_base(out_dim, in_dim):
+    """Q6_K rows of 8k super-blocks are whole 16-byte units: from a 16-byte aligned base the
+    super-blocks are read as aligned 16-byte pieces (their offsets into a unit cycle through 0..14),
+    from a base 4 bytes further as dwords.  Both agree with the oracle."""
+    w, rb, vals = qgen.random_matrix(Q6_K, out_dim, in_dim, seed=out_dim + 3 * in_dim)
+    assert rb % 16 == 0
+    x = qgen.random_x(1, in_dim, seed=in_dim + 5)
+    banner(f"gemv q6_k units N={out_dim} K={in_dim}")
+    ref = orc.matmul_f64(Q6_K, w, rb, x, out_dim, in_dim)
+    for off in (0, 4):
+        y = gpu_gemv(Q6_K, w, rb, x, out_dim, in_dim, w_offset=off)
+        assert normwise_rel_err(y, ref) <= GATE
+        assert cond_err(y, ref, vals, x) <= COND
+
+
 @pytest.mark.parametrize("qtype,m", [(Q4_K, 2), (Q4_K, 5), (Q8_0, 3), (Q4_0, 9)])
 def test_gemv_several_rows(qtype, m):
     in_dim = 1024
@@ -589,9 +605,10 @@ def test_swiglu_stream(ffn, hid):
 
 
 @pytest.mark.parametrize("qtype,ffn,hid", [(Q4_0, 18944, 3584), (Q8_0, 4864, 896 + 128), (Q8_0, 4864, 896),
-                                          (Q4_0, 9, 256)])
+                                          (Q4_0, 9, 256), (Q6_K, 300, 2048), (Q6_K, 17, 768)])
 def test_swiglu_matrix_core_formats(qtype, ffn, hid):
-    """Fused gate/up SiLU on the 32-weight formats (C2's gate/up pair in one launch)."""
+    """Fused gate/up SiLU on the 32-weight formats (C2's gate/up pair in one launch) and on Q6_K
+    (rows of whole 16-byte units at hid = 2048, of dwords at 768)."""
     wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=410 + hid)
     wu, _, _ = qgen.random_matrix(qtype, ffn, hid, seed=411 + hid)
     x = qgen.random_x(1, hid, seed=412)[0]
@@ -615,7 +632,7 @@ def test_gemv_multi_c3_qkv():
 
 
 @pytest.mark.parametrize("qtype,in_dim", [(Q4_K, 256), (Q4_K, 768), (Q4_0, 256), (Q4_0, 512), (Q8_0, 128),
-                                          (Q8_0, 384), (Q6_K, 256)])
+                                          (Q8_0, 384), (Q6_K, 256), (Q6_K, 2048)])
 def test_gemv_multi_four_ragged(qtype, in_dim):
     """Four matrices of ragged row counts (1, 17, 33, 300) in one launch: the per-row matrix lookup,
     row slices that end mid-tile, and a single chunk per row at the smallest in_dim."""
