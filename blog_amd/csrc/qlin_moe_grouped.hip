@@ -275,9 +275,11 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
         a_hi = on_hi ? xb : zb;
     }
     const ScaleDecoder dec(g);
-    // others: lane-group g's block starts bb*g bytes into the chunk; its payload (after d) is read
-    // from the dword at or 2 bytes before it
-    const int pl_dw = (F::bb * g + 2) >> 2, pl_sh = (F::bb * g + 2) & 3;
+    // others: lane-group g's block starts bb*g bytes into the chunk (bb = 2 mod 4), and nd + 1 dwords
+    // from the one holding d cover the block: d in its low half for even g (payload 2 bytes in), its
+    // high half for odd g (payload in the next dwords), so no 16-bit load is needed
+    const int d_dw = (F::bb * g) >> 2;
+    const bool d_hi = g & 1;
 
     struct Raw {
         uint32_t w[12];
@@ -331,12 +333,9 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 st.w[4] = qa.x; st.w[5] = qa.y; st.w[6] = qa.z; st.w[7] = qa.w;
                 st.w[8] = qb.x; st.w[9] = qb.y; st.w[10] = qb.z; st.w[11] = qb.w;
             } else {
-                // d as a 16-bit load; nd + 1 dwords of payload, the last clamped into the chunk
-                // (with a shift of 0 it is not used)
-                st.w[0] = ld_u16(q + F::bb * g);
+                // nd + 1 dwords from the one holding d (d_dw + nd is at most the chunk's last dword)
 #pragma unroll
-                for (int k = 0; k <= F::nd; ++k)
-                    st.w[1 + k] = *reinterpret_cast<const uint32_t *>(q + 4 * min(pl_dw + k, F::cb / 4 - 1));
+                for (int k = 0; k <= F::nd; ++k) st.w[1 + k] = *reinterpret_cast<const uint32_t *>(q + 4 * (d_dw + k));
             }
         };
 
@@ -415,8 +414,9 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             } else {
                 uint32_t C[F::nd];
 #pragma unroll
-                for (int k = 0; k < F::nd; ++k) C[k] = __builtin_amdgcn_alignbyte(cur.w[2 + k], cur.w[1 + k], pl_sh);
-                const float d = f16_bits_to_f32(cur.w[0]);
+                for (int k = 0; k < F::nd; ++k)
+                    C[k] = d_hi ? cur.w[2 + k] : __builtin_amdgcn_alignbyte(cur.w[2 + k], cur.w[1 + k], 2);
+                const float d = f16_bits_to_f32(d_hi ? cur.w[1] >> 16 : cur.w[1] & 0xffffu);
                 u32x4 B[F::tpb];
 #pragma unroll
                 for (int t = 0; t < F::tpb; ++t) {

@@ -136,18 +136,20 @@ def test_gemv_generic_path_agrees(qtype, out_dim, in_dim):
     assert normwise_rel_err(y_gen, ref) <= FP32
 
 
-@pytest.mark.parametrize("out_dim,in_dim", [(300, 2048), (70, 4096)])
-def test_q6k_rows_of_16_byte_units_and_offset_base(out_dim, in_dim):
-    """Q6_K rows of 8k super-blocks are whole 16-byte units: from a 16-byte aligned base the
-    super-blocks are read as aligned 16-byte pieces (their offsets into a unit cycle through 0..14),
-    from a base 4 bytes further as dwords.  Both agree with the oracle."""
-    w, rb, vals = qgen.random_matrix(Q6_K, out_dim, in_dim, seed=out_dim + 3 * in_dim)
+@pytest.mark.parametrize("qtype,out_dim,in_dim", [(Q6_K, 300, 2048), (Q6_K, 70, 4096), (Q4_0, 300, 3584),
+                                                  (Q4_0, 33, 256), (Q8_0, 300, 4096), (Q8_0, 77, 1024)])
+def test_rows_of_16_byte_units_and_offset_base(qtype, out_dim, in_dim):
+    """Rows that are whole 16-byte units (Q4_0 always, Q8_0 with an even number of 128-weight chunks,
+    Q6_K of 8k super-blocks), from a 16-byte aligned base and from one 4 bytes further.  Q6_K reads
+    aligned 16-byte pieces from the first (the offsets of its super-blocks into a unit cycle through
+    0..14) and dwords from the second.  Both agree with the oracle."""
+    w, rb, vals = qgen.random_matrix(qtype, out_dim, in_dim, seed=out_dim + 3 * in_dim + qtype)
     assert rb % 16 == 0
     x = qgen.random_x(1, in_dim, seed=in_dim + 5)
-    banner(f"gemv q6_k units N={out_dim} K={in_dim}")
-    ref = orc.matmul_f64(Q6_K, w, rb, x, out_dim, in_dim)
+    banner(f"gemv 16-byte units type={qtype} N={out_dim} K={in_dim}")
+    ref = orc.matmul_f64(qtype, w, rb, x, out_dim, in_dim)
     for off in (0, 4):
-        y = gpu_gemv(Q6_K, w, rb, x, out_dim, in_dim, w_offset=off)
+        y = gpu_gemv(qtype, w, rb, x, out_dim, in_dim, w_offset=off)
         assert normwise_rel_err(y, ref) <= GATE
         assert cond_err(y, ref, vals, x) <= COND
 
