@@ -165,7 +165,7 @@ def main() -> int:
                    "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "mfma_gemv_kernel<12, true, 1> (Q4_K gate/up SwiGLU, 2 x [18944, 3584])",
+                     "kernel": "mfma_gemv_kernel<12, true, 1, false> (Q4_K gate/up SwiGLU, 2 x [18944, 3584])",
                      "avg_launch_us": round(launch_us, 3),
                      "algorithmic_bytes_per_launch": gate_bytes},
     }
@@ -338,7 +338,7 @@ def gemv_config(args, torch, qlin, gen, workload, metric, qtype, shapes, copies)
                    "batch": 1, "algorithmic_bytes_per_step": step_bytes, "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(b0 / us0 / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(b0 / us0 / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": f"mfma_gemv_kernel<{qtype}, false, *> ({shapes[0][0]} [{n0}, {k0}])",
+                     "kernel": f"mfma_gemv_kernel<{qtype}, false, *, *> ({shapes[0][0]} [{n0}, {k0}])",
                      "avg_launch_us": round(us0, 3), "algorithmic_bytes_per_launch": b0},
     }
     if not args.no_cpu:
@@ -423,7 +423,7 @@ def wl_c3(args, torch, qlin, gen):
                    "prompt_32_plus_128_tokens_ms": round((us_pre + 128 * us) / 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "mfma_gemv_kernel<8, true, *> (Q8_0 gate/up SwiGLU, 2 x [4864, 896])",
+                     "kernel": "mfma_gemv_kernel<8, true, *, *> (Q8_0 gate/up SwiGLU, 2 x [4864, 896])",
                      "avg_launch_us": round(us_sw, 3), "algorithmic_bytes_per_launch": sw_bytes},
     }
     if not args.no_cpu:
