@@ -559,8 +559,78 @@ def wl_c5(args, torch, qlin, gen):
     }
 
 
+def wl_moe_token(args, torch, qlin, gen):
+    """The engine's per-token routed MoE (TensorTool::moe_routed_decode_indexed, TensorTool.cpp:271-336)
+    at DeepSeek-V2-Lite's shape: one decode token's router (top-6 of 64), then
+    qlin_moe_routed_decode_indexed -- the 6 routes' Q4_K gate/up SwiGLU [1408, 2048] and their Q5_0 down
+    [2048, 1408] added in route order.  A step is one token; 4 copies of the 64 experts (4 x 334 MB)
+    rotate, each with its own router logits."""
+    E, ffn, hid, k = 64, 1408, 2048, 6
+    Q5_0 = 6
+    copies = 4
+    mats = [(synth_blocks(torch, Q4_K, E * ffn, hid, gen), synth_blocks(torch, Q4_K, E * ffn, hid, gen),
+             synth_blocks(torch, Q5_0, E * hid, ffn, gen)) for _ in range(copies)]
+    x = torch.randn(hid, device="cuda", generator=gen)
+    logits = torch.randn(copies, E, device="cuda", generator=gen)
+    ids = torch.empty(copies, k, dtype=torch.int32, device="cuda")
+    rw = torch.empty(copies, k, device="cuda")
+    act = torch.empty(k, ffn, device="cuda")
+    out = torch.zeros(hid, device="cuda")
+    gub, db = mats[0][0].numel(), mats[0][2].numel()
+    g_rb, d_rb = qlin.row_bytes(Q4_K, hid), qlin.row_bytes(Q5_0, ffn)
+
+    def route():
+        for c in range(copies):
+            qlin.call("qlin_launch_moe_router_topk", logits[c], ids[c], rw[c], 1, E, k, 1.0)
+
+    def step():
+        for c, (wg, wu, wd) in enumerate(mats):
+            qlin.call("qlin_launch_moe_router_topk", logits[c], ids[c], rw[c], 1, E, k, 1.0)
+            qlin.call("qlin_moe_routed_decode_indexed", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, x,
+                      ids[c], rw[c], act, out, k)
+
+    def swiglu_only():
+        for c, (wg, wu, _) in enumerate(mats):
+            qlin.call("qlin_launch_quant_swiglu_indexed", Q4_K, wg, wu, gub // E, gub // E, g_rb, g_rb, x, ids[c],
+                      act, k, ffn, hid)
+
+    def down_only():
+        for c, (_, _, wd) in enumerate(mats):
+            qlin.call("qlin_launch_quant_down_f32_indexed_accum_ordered", Q5_0, wd, db // E, d_rb, act, ids[c], rw[c],
+                      out, k, hid, ffn)
+
+    reps = max(1, args.steps // 4)
+    us = graph_us(torch, qlin, step, reps) / copies
+    route()
+    torch.cuda.synchronize()
+    us_sw = graph_us(torch, qlin, swiglu_only, reps) / copies
+    us_dn = graph_us(torch, qlin, down_only, reps) / copies
+    distinct = min(int(torch.unique(ids[c][ids[c] >= 0]).numel()) for c in range(copies))
+    sw_bytes = k * 2 * ffn * g_rb + 4 * hid + 4 * k * ffn
+    dn_bytes = k * hid * d_rb + 4 * k * ffn + 8 * hid
+    nbytes = sw_bytes + dn_bytes + 4 * E
+    log(f"moe token: {us:.2f} us/token (router + routed decode), SwiGLU {us_sw:.2f} us, down {us_dn:.2f} us, "
+        f"{distinct} distinct experts per token at least")
+    return {
+        "metric": "per-token routed MoE decode HBM GB/s (DeepSeek-V2-Lite shape, top-6 of 64, 1 token)",
+        "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
+        "n_gpus": 1, "steps": reps * copies, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random Q4_K / Q5_0 expert blocks, f32 N(0,1) x and router logits), 4 weight copies",
+        "config": {"workload": "deepseek-moe-token", "experts": E, "ffn": ffn, "hidden": hid, "top_k": k,
+                   "gate_up": "Q4_K", "down": "Q5_0", "algorithmic_bytes_per_step": nbytes,
+                   "launches_per_step": "router_topk + moe_routed_decode_indexed (routed SwiGLU, routed down)",
+                   "swiglu_us": round(us_sw, 3), "down_us": round(us_dn, 3), "execution": "hip graph replay"},
+        "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "mfma_gemv_kernel<12, true, 1, false, true> (routed gate/up SwiGLU, 6 x 2 x [1408, 2048])",
+                     "avg_launch_us": round(us_sw, 3), "algorithmic_bytes_per_launch": sw_bytes},
+    }
+
+
 WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
-             "c3-q8_0-decode-token": wl_c3, "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k}
+             "c3-q8_0-decode-token": wl_c3, "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k,
+             "deepseek-moe-token": wl_moe_token}
 
 
 def cpu_baseline(torch, layer, shapes, xin, outs, seconds, bytes_per_step):

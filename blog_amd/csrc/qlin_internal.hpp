@@ -31,13 +31,25 @@ hipError_t q4k_stream_gemv(const uint8_t *const *w, float *const *y, const int *
 hipError_t q4k_stream_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
                              int ffn_dim, int in_dim, hipStream_t s);
 
-// Matrix-core decode kernels (m == 1) for Q4_K, Q4_0 and Q8_0, same contracts as the streaming ones.
+// Matrix-core decode kernels (m == 1) for Q4_K, Q4_0, Q8_0, Q5_0 and Q6_K, same contracts as the streaming ones.
 bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
              bool swiglu);
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat,
                      size_t row_bytes, const float *x, int in_dim, bool add, hipStream_t s);
 hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
                        int ffn_dim, int in_dim, hipStream_t s);
+// The routed-expert forms (qlin_mfma_gemv.hip): route r's weights are expert ids[r]'s (negative: none).
+// SwiGLU: act[r, o] = silu(Wg[e_r] x) (Wu[e_r] x), 0 for no expert.  Down: out[h] += the routes' dots
+// Wd[e_r][h] . act[r] added in route order as fmaf(dot, rw[r], total).  mfma_routed_ok takes the
+// SwiGLU's (rows = ffn, k = in_dim) or the down projection's (rows = hidden, k = ffn) shape.
+bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1, size_t expert_bytes,
+                    size_t row_bytes, const float *x, int routes, int rows, int k);
+hipError_t mfma_swiglu_routed(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
+                              const float *x, const int *ids, float *act, int routes, int ffn_dim, int in_dim,
+                              hipStream_t s);
+hipError_t mfma_down_routed(int type, const uint8_t *wd, size_t expert_bytes, size_t row_bytes, const float *act,
+                            const int *ids, const float *rw, float *out, int routes, int hidden, int ffn_dim,
+                            hipStream_t s);
 
 // Q4_K over m > 1 rows of f32 activations on the f32 matrix cores (qlin_dense.hip): mode 0 stores
 // y[r, o], 1 adds into it, 2 writes act[r, o] = silu(gate . x_r) * (up . x_r) with w1 the up matrix.

@@ -53,6 +53,10 @@ struct ScaleDecoder {
 
 __device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
+// bits 0..3 of b to bit 0 of bytes 0..3 (the four shifted copies of b do not overlap): the fifth
+// bits of four Q5_0 elements, ready to join their nibbles
+__device__ __forceinline__ uint32_t spread4(uint32_t b) { return __umul24(b & 0xfu, 0x204081u) & 0x01010101u; }
+
 // B operand of MFMA t from qs dword v: bf16(128 + q) for the 4 low nibbles, then the 4 high ones.
 // bf16 128 + q has bytes (q, 0x43); v_perm_b32 interleaves the nibble bytes with 0x43 bytes taken
 // from a constant register.

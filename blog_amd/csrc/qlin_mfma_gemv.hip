@@ -49,8 +49,16 @@
 //     (g/2, g%2+2), whose top 2 bits come from the matching qh bytes; u = 6-bit value is carried
 //     as bf16(128 + u).  Scales change every 16 elements, so MFMAs 0-3 and 4-7 accumulate
 //     separately and the x sums are kept per 16; y += d sum sc (D - 160 X16).
+//   Q5_0 (chunk = 4 blocks of 22 B, kernel.cu:1159-1175; int8 matrix cores only): lane group g
+//     decodes block g, q = nibble | (bit e of qh) << 4 as the int8 B operand; y += d (D - 16 X).
 //   Their blocks are only 2-byte aligned, so each lane loads aligned dwords and realigns them
 //     with v_alignbyte_b32.
+//
+// Routed experts (the per-token MoE, TensorTool.cpp:271-336 with kernel.cu:1340-1385, 2253-2287):
+// route r's weights are expert ids[r]'s.  The gate/up SwiGLU of k routes is the SwiGLU over k * ffn
+// concatenated rows whose row pointers come from the ids; the down projection of k routes is one
+// GEMV over the routes' activations laid end to end (chunk c of a row belongs to route c / cpr),
+// and each row adds its route dots in route order, fmaf(dot_r, w_r, total), as the reference does.
 //
 // Work decomposition.  One workgroup per CU; workgroup b of G owns the 16-row tiles b, b + G, ...,
 // so that the workgroups sweep one region of the weights together.  Its work is the flat sequence
@@ -83,6 +91,11 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 // over the decode step than 1: more outstanding requests per CU serve worse on this memory system.
 #define QLIN_MFMA_DEPTH 1
 #endif
+// The same for the routed launches: 2 measured slower there too (per-token MoE at DeepSeek-V2-Lite's
+// shape: SwiGLU 9.8 -> 11.0 us, down 11.9 -> 12.2 us).
+#ifndef QLIN_MFMA_ROUTED_DEPTH
+#define QLIN_MFMA_ROUTED_DEPTH 1
+#endif
 // Workgroup b of G takes 16-row tiles b, b + G, b + 2G, ... (1), so that all workgroups sweep one
 // region of the weights together, rather than a contiguous slice each (0): 1.6% faster over the
 // decode step (gate/up and lm_head, the launches with several tiles per workgroup).
@@ -105,7 +118,6 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #define QLIN_MFMA_MATMAJOR 1  // SwiGLU steps: 1 = all gate tiles, then all up tiles; 0 = tile-major
 #endif
 constexpr size_t kMaxLds = 160 * 1024;
-constexpr size_t kStaticLds = 256;      // the kernel's own __shared__ variables (claim counter, zeros)
 constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * threads
 
 // Weights per step chunk of one row, and its bytes.
@@ -113,6 +125,7 @@ template <int FMT> struct Chunk;
 template <> struct Chunk<T_Q4_K> { static constexpr int elems = 256, bytes = 144; };
 template <> struct Chunk<T_Q4_0> { static constexpr int elems = 256, bytes = 144; };
 template <> struct Chunk<T_Q8_0> { static constexpr int elems = 128, bytes = 136; };
+template <> struct Chunk<T_Q5_0> { static constexpr int elems = 128, bytes = 88; };
 template <> struct Chunk<T_Q6_K> { static constexpr int elems = 256, bytes = 210; };
 // Elements per x sum kept in LDS.
 template <int FMT> constexpr int kSumElems = FMT == T_Q6_K ? 16 : 32;
@@ -135,7 +148,18 @@ struct MfmaArgs {
     // wave, and the 16 waves of a CU share that unit).
     int rows_q, rows_r;
     uint32_t nsb_magic;
+    // Routed launches: route r's weights start at w[.] + ids[r] * eb (a negative id: no expert, its
+    // loads read expert 0 and its results are dropped).  SwiGLU: route r owns concatenated rows
+    // [r * route_rows, (r + 1) * route_rows); otherwise chunks [r * cpr, (r + 1) * cpr) of every row,
+    // weighted by rw[r].  The magics are ceil(2^32 / divisor), exact as nsb_magic (0: divisor 1).
+    const int *ids;
+    const float *rw;
+    size_t eb;
+    int routes, route_rows, cpr;
+    uint32_t route_magic, cpr_magic;
 };
+
+constexpr int kMaxRoutes = 16;  // routes of one routed launch (top-k of one token)
 
 // The argument arrays, copied into registers once: indexing the kernel-argument struct with a
 // per-lane value would compile to vector loads of the argument segment, whose completion shares the
@@ -180,8 +204,8 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_
 
 // XR: float4 loads of x per thread (K/4 <= XR * kThreads).  WIDE (Q6_K): every super-block lies in
 // whole 16-byte units of its row (16-aligned rows of 8k super-blocks), so its ql and qh are read as
-// three aligned 16-byte pieces each.
-template <int FMT, bool SWIGLU, int XR, bool WIDE = false>
+// three aligned 16-byte pieces each.  ROUTED: the routed-expert forms (a.ids).
+template <int FMT, bool SWIGLU, int XR, bool WIDE = false, bool ROUTED = false>
 __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const MfmaArgs a) {
     constexpr int kWaves = waves_for(SWIGLU), kThreads = threads_for(SWIGLU);
     constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
@@ -190,9 +214,12 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     constexpr int XS = kSumElems<FMT>;
     const int nsb = a.nsb, K = nsb * CE;
     // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
-    // per 32 elements, in no more LDS than the bf16 layout takes (3K + K/4 against 4K + K/8 bytes)
-    constexpr bool I8 = (FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0 || (FMT == T_Q6_K && QLIN_MFMA_I8_Q6K)) &&
-                        (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) || (QLIN_MFMA_I8 == 3 && XR <= 2));
+    // per 32 elements, in no more LDS than the bf16 layout takes (3K + K/4 against 4K + K/8 bytes).
+    // Q5_0 has only this form.
+    constexpr bool I8 = FMT == T_Q5_0 ||
+                        ((FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0 || (FMT == T_Q6_K && QLIN_MFMA_I8_Q6K)) &&
+                         (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) || (QLIN_MFMA_I8 == 3 && XR <= 2)));
+    constexpr bool K32 = FMT == T_Q8_0 || FMT == T_Q5_0;  // 128-weight chunks: lane group g, block g
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
     float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/XS] sum(hi + lo) per XS elements
     float *partial = xsum + K / XS;                                // [rows][NW][nsb]
@@ -243,7 +270,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // (Q6_K: lane group g's low-nibble group starts (g >> 1) * 128 + (g & 1) * 32 into the chunk, its
     // high-nibble group 64 further)
     const int8_t *a8 = planes + (n & 3) * K +
-                       (FMT == T_Q8_0 ? 32 * g : FMT == T_Q6_K ? (g >> 1) * 128 + (g & 1) * 32 : 64 * g);  // when i8_on
+                       (K32 ? 32 * g : FMT == T_Q6_K ? (g >> 1) * 128 + (g & 1) * 32 : 64 * g);  // when i8_on
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
     int a_lo_st, a_hi_st;
@@ -262,8 +289,17 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // A step: tw = tile * NW + matrix, sb = super-block; s = its index in the flat sequence.
     struct Pos {
         int s, tw, sb;
-        const uint8_t *rp;  // this lane's weight row
+        const uint8_t *rp;  // this lane's bytes of the step's chunk
     };
+    // Routed launches: the routes' experts (and down weights), read before the first weight load
+    __shared__ int s_ids[ROUTED ? kMaxRoutes : 1];
+    __shared__ float s_rw[ROUTED ? kMaxRoutes : 1];
+    // route of a concatenated SwiGLU row / of a down chunk
+    auto route_of = [&](int v, int d, uint32_t magic) {
+        return d == 1 ? v : static_cast<int>(__umulhi(static_cast<uint32_t>(v), magic));
+    };
+    // expert e's weights (a negative id reads expert 0, whose results are dropped)
+    auto expert = [&](const uint8_t *w, int r) { return w + static_cast<size_t>(max(s_ids[r], 0)) * a.eb; };
     const int ntiles = (nrows + 15) / 16;
     auto split_tw = [&](int tw, int &tile, int &which) {
         if constexpr (NW == 1) {
@@ -288,19 +324,31 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         int tile, which;
         split_tw(p.tw, tile, which);
         const int gr = grow(min(tile * 16 + n, nrows - 1));
-        if constexpr (SWIGLU) {
-            p.rp = (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes;
+        if constexpr (ROUTED && SWIGLU) {
+            // route of this lane's concatenated row (the 16 rows of a tile may span two routes)
+            const int r = route_of(gr, a.route_rows, a.route_magic);
+            const int row = gr - r * a.route_rows;
+            p.rp = expert(which ? mats.w[1] : mats.w[0], r) + static_cast<size_t>(row) * a.row_bytes +
+                   static_cast<size_t>(p.sb) * CB;
+        } else if constexpr (ROUTED) {
+            // chunk sb of the concatenated activations is chunk cl of route r (wave-uniform)
+            const int r = route_of(p.sb, a.cpr, a.cpr_magic);
+            const int cl = p.sb - r * a.cpr;
+            p.rp = expert(mats.w[0], r) + static_cast<size_t>(gr) * a.row_bytes + static_cast<size_t>(cl) * CB;
+        } else if constexpr (SWIGLU) {
+            p.rp = (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes +
+                   static_cast<size_t>(p.sb) * CB;
         } else {
             const uint8_t *wp;
             float *yp;
             int local;
             mats.locate(gr, wp, yp, local);
-            p.rp = wp + static_cast<size_t>(local) * a.row_bytes;
+            p.rp = wp + static_cast<size_t>(local) * a.row_bytes + static_cast<size_t>(p.sb) * CB;
         }
         return p;
     };
     auto load = [&](Raw &st, const Pos &p) {
-        const uint8_t *q = p.rp + static_cast<size_t>(p.sb) * CB;
+        const uint8_t *q = p.rp;
         if constexpr (FMT == T_Q4_K) {
             const u32x4 h = ld16(q), qa = ld16(q + 16 + 32 * g), qb = ld16(q + 32 + 32 * g);
             st.w[0] = h.x; st.w[1] = h.y; st.w[2] = h.z; st.w[3] = h.w;
@@ -339,6 +387,12 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
                 st.w[25] = *reinterpret_cast<const uint16_t *>(q + 196 + 8 * h + 2 * (g & 1));
                 st.w[26] = *reinterpret_cast<const uint16_t *>(q + 208) | (static_cast<uint32_t>(sh) << 16);
             }
+        } else if constexpr (FMT == T_Q5_0) {
+            // block g = bytes [22g, 22g+22), from the dword at or 2 bytes before it (6 dwords, inside
+            // the chunk for every g)
+            const uint8_t *b = q + 22 * g - 2 * (g & 1);
+#pragma unroll
+            for (int k = 0; k < 6; ++k) st.w[k] = ld4(b + 4 * k);
         } else {
             // Q4_0: blocks 2g, 2g+1 = bytes [36g, 36g+36).  Q8_0: block g = bytes [34g, 34g+34), read
             // from the dword at or 2 bytes before it.
@@ -356,6 +410,14 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     float4 xv[XR];
 #pragma unroll
     for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
+    if constexpr (ROUTED) {
+        // the routes' experts (and down weights): every weight address depends on them
+        if (tid < a.routes) {
+            s_ids[tid] = a.ids[tid];
+            if constexpr (!SWIGLU) s_rw[tid] = a.rw[tid];
+        }
+        __syncthreads();
+    }
 
     auto stage_x_i8 = [&]() {
         // x as three int8 digit planes and (scale, sum) per 32 elements (x_digits4)
@@ -415,12 +477,21 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // served equally (a wave that starts late stays behind), so a fixed share per wave leaves the
     // workgroup waiting for its slowest wave; claiming on demand ends all waves within about one step
     // of each other.
+    // DEPTH 2: wave w starts with steps w and w + kWaves, both requested before the x staging
+    // (Q6_K's 27-dword steps would spill with three buffers)
+    constexpr int DEPTH = ROUTED && FMT != T_Q6_K ? QLIN_MFMA_ROUTED_DEPTH : QLIN_MFMA_DEPTH;
     __shared__ int next_step;
-    if (tid == 0) next_step = kWaves;
+    if (tid == 0) next_step = DEPTH * kWaves;
     if (tid < 4) s_zero[tid] = u32x4{0u, 0u, 0u, 0u};
     Pos cur = at(wave);
     Raw buf;
     load(buf, cur);
+    Pos second = cur;
+    Raw bb;
+    if constexpr (DEPTH == 2) {
+        second = at(wave + kWaves);
+        load(bb, second);
+    }
     stage_x();
     __syncthreads();
 
@@ -500,7 +571,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             // the 8 dwords of this lane's stored integers: Q4_K the pair's 32 bytes; Q4_0 blocks 2g,
             // 2g + 1 (16 bytes each); Q8_0 block g's 32 bytes
             uint32_t src[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-            if constexpr (FMT == T_Q6_K) {
+            if constexpr (FMT == T_Q6_K || FMT == T_Q5_0) {
                 // decoded below
             } else if constexpr (FMT == T_Q4_K) {
 #pragma unroll
@@ -567,6 +638,27 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
                 const float2 sx = *reinterpret_cast<const float2 *>(sxp + 2 * (p.sb * 4 + g));  // s of block g
                 const float dq = f16_bits_to_f32((cur.w[0] >> (16 * (g & 1))) & 0xffffu);
                 r = dq * (sx.x * digits(de));
+            } else if constexpr (FMT == T_Q5_0) {
+                // block g from its 6 dwords: d, then qh and qs (2 bytes into the window for even g)
+                const bool odd = g & 1;
+                const uint32_t qh = odd ? cur.w[1] : __builtin_amdgcn_alignbyte(cur.w[1], cur.w[0], 2);
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t qs = odd ? cur.w[2 + t] : __builtin_amdgcn_alignbyte(cur.w[2 + t], cur.w[1 + t], 2);
+                    lo[t] = (qs & M) | (spread4(qh >> (4 * t)) << 4);              // elements 4t .. 4t+3
+                    hi[t] = ((qs >> 4) & M) | (spread4(qh >> (16 + 4 * t)) << 4);  // elements 16+4t ..
+                }
+                const i32x4 b0 = {static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]),
+                                  static_cast<int>(lo[3])};
+                const i32x4 b1 = {static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]),
+                                  static_cast<int>(hi[3])};
+                i32x4 de = mfma_i8(pa[0], b0, i32x4{0, 0, 0, 0});
+                de = mfma_i8(pa[1], b1, de);
+                const float2 sx = *reinterpret_cast<const float2 *>(sxp + 2 * (p.sb * 4 + g));  // s, X of block g
+                const float dq = f16_bits_to_f32((cur.w[0] >> (16 * (g & 1))) & 0xffffu);
+                // q - 16: the offset leaves with the block sum
+                r = dq * (sx.x * digits(de) - 16.0f * sx.y);
             } else {
                 // MFMAs 0, 1 carry unit 2g (Q4_K: low nibbles of bytes 0..15, 16..31; Q4_0: block 2g's
                 // low, then high nibbles), 2, 3 unit 2g + 1
@@ -733,13 +825,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         if (lane == 0) c = atomicAdd(&next_step, 1);
         return at(__builtin_amdgcn_readfirstlane(c));
     };
-#if QLIN_MFMA_DEPTH == 2
+    if constexpr (DEPTH == 2) {
     // Two steps in flight while one is computed: a ring of three buffers, unrolled so that no
     // buffer is copied (a loop-carried copy of loaded registers waits for every outstanding load).
     // Claims are monotonic per wave, so once a claimed step is past the end, so are the later ones.
-    Pos pa = cur, pb = claim();
-    Raw bb;
-    load(bb, pb);
+    Pos pa = cur, pb = second;
     for (;;) {
         if (pa.s >= nsteps) break;
         const Pos pc = claim();
@@ -758,7 +848,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         __builtin_amdgcn_sched_barrier(0);
         process(bc, pc);
     }
-#else
+    } else {
     while (cur.s < nsteps) {
         const Pos nxt = claim();
         Raw nb;
@@ -768,9 +858,31 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         buf = nb;
         cur = nxt;
     }
-#endif
+    }
 
     __syncthreads();
+    if constexpr (ROUTED && !SWIGLU) {
+        // each route's dot in chunk order, one thread per (row, route), parked in the route's first
+        // chunk slot; then the routes in route order: out += sum fmaf(dot, w, .)
+        const int nq = a.routes, cpr = a.cpr;
+        for (int i = tid; i < nrows * nq; i += kThreads) {
+            float *pr = partial + (i / nq) * nsb + (i % nq) * cpr;
+            float dot = 0.0f;
+#pragma unroll 4
+            for (int c = 0; c < cpr; ++c) dot += pr[c];
+            pr[0] = dot;
+        }
+        __syncthreads();
+        for (int r = tid; r < nrows; r += kThreads) {
+            const float *pr = partial + r * nsb;
+            float total = 0.0f;
+            for (int q = 0; q < nq; ++q)
+                if (s_ids[q] >= 0) total = fmaf(pr[q * cpr], s_rw[q], total);
+            float *yp = mats.y[0] + grow(r);
+            *yp += total;
+        }
+        return;
+    }
     for (int r = tid; r < nrows; r += kThreads) {
         float tot[NW];
 #pragma unroll
@@ -782,7 +894,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             for (int sb = 0; sb < nsb; ++sb) tot[q] += partial[(r * NW + q) * nsb + sb];
         }
         const int gr = grow(r);
-        if constexpr (SWIGLU) {
+        if constexpr (ROUTED) {
+            // a route without an expert gives 0 (kernel.cu:1340-1385)
+            const bool none = s_ids[route_of(gr, a.route_rows, a.route_magic)] < 0;
+            mats.y[0][gr] = none ? 0.0f : tot[0] / (1.0f + expf(-tot[0])) * tot[1];
+        } else if constexpr (SWIGLU) {
             mats.y[0][gr] = tot[0] / (1.0f + expf(-tot[0])) * tot[1];
         } else {
             const uint8_t *wp;
@@ -800,6 +916,8 @@ struct Plan {
     bool magic_exact;  // every step index c of a workgroup has c * nsb < 2^32
 };
 
+// Dynamic LDS of a launch: x in the bf16 layout (which the int8 digits never exceed), the x sums,
+// and one partial per (row, matrix, chunk) of the workgroup's rows.
 Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
     Plan p;
     p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
@@ -814,73 +932,163 @@ Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int FMT, bool SWIGLU, int XR, bool WIDE>
-void launch_xr(const Plan &p, const MfmaArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((mfma_gemv_kernel<FMT, SWIGLU, XR, WIDE>), dim3(p.grid), dim3(threads_for(SWIGLU)), p.lds, s,
-                       a);
+// One instantiation of the kernel, with its own (static) LDS as the compiler laid it out: a plan
+// fits when that plus the plan's dynamic LDS is within the CU's 160 KB.
+struct Kern {
+    const void *fn = nullptr;
+    size_t static_lds = kMaxLds;
+    unsigned threads = 0;
+};
+template <int FMT, bool SW, int XR, bool WIDE, bool R>
+Kern kern() {
+    const void *fn = reinterpret_cast<const void *>(&mfma_gemv_kernel<FMT, SW, XR, WIDE, R>);
+    static const size_t lds = [fn] {
+        hipFuncAttributes fa{};
+        return hipFuncGetAttributes(&fa, fn) == hipSuccess ? fa.sharedSizeBytes : kMaxLds;
+    }();
+    return Kern{fn, lds, static_cast<unsigned>(threads_for(SW))};
 }
-
-template <int FMT, bool SWIGLU, bool WIDE>
-void launch_sw(const Plan &p, const MfmaArgs &a, int k, hipStream_t s) {
-    constexpr int kThreads = threads_for(SWIGLU);
-    const int need = (k / 4 + kThreads - 1) / kThreads;  // float4 loads of x per thread
-    if (need <= 1) launch_xr<FMT, SWIGLU, 1, WIDE>(p, a, s);
-    else if (need <= 2) launch_xr<FMT, SWIGLU, 2, WIDE>(p, a, s);
-    else if (need <= 4) launch_xr<FMT, SWIGLU, 4, WIDE>(p, a, s);
-    else if (need <= 6) launch_xr<FMT, SWIGLU, 6, WIDE>(p, a, s);
-    else launch_xr<FMT, SWIGLU, kMaxXr, WIDE>(p, a, s);
-}
-
-template <int FMT, bool WIDE = false>
-void launch_fmt(const Plan &p, const MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
-    if (swiglu) launch_sw<FMT, true, WIDE>(p, a, k, s);
-    else launch_sw<FMT, false, WIDE>(p, a, k, s);
-}
-
-int chunk_elems(int type) { return type == T_Q8_0 ? Chunk<T_Q8_0>::elems : Chunk<T_Q4_K>::elems; }
-int sum_elems(int type) { return type == T_Q6_K ? kSumElems<T_Q6_K> : kSumElems<T_Q4_K>; }
-
-hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, hipStream_t s) {
-    const Plan p = plan(a.total, k, a.nsb, swiglu, sum_elems(type));
-    if (!p.magic_exact) return hipErrorInvalidValue;  // mfma_ok rejects these shapes first
-    const int units = QLIN_MFMA_INTERLEAVE ? (a.total + 15) / 16 : a.total;  // tiles or rows per workgroup
-    a.rows_q = units / p.grid;
-    a.rows_r = units % p.grid;
-    a.nsb_magic = a.nsb > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + a.nsb - 1) / a.nsb) : 0u;
-    bool q6_wide = type == T_Q6_K && a.row_bytes % 16 == 0;
-    for (int i = 0; i < (swiglu ? 2 : a.nmat); ++i) q6_wide = q6_wide && aligned16(a.w[i]);
-    switch (type) {
-        case T_Q4_K: launch_fmt<T_Q4_K>(p, a, k, swiglu, s); break;
-        case T_Q4_0: launch_fmt<T_Q4_0>(p, a, k, swiglu, s); break;
-        case T_Q8_0: launch_fmt<T_Q8_0>(p, a, k, swiglu, s); break;
-        case T_Q6_K:
-            if (q6_wide) launch_fmt<T_Q6_K, true>(p, a, k, swiglu, s);
-            else launch_fmt<T_Q6_K>(p, a, k, swiglu, s);
-            break;
-        default: return hipErrorInvalidValue;
+// x loads per thread from K; routed launches have at most 4 (K <= 16 * threads)
+template <int FMT, bool SW, bool WIDE, bool R>
+Kern kern_xr(int k) {
+    constexpr int kThreads = threads_for(SW);
+    const int need = (k / 4 + kThreads - 1) / kThreads;
+    if (need <= 1) return kern<FMT, SW, 1, WIDE, R>();
+    if (need <= 2) return kern<FMT, SW, 2, WIDE, R>();
+    if (need <= 4) return kern<FMT, SW, 4, WIDE, R>();
+    if constexpr (!R) {
+        if (need <= 6) return kern<FMT, SW, 6, WIDE, R>();
+        if (need <= kMaxXr) return kern<FMT, SW, kMaxXr, WIDE, R>();
     }
-    return hipGetLastError();
+    return Kern{};
+}
+template <bool SW, bool R>
+Kern kern_for(int type, bool wide, int k) {
+    switch (type) {
+        case T_Q4_K: return kern_xr<T_Q4_K, SW, false, R>(k);
+        case T_Q4_0: return kern_xr<T_Q4_0, SW, false, R>(k);
+        case T_Q8_0: return kern_xr<T_Q8_0, SW, false, R>(k);
+        case T_Q5_0: return kern_xr<T_Q5_0, SW, false, R>(k);
+        case T_Q6_K:
+            if constexpr (!R) {
+                if (wide) return kern_xr<T_Q6_K, SW, true, R>(k);
+            }
+            return kern_xr<T_Q6_K, SW, false, R>(k);
+        default: return Kern{};
+    }
+}
+Kern kernel_for(int type, bool swiglu, bool routed, bool wide, int k) {
+    if (routed) return swiglu ? kern_for<true, true>(type, false, k) : kern_for<false, true>(type, false, k);
+    return swiglu ? kern_for<true, false>(type, wide, k) : kern_for<false, false>(type, wide, k);
+}
+
+int chunk_elems(int type) { return type == T_Q8_0 || type == T_Q5_0 ? 128 : 256; }
+int sum_elems(int type) { return type == T_Q6_K ? kSumElems<T_Q6_K> : kSumElems<T_Q4_K>; }
+bool mfma_type(int type) {
+    return type == T_Q4_K || type == T_Q4_0 || type == T_Q8_0 || type == T_Q6_K || type == T_Q5_0;
+}
+// Q4_K loads 16-byte pieces; the 32-weight formats and Q6_K aligned dwords
+size_t weight_align(int type) { return type == T_Q4_K ? 16 : 4; }
+uint32_t magic_of(int d) { return d > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + d - 1) / d) : 0u; }
+
+// Q6_K rows of whole 16-byte units from 16-aligned bases take the 16-byte-piece form
+bool q6_wide(int type, const MfmaArgs &a, int nw) {
+    bool wide = type == T_Q6_K && a.row_bytes % 16 == 0;
+    for (int i = 0; i < nw; ++i) wide = wide && aligned16(a.w[i]);
+    return wide;
+}
+
+// The launch's kernel and plan, or no kernel when the shape does not fit (callers then take the
+// per-element kernels).
+struct Launch {
+    Kern k;
+    Plan p;
+    bool ok = false;
+};
+Launch prepare(int type, const MfmaArgs &a, int k, bool swiglu, bool routed) {
+    Launch l;
+    l.k = kernel_for(type, swiglu, routed, !routed && q6_wide(type, a, swiglu ? 2 : a.nmat), k);
+    if (!l.k.fn) return l;
+    l.p = plan(a.total, k, a.nsb, swiglu, sum_elems(type));
+    l.ok = l.p.magic_exact && l.p.lds + l.k.static_lds <= kMaxLds;
+    return l;
+}
+
+hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStream_t s) {
+    const Launch l = prepare(type, a, k, swiglu, routed);
+    if (!l.ok) return hipErrorInvalidValue;  // the *_ok checks reject these shapes first
+    const int units = QLIN_MFMA_INTERLEAVE ? (a.total + 15) / 16 : a.total;  // tiles or rows per workgroup
+    a.rows_q = units / l.p.grid;
+    a.rows_r = units % l.p.grid;
+    a.nsb_magic = magic_of(a.nsb);
+    void *args[] = {&a};
+    const hipError_t e = hipLaunchKernel(l.k.fn, dim3(l.p.grid), dim3(l.k.threads), args, l.p.lds, s);
+    return e != hipSuccess ? e : hipGetLastError();
+}
+
+MfmaArgs base_args(int type, size_t rb, const float *x, int k) {
+    MfmaArgs a{};
+    a.row_bytes = rb;
+    a.x = x;
+    a.nsb = k / chunk_elems(type);
+    return a;
+}
+
+MfmaArgs swiglu_routed_args(int type, const uint8_t *wg, const uint8_t *wu, size_t eb, size_t rb, const float *x,
+                            const int *ids, float *act, int routes, int ffn, int k) {
+    MfmaArgs a = base_args(type, rb, x, k);
+    a.w[0] = wg;
+    a.w[1] = wu;
+    a.y[0] = act;
+    a.nmat = 1;
+    a.total = routes * ffn;
+    a.row_end[0] = a.total;
+    a.ids = ids;
+    a.eb = eb;
+    a.routes = routes;
+    a.route_rows = ffn;
+    a.route_magic = magic_of(ffn);
+    return a;
+}
+
+MfmaArgs down_routed_args(int type, const uint8_t *wd, size_t eb, size_t rb, const float *act, const int *ids,
+                          const float *rw, float *out, int routes, int hidden, int ffn) {
+    MfmaArgs a = base_args(type, rb, act, routes * ffn);
+    a.w[0] = wd;
+    a.y[0] = out;
+    a.nmat = 1;
+    a.total = hidden;
+    a.row_end[0] = hidden;
+    a.ids = ids;
+    a.rw = rw;
+    a.eb = eb;
+    a.routes = routes;
+    a.cpr = ffn / chunk_elems(type);
+    a.cpr_magic = magic_of(a.cpr);
+    return a;
 }
 
 }  // namespace
 
 bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float *x, int total, int k, bool swiglu) {
-    if (type != T_Q4_K && type != T_Q4_0 && type != T_Q8_0 && type != T_Q6_K) return false;
-    // Q4_K loads 16-byte pieces; the 32-weight formats aligned dwords
-    const size_t wal = type == T_Q4_K ? 16 : 4;
-    // whole chunks (Q8_0: 128 weights, the others 256); x is staged as float4s in groups of 8 lanes
+    if (!mfma_type(type)) return false;
+    const size_t wal = weight_align(type);
+    // whole chunks (Q8_0, Q5_0: 128 weights, the others 256); x is staged as float4s in groups of 8 lanes
     if (nmat < 1 || nmat > kMaxStreamMats || k % chunk_elems(type) || rb % wal || !aligned16(x) || total <= 0)
         return false;
-    if (k / 4 > kMaxXr * threads_for(swiglu)) return false;
-    for (int i = 0; i < nmat; ++i)
+    MfmaArgs a = base_args(type, rb, x, k);
+    for (int i = 0; i < nmat; ++i) {
         if (reinterpret_cast<uintptr_t>(w[i]) % wal) return false;
-    const Plan p = plan(total, k, k / chunk_elems(type), swiglu, sum_elems(type));
-    return p.lds + kStaticLds <= kMaxLds && p.magic_exact;
+        a.w[i] = w[i];
+    }
+    a.nmat = nmat;
+    a.total = total;
+    return prepare(type, a, k, swiglu, false).ok;
 }
 
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,
                      const float *x, int k, bool add, hipStream_t s) {
-    MfmaArgs a{};
+    MfmaArgs a = base_args(type, rb, x, k);
     int total = 0;
     for (int i = 0; i < nmat; ++i) {
         a.w[i] = w[i];
@@ -890,28 +1098,55 @@ hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const i
     }
     if (total == 0) return hipSuccess;
     a.nmat = nmat;
-    a.row_bytes = rb;
-    a.x = x;
-    a.nsb = k / chunk_elems(type);
     a.total = total;
     a.add = add ? 1 : 0;
-    return launch(type, a, k, false, s);
+    return launch(type, a, k, false, false, s);
 }
 
 hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x, float *act, int ffn,
                        int k, hipStream_t s) {
     if (ffn == 0) return hipSuccess;
-    MfmaArgs a{};
+    MfmaArgs a = base_args(type, rb, x, k);
     a.w[0] = wg;
     a.w[1] = wu;
     a.y[0] = act;
     a.row_end[0] = ffn;
     a.nmat = 1;
-    a.row_bytes = rb;
-    a.x = x;
-    a.nsb = k / chunk_elems(type);
     a.total = ffn;
-    return launch(type, a, k, true, s);
+    return launch(type, a, k, true, false, s);
+}
+
+bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1, size_t eb, size_t rb, const float *x,
+                    int routes, int rows, int k) {
+    if (!mfma_type(type) || routes < 1 || routes > kMaxRoutes || rows <= 0 || k <= 0) return false;
+    const size_t wal = weight_align(type);
+    const auto al = [wal](const void *p) { return reinterpret_cast<uintptr_t>(p) % wal == 0; };
+    if (k % chunk_elems(type) || rb % wal || eb % wal || !al(w0) || (swiglu && !al(w1)) || !aligned16(x)) return false;
+    const uint64_t lim = uint64_t{1} << 32;
+    MfmaArgs a;
+    if (swiglu) {
+        // route_of(gr) for every concatenated row gr < routes * rows
+        if (static_cast<uint64_t>(routes) * rows * rows >= lim) return false;
+        a = swiglu_routed_args(type, w0, w1, eb, rb, x, nullptr, nullptr, routes, rows, k);
+        return prepare(type, a, k, true, true).ok;
+    }
+    // the down projection: rows = hidden, k = ffn per route; route_of(chunk) for every chunk
+    const int cpr = k / chunk_elems(type);
+    if (static_cast<uint64_t>(routes) * cpr * cpr >= lim) return false;
+    a = down_routed_args(type, w0, eb, rb, x, nullptr, nullptr, nullptr, routes, rows, k);
+    return prepare(type, a, routes * k, false, true).ok;
+}
+
+hipError_t mfma_swiglu_routed(int type, const uint8_t *wg, const uint8_t *wu, size_t eb, size_t rb, const float *x,
+                              const int *ids, float *act, int routes, int ffn, int k, hipStream_t s) {
+    MfmaArgs a = swiglu_routed_args(type, wg, wu, eb, rb, x, ids, act, routes, ffn, k);
+    return launch(type, a, k, true, true, s);
+}
+
+hipError_t mfma_down_routed(int type, const uint8_t *wd, size_t eb, size_t rb, const float *act, const int *ids,
+                            const float *rw, float *out, int routes, int hidden, int ffn, hipStream_t s) {
+    MfmaArgs a = down_routed_args(type, wd, eb, rb, act, ids, rw, out, routes, hidden, ffn);
+    return launch(type, a, routes * ffn, false, true, s);
 }
 
 }  // namespace qlin

@@ -6,7 +6,9 @@
 //   swiglu                 1289-1328  act[o] = g / (1 + exp(-g)) * u, g = Wg[o].x, u = Wu[o].x
 //   swiglu_indexed         1340-1385  the same per route r on expert expert_ids[r]; id < 0 -> 0.
 //   down_indexed_ordered   2253-2287  out[h] += sum_r fmaf(Wd[e_r][h].act[r], w_r, .) in route order
-// One wave64 per output row; the dot products decode weights per element (any alignment).
+// swiglu_indexed and down_indexed_ordered run on the matrix-core decode kernel's routed forms
+// (qlin_mfma_gemv.hip) when the layout meets its alignment; otherwise, and for the rest here, one
+// wave64 per output row, the dot products decoding weights per element (any alignment).
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 
@@ -221,6 +223,9 @@ hipError_t swiglu_indexed(int type, const uint8_t *wg, const uint8_t *wu, size_t
                           int ffn, int in_dim, hipStream_t s) {
     const int64_t waves = static_cast<int64_t>(k) * ffn;
     if (waves == 0) return hipSuccess;
+    // the k routes' gate/up pairs as one matrix-core SwiGLU launch when the layout allows
+    if (ids && g_eb == u_eb && g_rb == u_rb && mfma_routed_ok(type, true, wg, wu, g_eb, g_rb, x, k, ffn, in_dim))
+        return mfma_swiglu_routed(type, wg, wu, g_eb, g_rb, x, ids, act, k, ffn, in_dim, s);
     const int blocks = static_cast<int>((waves + 3) / 4);
     QLIN_TYPE_SWITCH(type, hipLaunchKernelGGL((swiglu_kernel<TT>), dim3(blocks), dim3(kBlock), 0, s, wg, wu,
                                               g_eb, u_eb, g_rb, u_rb, x, ids, act, k, ffn, in_dim));
@@ -241,6 +246,9 @@ hipError_t down_indexed_ordered(int type, const uint8_t *wd, size_t d_eb, size_t
                                 const int *ids, const float *rw, float *out, int k, int hidden, int ffn,
                                 hipStream_t s) {
     if (hidden == 0) return hipSuccess;
+    // the k routes' down rows as one matrix-core GEMV over their activations end to end
+    if (k > 0 && mfma_routed_ok(type, false, wd, wd, d_eb, d_rb, act, k, hidden, ffn))
+        return mfma_down_routed(type, wd, d_eb, d_rb, act, ids, rw, out, k, hidden, ffn, s);
     const int blocks = (hidden + 3) / 4;
     QLIN_TYPE_SWITCH(type, hipLaunchKernelGGL((down_kernel<TT>), dim3(blocks), dim3(kBlock), 0, s, wd, d_eb, d_rb,
                                               act, ids, rw, out, k, hidden, ffn));

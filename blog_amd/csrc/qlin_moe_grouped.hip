@@ -182,9 +182,6 @@ __device__ __forceinline__ int64_t uni(int64_t v) {
                                 static_cast<uint32_t>(uni(static_cast<int>(u))));
 }
 
-// bits 0..3 of b to bit 0 of bytes 0..3 (the four shifted copies of b do not overlap)
-__device__ __forceinline__ uint32_t spread4(uint32_t b) { return __umul24(b & 0xfu, 0x204081u) & 0x01010101u; }
-
 // Cost of one 16-row tile of an expert with cnt routes: its passes and its routes.
 template <int FMT, int NQ>
 __device__ __forceinline__ int64_t tile_cost(int cnt) {

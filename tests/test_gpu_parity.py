@@ -104,7 +104,7 @@ GEMV_CASES = [
     (Q8_0, 4096, 4096), (Q8_0, 7, 96), (Q8_0, 4864, 896), (Q8_0, 33, 256), (Q8_0, 1000, 8448),
     (Q8_0, 896, 896), (Q8_0, 896, 4864), (Q8_0, 128, 128),
     (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64), (Q4_0, 17, 256), (Q4_0, 300, 4608),
-    (Q5_0, 2048, 1408), (Q5_0, 5, 64),
+    (Q5_0, 2048, 1408), (Q5_0, 5, 64), (Q5_0, 300, 4096), (Q5_0, 33, 128), (Q5_0, 100, 18944),
     (Q6_K, 64, 512), (Q6_K, 257, 2048), (Q6_K, 16384, 2048), (Q6_K, 33, 768), (Q6_K, 100, 7168),
 ]
 
@@ -122,7 +122,7 @@ def test_gemv_parity(qtype, out_dim, in_dim):
 
 
 @pytest.mark.parametrize("qtype,out_dim,in_dim", [(Q4_K, 300, 3584), (Q4_K, 1000, 8448), (Q8_0, 300, 4096),
-                                                  (Q8_0, 300, 896), (Q4_0, 1000, 3584)])
+                                                  (Q8_0, 300, 896), (Q4_0, 1000, 3584), (Q5_0, 300, 1408)])
 def test_gemv_generic_path_agrees(qtype, out_dim, in_dim):
     """A weight pointer 2 bytes off the alignment the matrix-core kernel needs takes the generic
     kernel: both agree with the oracle."""
@@ -439,6 +439,60 @@ def test_swiglu_indexed_and_down_ordered():
               dev(rw), out_d, k, hid, ffn)
     ref = orc.down_indexed_ordered(Q5_0, wdn, deb, drb, act_ref, ids, rw, out0, hid, ffn)
     assert normwise_rel_err(host(out_d), ref) <= FP32
+
+
+ROUTED_CASES = [
+    # DeepSeek-V2-Lite's routes (64 x [1408, 2048] Q4_K gate/up, [2048, 1408] Q5_0 down)
+    (Q4_K, Q5_0, 64, 1408, 2048, [3, 17, 63, 0, 42, 9]),
+    # tiles of 16 concatenated rows that span two routes (ffn 200, SwiGLU only), no expert, a repeat
+    (Q4_K, Q8_0, 16, 200, 768, [5, -1, 5, 2]),
+    (Q4_K, Q8_0, 16, 256, 768, [5, -1, 5, 2]),
+    # 16 routes (the most one launch takes), Q6_K gate/up, Q4_K down
+    (Q6_K, Q4_K, 8, 256, 512, [7, 1, -1, 0, 3, 2, 6, 4, 5, 1, 0, 2, 3, 4, 5, 6]),
+    (Q4_K, Q6_K, 4, 512, 256, [-1, -1]),                 # no expert at all
+    (Q8_0, Q5_0, 6, 384, 1024, [2, 4, 1]),
+    (Q4_0, Q8_0, 5, 128, 256, [4, 0, 3, 1, 2, 4, 0, 3, 1, 2, 4, 0, 3, 1, 2, 4, 0]),  # 17 routes: per-element kernels
+]
+
+
+@pytest.mark.parametrize("gu_type,dn_type,E,ffn,hid,ids", ROUTED_CASES)
+def test_routed_swiglu_and_down(gu_type, dn_type, E, ffn, hid, ids):
+    """launch_quant_swiglu_indexed and launch_quant_down_f32_indexed_accum_ordered (kernel.cu:1340-1385,
+    2253-2287) on the matrix-core routed forms, and from a base 2 bytes off their alignment on the
+    per-element kernels: both agree with the oracle, and a route without an expert gives 0."""
+    k = len(ids)
+    ids = np.array(ids, np.int32)
+    wg, grb, geb = _experts(gu_type, E, ffn, hid, 900 + ffn + k)
+    wu, _, _ = _experts(gu_type, E, ffn, hid, 901 + ffn + k)
+    # (a SwiGLU width that is not whole 32-weight blocks has no down projection)
+    has_down = ffn % qgen.BLOCK[dn_type][0] == 0
+    wdn, drb, deb = _experts(dn_type, E, hid, ffn, 902 + ffn + k) if has_down else (np.zeros(4, np.uint8), 0, 0)
+    x = qgen.random_x(1, hid, seed=903 + k)[0]
+    rw = np.random.default_rng(904 + k).uniform(0.05, 1.0, k).astype(np.float32)
+    act_ref = orc.swiglu_indexed(gu_type, wg, wu, geb, geb, grb, grb, x, ids, ffn, hid)
+    out0 = np.random.default_rng(905).standard_normal(hid).astype(np.float32)
+    ref = orc.down_indexed_ordered(dn_type, wdn, deb, drb, act_ref, ids, rw, out0, hid, ffn) if has_down else None
+    for off in (0, 2):
+        banner(f"routed swiglu/down gu={gu_type} dn={dn_type} ffn={ffn} hid={hid} k={k} offset={off}")
+        pad = np.zeros(off, np.uint8)
+        wgd, wud, wdd = dev(np.concatenate([pad, wg])), dev(np.concatenate([pad, wu])), dev(np.concatenate([pad, wdn]))
+        act_d = empty_f32(k, ffn)
+        qlin.call("qlin_launch_quant_swiglu_indexed", gu_type, wgd.data_ptr() + off, wud.data_ptr() + off, geb, geb,
+                  grb, grb, dev(x), dev(ids), act_d, k, ffn, hid)
+        act = host(act_d)
+        assert np.all(act[ids < 0] == 0.0)
+        assert normwise_rel_err(act, act_ref) <= 1e-4
+        if not has_down:
+            continue
+        out_d = dev(out0)
+        qlin.call("qlin_launch_quant_down_f32_indexed_accum_ordered", dn_type, wdd.data_ptr() + off, deb, drb,
+                  dev(act_ref), dev(ids), dev(rw), out_d, k, hid, ffn)
+        got = host(out_d)
+        if np.all(ids < 0):
+            assert np.array_equal(got, out0)  # nothing added
+            continue
+        assert normwise_rel_err(got - out0, ref - out0) <= 1e-4
+        assert normwise_rel_err(got, ref) <= FP32
 
 
 def test_shared_swiglu():
