@@ -671,4 +671,22 @@ int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8
     return QLIN_OK;
 }
 
+int qlin_moe_routed_decode_grouped_noalloc(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                           int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
+                                           int ffn_dim, int in_dim, int hidden, const float *x, const int *ids,
+                                           const float *rw, float *out, int tokens, int k) {
+    static_assert(QLIN_MOE_NOALLOC_SCRATCH_BYTES == qlin::kMoeStaticScratchBytes, "header and library agree");
+    // a batch whose workspace would not fit the library's scratch is refused before anything runs
+    const size_t need = qlin_moe_grouped_workspace_bytes(tokens, k, n_experts, ffn_dim, hidden);
+    if (need > qlin::kMoeStaticScratchBytes) return QLIN_ERR_LIMIT;
+    void *ws = nullptr;
+    if (tokens > 0 && k > 0 && need > 0) {
+        ws = qlin::moe_static_scratch();
+        if (!ws) return QLIN_ERR_LAUNCH;
+    }
+    return qlin_moe_routed_decode_grouped(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts,
+                                          ffn_dim, in_dim, hidden, x, ids, rw, ws, qlin::kMoeStaticScratchBytes, out,
+                                          tokens, k);
+}
+
 }  // extern "C"

@@ -126,6 +126,10 @@ hipError_t down_indexed_ordered(int type, const uint8_t *wd, size_t d_expert_byt
 
 // Batched routed decode, each selected expert read once per pass over its routes (qlin_moe_grouped.hip).
 size_t moe_grouped_workspace(int tokens, int k, int n_experts, int ffn_dim, int hidden);
+// The per-device scratch of the allocation-free batched entry point (kMoeStaticScratchBytes), its
+// address resolved once per device; nullptr when it cannot be.
+constexpr size_t kMoeStaticScratchBytes = size_t{8} << 20;
+void *moe_static_scratch();
 bool moe_grouped_shape_ok(int n_experts, int64_t routes);
 bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
                        const float *x, int in_dim, int ffn_dim, int n_experts, int routes);

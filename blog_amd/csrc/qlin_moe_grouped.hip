@@ -21,6 +21,7 @@
 #include "qlin_mfma.hpp"
 
 #include <algorithm>
+#include <mutex>
 
 namespace qlin {
 namespace {
@@ -840,6 +841,33 @@ bool down_stream_ok(int type, const uint8_t *w, size_t eb, size_t rb, int ffn) {
 }
 
 }  // namespace
+
+// ---- the scratch of the allocation-free batched entry point --------------------------------------
+// Callers that cannot allocate device memory (HIP graph capture, serving loops that forbid it) run
+// the batched decode on this array instead of a workspace of their own.  Each GPU the library runs
+// on holds its own copy until the process ends, and every call on that GPU shares it: calls that
+// overlap on one GPU race.  Nothing in it has to start at zero: each call writes every word of it
+// that it reads (group_kernel the offsets, lists and selected experts; the streaming launches the
+// activations and route results they hand on).
+namespace {
+static __device__ __align__(256) uint8_t scratch[kMoeStaticScratchBytes];
+}  // namespace
+
+void *moe_static_scratch() {
+    constexpr int kMaxDevices = 64;
+    static void *ptrs[kMaxDevices] = {};
+    static std::mutex m;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(m);
+    if (!ptrs[dev]) {
+        // this device's copy of the array (the device is current); host code uses only this address
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        ptrs[dev] = p;
+    }
+    return ptrs[dev];
+}
 
 size_t moe_grouped_workspace(int tokens, int k, int n_experts, int ffn, int hidden) {
     const size_t R = static_cast<size_t>(tokens) * k;

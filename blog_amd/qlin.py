@@ -71,6 +71,7 @@ SIGNATURES = {
     "qlin_moe_routed_decode_indexed": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, P, I]),
     "qlin_moe_grouped_workspace_bytes": (SZ, [I, I, I, I, I]),
     "qlin_moe_routed_decode_grouped": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, SZ, P, I, I]),
+    "qlin_moe_routed_decode_grouped_noalloc": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, I, I]),
     "qlin_launch_quant_embedding": (I, [I, P, P, P, SZ, I, I]),
     "qlin_launch_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
     "qlin_launch_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),

@@ -254,6 +254,20 @@ int qlin_moe_routed_decode_grouped(int gate_up_type, const uint8_t *gate_exps, c
                                    const float *x, const int *expert_ids, const float *route_weights,
                                    void *workspace, size_t workspace_bytes, float *out, int tokens, int k);
 
+/* No counterpart in the reference: qlin_moe_routed_decode_grouped for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid it).  The same arguments
+ * without the workspace: the call runs on a scratch array the library keeps on each GPU for the
+ * life of the process, QLIN_MOE_NOALLOC_SCRATCH_BYTES long, and allocates nothing.  A batch whose
+ * qlin_moe_grouped_workspace_bytes(...) exceeds that size is refused with QLIN_ERR_LIMIT before
+ * anything runs.  Every call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. */
+#define QLIN_MOE_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int qlin_moe_routed_decode_grouped_noalloc(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                           size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                           size_t down_bytes, int n_experts, int ffn_dim, int in_dim,
+                                           int hidden_size, const float *x, const int *expert_ids,
+                                           const float *route_weights, float *out, int tokens, int k);
+
 /* launch_quant_embedding (kernel.cuh:141-142): output[t, :] = the dequantized row input[t] of a
  * quantized table [vocab, hidden_size] (Q4_K, Q6_K, Q5_0 or Q8_0; bit-exact element values).  As in
  * the reference, the ids must be rows of the table; they are device data and are not checked. */
