@@ -114,6 +114,9 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #ifndef QLIN_MFMA_FINAL_UNROLL
 #define QLIN_MFMA_FINAL_UNROLL 4  // batches the final per-row sum's LDS reads (same order of adds)
 #endif
+#ifndef QLIN_MFMA_FINAL_SPLIT
+#define QLIN_MFMA_FINAL_SPLIT 8  // lanes per row in the final sum of rows of many chunks (1: one thread)
+#endif
 #ifndef QLIN_MFMA_MATMAJOR
 #define QLIN_MFMA_MATMAJOR 1  // SwiGLU steps: 1 = all gate tiles, then all up tiles; 0 = tile-major
 #endif
@@ -883,16 +886,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         }
         return;
     }
-    for (int r = tid; r < nrows; r += kThreads) {
-        float tot[NW];
-#pragma unroll
-        for (int q = 0; q < NW; ++q) {
-            tot[q] = 0.0f;
-#if QLIN_MFMA_FINAL_UNROLL > 1
-#pragma unroll QLIN_MFMA_FINAL_UNROLL
-#endif
-            for (int sb = 0; sb < nsb; ++sb) tot[q] += partial[(r * NW + q) * nsb + sb];
-        }
+    auto write_row = [&](int r, const float (&tot)[NW]) {
         const int gr = grow(r);
         if constexpr (ROUTED) {
             // a route without an expert gives 0 (kernel.cu:1340-1385)
@@ -907,6 +901,40 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             mats.locate(gr, wp, yp, local);
             yp[local] = a.add ? yp[local] + tot[0] : tot[0];
         }
+    };
+    // Each row's step partials added in a fixed order.  With many chunks, L consecutive lanes share
+    // a row, lane j adding partials j, j + L, ..., then a butterfly over the L lanes: a thread alone
+    // would wait on nsb dependent LDS reads (74 for a K = 18944 row).
+    constexpr int L = QLIN_MFMA_FINAL_SPLIT;
+    if (L > 1 && nsb >= 2 * L) {
+        const int span = (nrows * L + 63) / 64 * 64;  // whole waves, for the shuffles
+        for (int i = tid; i < span; i += kThreads) {
+            const int r = i / L, j = i % L;
+            const bool live = r < nrows;
+            float tot[NW];
+#pragma unroll
+            for (int q = 0; q < NW; ++q) {
+                tot[q] = 0.0f;
+                if (live)
+                    for (int sb = j; sb < nsb; sb += L) tot[q] += partial[(r * NW + q) * nsb + sb];
+#pragma unroll
+                for (int m = L / 2; m > 0; m >>= 1) tot[q] += __shfl_xor(tot[q], m, 64);
+            }
+            if (live && j == 0) write_row(r, tot);
+        }
+        return;
+    }
+    for (int r = tid; r < nrows; r += kThreads) {
+        float tot[NW];
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+            tot[q] = 0.0f;
+#if QLIN_MFMA_FINAL_UNROLL > 1
+#pragma unroll QLIN_MFMA_FINAL_UNROLL
+#endif
+            for (int sb = 0; sb < nsb; ++sb) tot[q] += partial[(r * NW + q) * nsb + sb];
+        }
+        write_row(r, tot);
     }
 }
 
