@@ -541,7 +541,7 @@ def wl_c5(args, torch, qlin, gen):
     log(f"c5: grouped {us:.2f} us/step, per-token facade {us_tok:.2f} us, {distinct} distinct experts")
     return {
         "metric": "MoE layer decode HBM GB/s (DeepSeek-V2-Lite shape, 16 tokens, top-6 of 64 + 2 shared)",
-        "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / 8000, 2),
+        "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
         "n_gpus": 1, "steps": reps * copies, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (random Q4_K / Q5_0 expert blocks, f32 N(0,1) x and router logits), 4 weight copies",

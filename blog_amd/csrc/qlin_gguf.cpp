@@ -227,8 +227,13 @@ struct qlin_gguf {
             t.type = static_cast<int>(c.uint(4));
             t.offset = c.uint(8);
             int64_t be, bb;
-            if (!block_trait(t.type, be, bb) || elems % static_cast<uint64_t>(be)) throw FormatError{};
-            t.nbytes = elems / static_cast<uint64_t>(be) * static_cast<uint64_t>(bb);
+            // whole blocks per row (ne[0], the innermost dimension), and a byte count that fits in 64 bits
+            if (!block_trait(t.type, be, bb) || elems % static_cast<uint64_t>(be) ||
+                (nd > 0 && dims[0] % static_cast<uint64_t>(be)))
+                throw FormatError{};
+            const uint64_t nblocks = elems / static_cast<uint64_t>(be);
+            if (nblocks > UINT64_MAX / static_cast<uint64_t>(bb)) throw FormatError{};
+            t.nbytes = nblocks * static_cast<uint64_t>(bb);
         }
         size_t start = c.pos();
         if (start % alignment) start += alignment - start % alignment;

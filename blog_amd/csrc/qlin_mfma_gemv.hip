@@ -72,6 +72,7 @@
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
+#include "qlin_plan.hpp"
 
 namespace qlin {
 namespace {
@@ -120,7 +121,7 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #ifndef QLIN_MFMA_MATMAJOR
 #define QLIN_MFMA_MATMAJOR 1  // SwiGLU steps: 1 = all gate tiles, then all up tiles; 0 = tile-major
 #endif
-constexpr size_t kMaxLds = 160 * 1024;
+using plan::kMaxLds;
 constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * threads
 
 // Weights per step chunk of one row, and its bytes.
@@ -938,24 +939,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     }
 }
 
-struct Plan {
-    int grid;
-    size_t lds;
-    bool magic_exact;  // every step index c of a workgroup has c * nsb < 2^32
-};
+using Plan = plan::Gemv;
 
-// Dynamic LDS of a launch: x in the bf16 layout (which the int8 digits never exceed), the x sums,
-// and one partial per (row, matrix, chunk) of the workgroup's rows.
-Plan plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
-    Plan p;
-    p.grid = max(1, min(device_info().cu_count, (total + 15) / 16));
-    const int rows = QLIN_MFMA_INTERLEAVE ? ((total + 15) / 16 + p.grid - 1) / p.grid * 16 : (total + p.grid - 1) / p.grid;
-    const uint64_t steps = static_cast<uint64_t>((rows + 15) / 16) * (swiglu ? 2 : 1) * nsb;
-    p.magic_exact = steps * static_cast<uint64_t>(nsb) < (uint64_t{1} << 32);
-    const size_t K = static_cast<size_t>(k);
-    p.lds = 4 * K + (K / sum_elems) * sizeof(float) +
-            static_cast<size_t>(rows) * (swiglu ? 2 : 1) * nsb * sizeof(float);
-    return p;
+Plan make_plan(int total, int k, int nsb, bool swiglu, int sum_elems) {
+    return plan::gemv(total, k, nsb, swiglu, sum_elems, device_info().cu_count, QLIN_MFMA_INTERLEAVE != 0);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1037,8 +1024,8 @@ Launch prepare(int type, const MfmaArgs &a, int k, bool swiglu, bool routed) {
     Launch l;
     l.k = kernel_for(type, swiglu, routed, !routed && q6_wide(type, a, swiglu ? 2 : a.nmat), k);
     if (!l.k.fn) return l;
-    l.p = plan(a.total, k, a.nsb, swiglu, sum_elems(type));
-    l.ok = l.p.magic_exact && l.p.lds + l.k.static_lds <= kMaxLds;
+    l.p = make_plan(a.total, k, a.nsb, swiglu, sum_elems(type));
+    l.ok = plan::gemv_fits(l.p, l.k.static_lds);
     return l;
 }
 

@@ -19,6 +19,7 @@
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
+#include "qlin_plan.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -772,56 +773,36 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-constexpr size_t kMaxLds = 160 * 1024;
-// the streaming kernel's static LDS (cost prefix, scan totals, zero operands, step counter), with
-// some margin; launch_stream checks the compiled size against it
-constexpr size_t kStreamStaticLds = (kMaxExperts + 1 + kSWaves) * sizeof(int64_t) + 256;
+using plan::kMaxLds;
 
-// A streaming launch: one workgroup per CU, routes per pass, and the tiles whose partials fit in
-// LDS at once (a workgroup's share is taken in pieces of that many).  The number of selected experts
-// is only known on the device: a piece is sized for twice an even share of min(E, R) of them.
-struct StreamPlan {
-    bool ok = false;
-    int nq = 0, grid = 0, piece = 0;
-    size_t lds = 0;
-};
-
-template <int FMT, bool SW>
-StreamPlan stream_plan(int rows, int K, int E, int R) {
-    using F = StepFmt<FMT>;
-    constexpr int NW = SW ? 2 : 1;
-    constexpr size_t budget = kMaxLds - kStreamStaticLds;
-    StreamPlan p;
-    const int nblk = K / 32, nchunk = K / F::ce, tpe = (rows + 15) / 16;
-    const int grid = device_info().cu_count;
-    const int64_t share = (static_cast<int64_t>(min(E, R)) * tpe + grid - 1) / grid;
-    for (int nq = 4; nq >= 2; nq -= 2) {
-        const size_t stage = FMT == T_Q4_K ? static_cast<size_t>(nq) * 4 * K
-                                           : static_cast<size_t>(nq) * 2 * nblk * F::tpb * 16;
-        const size_t fixed = stage + static_cast<size_t>(nq) * nblk * sizeof(float);
-        const size_t per_tile = static_cast<size_t>(NW) * nq * nchunk * 16 * sizeof(float);
-        if (fixed + per_tile > budget) continue;
-        const int64_t cap = static_cast<int64_t>((budget - fixed) / per_tile);
-        p.ok = true;
-        p.nq = nq;
-        p.grid = grid;
-        p.piece = static_cast<int>(std::min<int64_t>(cap, std::max<int64_t>(1, 2 * share)));
-        p.lds = fixed + static_cast<size_t>(p.piece) * per_tile;
-        return p;
-    }
-    return p;
-}
-
-// Refuses (rather than dispatches) a launch whose dynamic plus static LDS would exceed the CU's.
+// The static LDS of one streaming-kernel instantiation, as compiled (cost prefix, scan totals,
+// zero operands, step counter), read once; kMaxLds if it cannot be read, so no plan takes it.
 template <int FMT, int NQ, bool SW>
-hipError_t launch_stream_nq(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
-    static const size_t static_lds = [] {
+size_t stream_static_lds() {
+    static const size_t v = [] {
         hipFuncAttributes fa{};
         return hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&stream_kernel<FMT, NQ, SW>)) == hipSuccess
                    ? fa.sharedSizeBytes
                    : kMaxLds;
     }();
-    if (p.lds + static_lds > kMaxLds) return hipErrorInvalidConfiguration;
+    return v;
+}
+
+// A streaming launch: one workgroup per CU, routes per pass, and the tiles whose partials fit in
+// LDS at once (qlin_plan.hpp); not ok when no pass of 2 or 4 routes fits, so the per-element
+// kernels take the call.
+using StreamPlan = plan::Stream;
+
+template <int FMT, bool SW>
+StreamPlan stream_plan(int rows, int K, int E, int R) {
+    using F = StepFmt<FMT>;
+    const plan::StreamFmt f{F::ce, FMT == T_Q4_K, F::tpb};
+    return plan::stream(f, SW, rows, K, E, R, device_info().cu_count, stream_static_lds<FMT, 4, SW>(),
+                        stream_static_lds<FMT, 2, SW>());
+}
+
+template <int FMT, int NQ, bool SW>
+hipError_t launch_stream_nq(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((stream_kernel<FMT, NQ, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
     return hipGetLastError();
 }

@@ -143,6 +143,10 @@ def test_rejections(tmp_path):
     assert _status(p("type")) == FORMAT
     gw.write(p("partial"), META, tensors, dims_override=[300, 32])  # 9600 elements, not whole Q4_K blocks
     assert _status(p("partial")) == FORMAT
+    gw.write(p("rows"), META, tensors, dims_override=[288, 64])    # whole blocks in all, not per row
+    assert _status(p("rows")) == FORMAT
+    gw.write(p("wrap"), META, tensors, dims_override=[1 << 40, 1 << 22], type_override=0)  # 2^64 bytes of F32
+    assert _status(p("wrap")) == FORMAT
     gw.write(p("dims5"), META, tensors, dims_override=[512, 32, 1, 1, 1])
     assert _status(p("dims5")) == FORMAT
     gw.write(p("beyond"), META, tensors, offset_shift=1 << 20)      # data past the end of the file

@@ -106,6 +106,8 @@ GEMV_CASES = [
     (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64), (Q4_0, 17, 256), (Q4_0, 300, 4608),
     (Q5_0, 2048, 1408), (Q5_0, 5, 64), (Q5_0, 300, 4096), (Q5_0, 33, 128), (Q5_0, 100, 18944),
     (Q6_K, 64, 512), (Q6_K, 257, 2048), (Q6_K, 16384, 2048), (Q6_K, 33, 768), (Q6_K, 100, 7168),
+    # K > 8192: the bf16 (not int8) operands, rows of dwords (18944) and of 16-byte units (14336)
+    (Q6_K, 100, 18944), (Q6_K, 64, 14336),
 ]
 
 
@@ -136,7 +138,8 @@ def test_gemv_generic_path_agrees(qtype, out_dim, in_dim):
     assert normwise_rel_err(y_gen, ref) <= FP32
 
 
-@pytest.mark.parametrize("qtype,out_dim,in_dim", [(Q6_K, 300, 2048), (Q6_K, 70, 4096), (Q4_0, 300, 3584),
+@pytest.mark.parametrize("qtype,out_dim,in_dim", [(Q6_K, 300, 2048), (Q6_K, 70, 4096), (Q6_K, 64, 10240),
+                                                  (Q4_0, 300, 3584),
                                                   (Q4_0, 33, 256), (Q8_0, 300, 4096), (Q8_0, 77, 1024)])
 def test_rows_of_16_byte_units_and_offset_base(qtype, out_dim, in_dim):
     """Rows that are whole 16-byte units (Q4_0 always, Q8_0 with an even number of 128-weight chunks,
@@ -234,6 +237,20 @@ def test_gemv_add(qtype):
     qlin.quant_gemv_add(qtype, dev(w), rb, dev(x), yd, 333, in_dim)
     ref = orc.gemv_add(qtype, w, rb, x, y0, 333, in_dim)
     assert normwise_rel_err(host(yd), ref) <= FP32
+
+
+def test_q4k_wide_plans_take_the_vector_streaming_kernel():
+    """[16448, 32768] Q4_K: the matrix-core kernel's LDS plan (x, 128 KB, plus 80 rows x 128 chunk
+    partials) exceeds 160 KB, so the GEMV takes the VALU streaming kernel (qlin_q4k_stream.hip, x
+    staged as f32, partials per 16 chunks).  The weight repeats a random [64, 32768] block, so every
+    row's reference is one of 64 oracle dots."""
+    n_unique, out_dim, in_dim = 64, 16448, 32768
+    w, rb, _ = qgen.random_matrix(Q4_K, n_unique, in_dim, seed=77)
+    x = qgen.random_x(1, in_dim, seed=78)
+    ref = np.tile(orc.matmul_f64(Q4_K, w, rb, x, n_unique, in_dim)[0], out_dim // n_unique)
+    banner(f"gemv vector streaming kernel N={out_dim} K={in_dim}")
+    y = gpu_gemv(Q4_K, np.tile(w, out_dim // n_unique), rb, x, out_dim, in_dim)[0]
+    assert normwise_rel_err(y, ref) <= FP32
 
 
 def test_gemm_facade_derives_row_bytes():
@@ -661,7 +678,8 @@ def test_swiglu_stream(ffn, hid):
 
 
 @pytest.mark.parametrize("qtype,ffn,hid", [(Q4_0, 18944, 3584), (Q8_0, 4864, 896 + 128), (Q8_0, 4864, 896),
-                                          (Q4_0, 9, 256), (Q6_K, 300, 2048), (Q6_K, 17, 768)])
+                                          (Q4_0, 9, 256), (Q6_K, 300, 2048), (Q6_K, 17, 768),
+                                          (Q6_K, 100, 10240), (Q6_K, 64, 9216 + 256)])
 def test_swiglu_matrix_core_formats(qtype, ffn, hid):
     """Fused gate/up SiLU on the 32-weight formats (C2's gate/up pair in one launch) and on Q6_K
     (rows of whole 16-byte units at hid = 2048, of dwords at 768)."""
