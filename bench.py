@@ -285,7 +285,9 @@ def graph_us(torch, qlin, fn, reps):
 
 
 def cpu_threads():
-    return min(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1), 16)
+    """The process's CPU thread share: OMP_NUM_THREADS (16 per GPU job on the GPU boxes), else every
+    CPU it may run on."""
+    return int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or host_cpu()["cpus_allowed"]
 
 
 def cpu_gemv_gbs(torch, qtype, w_dev, rb, n, k, seconds):
@@ -295,16 +297,23 @@ def cpu_gemv_gbs(torch, qtype, w_dev, rb, n, k, seconds):
     threads = cpu_threads()
     w = w_dev.cpu().numpy()
     x = np.random.default_rng(5).standard_normal(k).astype(np.float32)
-    passes, t = 0, 0.0
-    while t < seconds:
-        t0 = time.perf_counter()
-        orc.matmul_f32(qtype, w, rb, x, n, k, threads)
-        t += time.perf_counter() - t0
-        passes += 1
     nbytes = n * rb + 4 * (n + k)
-    return {"value": round(nbytes * passes / t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+
+    def timed(nthreads, budget):
+        passes, t = 0, 0.0
+        while t < budget or passes == 0:
+            t0 = time.perf_counter()
+            orc.matmul_f32(qtype, w, rb, x, n, k, nthreads)
+            t += time.perf_counter() - t0
+            passes += 1
+        return nbytes * passes / t / 1e9, passes, t
+
+    gbs, passes, t = timed(threads, seconds)
+    gbs1, p1, t1 = timed(1, seconds / 2)
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"[{n}, {k}] type {qtype} GEMV ({nbytes / 1e6:.1f} MB) x {passes} passes, {t:.1f} s; "
-                      f"oracle orc_matmul_f32 (OpenMP over rows)"}
+                      f"oracle orc_matmul_f32 (OpenMP over rows)",
+            "one_thread_gbs": round(gbs1, 3), "one_thread_sample": f"{p1} passes, {t1:.1f} s", **host_cpu()}
 
 
 def gemv_config(args, torch, qlin, gen, workload, metric, qtype, shapes, copies):
@@ -363,72 +372,140 @@ def wl_q6k(args, torch, qlin, gen):
 
 
 def wl_c3(args, torch, qlin, gen):
-    """C3: the quantized-linear work of one decode token of a Qwen2.5-0.5B-architecture model in Q8_0
-    (24 layers of q/k/v, o, gate/up + SiLU, down, then the lm_head): 97 launches, as the default
-    workload does for Qwen2-7B.  Attention, norms and RoPE are outside this path."""
-    L, H, KVD, F, V = 24, 896, 128, 4864, 151936
+    """C3: greedy decoding of a random-init Qwen2.5-0.5B-architecture model with every linear in Q8_0
+    (blog_amd/decoder.py): a 32-token uniform prompt in one batched pass, then 128 greedy tokens, one
+    decode step per token (RMSNorm, q/k/v, rotary + KV store, attention, o, RMSNorm, gate/up SwiGLU,
+    down, for 24 layers; final norm, tied Q8_0 head, argmax).  Prefill and decode step are each one
+    captured HIP graph; the decode graph reads its token and position from device memory, so 127
+    replays after the prefill are the whole generation.  The linear launches alone are timed too."""
+    from blog_amd.decoder import Qwen2Config, Qwen2Decoder, make_weights
+    cfg = Qwen2Config()
+    L, H, KVD, F, V = cfg.layers, cfg.hidden, cfg.kv_dim, cfg.ffn, cfg.vocab
+    P, NEW = 32, 128
+    log("c3: random-init Q8_0 weights")
+    w = make_weights(torch, cfg, seed=2024)
+    dec = Qwen2Decoder(torch, cfg, w, max_seq=P + NEW, max_prompt=P)
+    prompt = torch.randint(0, V, (P,), dtype=torch.int32, device="cuda", generator=gen)
+
+    def capture(fn):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    g_pre = capture(lambda: dec.prefill(prompt))
+    g_step = capture(dec.step)
+
+    def generation():
+        g_pre.replay()
+        for _ in range(NEW - 1):
+            g_step.replay()
+
+    for _ in range(2):
+        generation()
+    torch.cuda.synchronize()
+    reps = max(2, args.steps // 20)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        generation()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / reps
+    gen_ms = e0.elapsed_time(e1) / reps
+    us_pre = graph_replay_us(torch, g_pre, reps)
+    us_step = graph_replay_us(torch, g_step, 4 * reps)
+    # the quantized linears of one decode step alone (97 launches), and the gate/up SwiGLU launches
     rb_h, rb_f = qlin.row_bytes(Q8_0, H), qlin.row_bytes(Q8_0, F)
-    shapes = [("q", H, H), ("k", KVD, H), ("v", KVD, H), ("o", H, H), ("gate", F, H), ("up", F, H), ("down", H, F)]
-    layers = [{nm: synth_blocks(torch, Q8_0, n, k, gen) for nm, n, k in shapes} for _ in range(L)]
-    lm_head = synth_blocks(torch, Q8_0, V, H, gen)
-    x_h, x_f = torch.randn(H, device="cuda", generator=gen), torch.randn(F, device="cuda", generator=gen)
-    y = {nm: torch.empty(n, device="cuda") for nm, n, _ in shapes}
-    act, logits = torch.empty(F, device="cuda"), torch.empty(V, device="cuda")
+    x_h, act = dec.xn[0], dec.act[0]
+    yq, yk, yv, yo, logits = (torch.empty(n, device="cuda") for n in (H, KVD, KVD, H, V))
 
-    def step():
-        for Lw in layers:
-            qlin.quant_gemv_multi(Q8_0, [Lw["q"], Lw["k"], Lw["v"]], rb_h, x_h, [y["q"], y["k"], y["v"]], [H, KVD, KVD], H)
-            qlin.quant_gemv(Q8_0, Lw["o"], rb_h, x_h, y["o"], H, H, 1)
-            qlin.quant_swiglu(Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, x_h, act, F, H)
-            qlin.quant_gemv(Q8_0, Lw["down"], rb_f, act, y["down"], H, F, 1)
-        qlin.quant_gemv(Q8_0, lm_head, rb_h, x_h, logits, V, H, 1)
+    def linears():
+        for W in w["layers"]:
+            qlin.quant_gemv_multi(Q8_0, [W["wq"], W["wk"], W["wv"]], rb_h, x_h, [yq, yk, yv], [H, KVD, KVD], H)
+            qlin.quant_gemv(Q8_0, W["wo"], rb_h, x_h, yo, H, H, 1)
+            qlin.quant_swiglu(Q8_0, W["wg"], W["wu"], rb_h, rb_h, x_h, act, F, H)
+            qlin.quant_gemv(Q8_0, W["wd"], rb_f, act, yo, H, F, 1)
+        qlin.quant_gemv(Q8_0, w["table"], rb_h, x_h, logits, V, H, 1)
 
-    per_layer = ((H + 2 * KVD) * rb_h + 4 * (H + H + 2 * KVD) + H * rb_h + 8 * H
-                 + 2 * F * rb_h + 4 * (H + F) + H * rb_f + 4 * (F + H))
-    nbytes = L * per_layer + V * rb_h + 4 * (H + V)
-    reps = max(1, args.steps // 4)
-    us = graph_us(torch, qlin, step, reps)
-    # the launches that take the most time together: the 24 gate/up SwiGLU launches
-    us_sw = graph_us(torch, qlin, lambda: [qlin.quant_swiglu(Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, x_h, act, F, H)
-                                           for Lw in layers], reps) / L
+    us_lin = graph_us(torch, qlin, linears, reps)
+    us_sw = graph_us(torch, qlin, lambda: [qlin.quant_swiglu(Q8_0, W["wg"], W["wu"], rb_h, rb_h, x_h, act, F, H)
+                                           for W in w["layers"]], reps) / L
     sw_bytes = 2 * F * rb_h + 4 * (H + F)
-    # the 32-token prompt: every linear over 32 rows (f32 matrix-core matmul, batched SwiGLU), then
-    # the lm_head for the last row, whose logits start the greedy decode
-    P = 32
-    xp_h, xp_f = torch.randn(P, H, device="cuda", generator=gen), torch.randn(P, F, device="cuda", generator=gen)
-    yp = {nm: torch.empty(P, n, device="cuda") for nm, n, _ in shapes}
-    actp = torch.empty(P, F, device="cuda")
-
-    def prefill():
-        for Lw in layers:
-            for nm, n in (("q", H), ("k", KVD), ("v", KVD), ("o", H)):
-                qlin.quant_matmul(Q8_0, Lw[nm], rb_h, xp_h, yp[nm], n, H, P)
-            qlin.call("qlin_launch_quant_swiglu_rows", Q8_0, Lw["gate"], Lw["up"], rb_h, rb_h, xp_h, actp, F, H, P)
-            qlin.quant_matmul(Q8_0, Lw["down"], rb_f, xp_f, yp["down"], H, F, P)
-        qlin.quant_gemv(Q8_0, lm_head, rb_h, xp_h[P - 1], logits, V, H, 1)
-
-    us_pre = graph_us(torch, qlin, prefill, max(1, reps // 4))
-    log(f"c3: {us:.2f} us/token ({1e6 / us:.0f} tok/s), gate/up SwiGLU {us_sw:.2f} us/launch, "
-        f"32-token prefill {us_pre:.1f} us")
+    lin_bytes = L * ((H + 2 * KVD) * rb_h + H * rb_h + 2 * F * rb_h + H * rb_f + 4 * (3 * H + 2 * KVD + 3 * F + 2 * H)) \
+        + V * rb_h + 4 * (H + V)
+    log(f"c3: {gen_ms:.2f} ms per generation (32-token prompt {us_pre:.0f} us + 127 steps of {us_step:.1f} us), "
+        f"{1e6 / us_step:.0f} decode tok/s; linears alone {us_lin:.1f} us/token, SwiGLU {us_sw:.2f} us")
     result = {
-        "metric": "decode GEMV HBM GB/s + tokens/s, Qwen2.5-0.5B-arch Q8_0 linear work per token, 1 GPU",
-        "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
-        "tokens_per_s": round(1e6 / us, 1), "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (random Q8_0 blocks, f32 N(0,1) activations)",
-        "config": {"workload": "c3-q8_0-decode-token", "layers": L, "hidden": H, "ffn": F, "kv_dim": KVD, "vocab": V,
-                   "weight_format": "Q8_0", "batch": 1, "launches_per_step": 4 * L + 1,
-                   "algorithmic_bytes_per_step": nbytes, "execution": "hip graph replay",
-                   "prefill_32_tokens_us": round(us_pre, 2),
-                   "prompt_32_plus_128_tokens_ms": round((us_pre + 128 * us) / 1e3, 3)},
+        "metric": "greedy decode tokens/s, Qwen2.5-0.5B-arch Q8_0 (32-token prompt + 128 tokens), 1 GPU",
+        "value": round(1e6 / us_step, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": 2,
+        "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (Q8_0 weights)",
+        "data": "synthetic (random-init N(0, 0.02) weights quantized to Q8_0; uniform random prompt ids)",
+        "config": {"workload": "c3-q8_0-decode-token", "layers": L, "hidden": H, "heads": cfg.n_heads,
+                   "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "ffn": F, "vocab": V, "weight_format": "Q8_0",
+                   "prompt_tokens": P, "new_tokens": NEW, "execution": "hip graph replay (prefill graph + step graph)",
+                   "generation_ms": round(gen_ms, 3), "generation_wall_ms": round(wall * 1e3, 3),
+                   "prefill_us": round(us_pre, 1), "decode_step_us": round(us_step, 2),
+                   "decode_step_hbm_gbs": round(lin_bytes / us_step / 1e3, 1),
+                   "linear_only_us_per_token": round(us_lin, 2),
+                   "linear_only_tokens_per_s": round(1e6 / us_lin, 1),
+                   "linear_algorithmic_bytes_per_token": lin_bytes},
         "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": "mfma_gemv_kernel<8, true, *, *> (Q8_0 gate/up SwiGLU, 2 x [4864, 896])",
                      "avg_launch_us": round(us_sw, 3), "algorithmic_bytes_per_launch": sw_bytes},
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_gemv_gbs(torch, Q8_0, layers[0]["gate"], rb_h, F, H, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_decoder_tps(torch, cfg, w, prompt, args.cpu_seconds)
     return result
+
+
+def cpu_decoder_tps(torch, cfg, w, prompt, seconds):
+    """The oracle's decoder twin (double precision, OpenMP over each matrix's rows) on this host: the
+    prompt, then as many new positions as about `seconds` allow, timed per new position."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    def bf16_values(t):
+        return (t.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+    layers = [{n: L[n].cpu().numpy() for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")} |
+              {"attn_norm": bf16_values(L["attn_norm"]), "ffn_norm": bf16_values(L["ffn_norm"])} for L in w["layers"]]
+    c = dict(layers=cfg.layers, hidden=cfg.hidden, n_heads=cfg.n_heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+             ffn=cfg.ffn, vocab=cfg.vocab, wtype=cfg.wtype, eps=cfg.eps, theta=cfg.theta)
+    final, table = bf16_values(w["final_norm"]), w["table"].cpu().numpy()
+    threads = cpu_threads()
+    toks = prompt.cpu().numpy().tolist()
+    P = len(toks)
+    # one timed pass with 2 new positions, then one sized to the budget
+    t0 = time.perf_counter()
+    orc.qwen2_logits(c, layers, final, table, toks + [1, 2], first=P, threads=threads)
+    t_small = time.perf_counter() - t0
+    n_new = max(2, min(64, int(2 * seconds / max(t_small, 1e-3))))
+    t0 = time.perf_counter()
+    orc.qwen2_logits(c, layers, final, table, toks + list(range(1, n_new + 1)), first=P, threads=threads)
+    t = time.perf_counter() - t0
+    per_new = (t - t_small) / (n_new - 2) if n_new > 2 else t / (P + n_new)
+    return {"value": round(1.0 / per_new, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle orc_qwen2_logits (double precision, OpenMP over rows): the 32-token prompt plus "
+                      f"{n_new} new positions in {t:.1f} s against 2 in {t_small:.1f} s; the difference per position"}
+
+
+def graph_replay_us(torch, g, reps):
+    """Average microseconds of one replay of a captured graph."""
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
 
 
 def wl_c4(args, torch, qlin, gen):
@@ -539,7 +616,7 @@ def wl_c5(args, torch, qlin, gen):
     shared = 2 * sffn * s_rb + hid * sd_rb
     nbytes = distinct * per_expert + shared + 4 * tokens * (hid + hid) + 4 * tokens * E
     log(f"c5: grouped {us:.2f} us/step, per-token facade {us_tok:.2f} us, {distinct} distinct experts")
-    return {
+    result = {
         "metric": "MoE layer decode HBM GB/s (DeepSeek-V2-Lite shape, 16 tokens, top-6 of 64 + 2 shared)",
         "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
         "n_gpus": 1, "steps": reps * copies, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
@@ -557,6 +634,35 @@ def wl_c5(args, torch, qlin, gen):
                                "stream_kernel<Q5_0> down, combine_kernel, q4k_dense_kernel SwiGLU and add)",
                      "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": nbytes},
     }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_moe_gbs(torch, mats[0], x, ids, rw, E, ffn, hid, k, args.cpu_seconds)
+    return result
+
+
+def cpu_moe_gbs(torch, mats, x, ids, rw, E, ffn, hid, k, seconds):
+    """The oracle's per-token routed MoE (orc_swiglu_indexed, then orc_down_indexed_ordered; one thread,
+    double-precision sums) over the batch's tokens for about `seconds`: GB/s of the expert bytes that
+    each token's routes read."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    wg, wu, wd = (t.cpu().numpy() for t in mats[:3])
+    geb, deb = wg.size // E, wd.size // E
+    grb, drb = geb // ffn, deb // hid
+    xs, idh, rwh = x.cpu().numpy(), ids.cpu().numpy(), rw.cpu().numpy()
+    per_token = k * (2 * geb + deb)
+    tokens, t = 0, 0.0
+    out = np.zeros(hid, np.float32)
+    while t < seconds or tokens == 0:
+        i = tokens % xs.shape[0]
+        t0 = time.perf_counter()
+        act = orc.swiglu_indexed(Q4_K, wg, wu, geb, geb, grb, grb, xs[i], idh[i], ffn, hid)
+        orc.down_indexed_ordered(6, wd, deb, drb, act, idh[i], rwh[i], out, hid, ffn)
+        t += time.perf_counter() - t0
+        tokens += 1
+    return {"value": round(per_token * tokens / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "tokens_per_s": round(tokens / t, 2),
+            "sample": f"{tokens} tokens' routed experts ({per_token / 1e6:.1f} MB each), {t:.1f} s; oracle "
+                      f"orc_swiglu_indexed + orc_down_indexed_ordered (one thread)", **host_cpu()}
 
 
 def wl_moe_token(args, torch, qlin, gen):
@@ -611,7 +717,7 @@ def wl_moe_token(args, torch, qlin, gen):
     nbytes = sw_bytes + dn_bytes + 4 * E
     log(f"moe token: {us:.2f} us/token (router + routed decode), SwiGLU {us_sw:.2f} us, down {us_dn:.2f} us, "
         f"{distinct} distinct experts per token at least")
-    return {
+    result = {
         "metric": "per-token routed MoE decode HBM GB/s (DeepSeek-V2-Lite shape, top-6 of 64, 1 token)",
         "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
         "n_gpus": 1, "steps": reps * copies, "warmup": 3, "ms_per_step": round(us / 1e3, 5),
@@ -626,6 +732,10 @@ def wl_moe_token(args, torch, qlin, gen):
                      "kernel": "mfma_gemv_kernel<12, true, 1, false, true> (routed gate/up SwiGLU, 6 x 2 x [1408, 2048])",
                      "avg_launch_us": round(us_sw, 3), "algorithmic_bytes_per_launch": sw_bytes},
     }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_moe_gbs(torch, mats[0], x.view(1, hid), ids[0:1], rw[0:1], E, ffn, hid, k,
+                                             args.cpu_seconds)
+    return result
 
 
 WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
@@ -633,12 +743,33 @@ WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_
              "deepseek-moe-token": wl_moe_token}
 
 
+def host_cpu() -> dict:
+    """The host's CPU model, its logical CPU count, and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count() or 1, "cpus_allowed": allowed}
+
+
 def cpu_baseline(torch, layer, shapes, xin, outs, seconds, bytes_per_step):
-    """The oracle's f32 GEMV (OpenMP over rows) on this host, over layer 0's seven matrices."""
+    """The oracle's GEMV on this host over layer 0's seven matrices: the f32 variant (OpenMP over rows)
+    on one thread and on the process's thread share (OMP_NUM_THREADS, else every allowed CPU; the GPU
+    boxes give one GPU's job 16), and the double-precision variant on one thread, each for a bounded
+    time.  value is the f32 figure on the thread share."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    threads = min(threads, 16)
+    info = host_cpu()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or info["cpus_allowed"]
     mats = []
     for name, n, k in shapes:
         w = layer[name].cpu().numpy()
@@ -655,24 +786,33 @@ def cpu_baseline(torch, layer, shapes, xin, outs, seconds, bytes_per_step):
         gpu_y[name] = y
     torch.cuda.synchronize()
     layer_bytes = sum(w.size + 4 * k + 4 * n for _, w, _, _, n, k in mats)
-    log(f"cpu baseline: oracle f32 GEMV, {threads} threads, ~{seconds:.0f} s")
+
+    def timed(fn, budget):
+        passes, t_total = 0, 0.0
+        while t_total < budget or passes == 0:
+            for name, w, rb, x, n, k in mats:
+                t0 = time.perf_counter()
+                fn(w, rb, x, n, k)
+                t_total += time.perf_counter() - t0
+            passes += 1
+        return layer_bytes * passes / t_total / 1e9, passes, t_total
+
+    log(f"cpu baseline: oracle f32 GEMV, {threads} threads and 1 thread, f64 on 1 thread ({info['cpu_model']})")
     worst = 0.0
-    passes, t_total = 0, 0.0
-    while t_total < seconds:
-        for name, w, rb, x, n, k in mats:
-            t0 = time.perf_counter()
-            y = orc.matmul_f32(Q4_K, w, rb, x, n, k, threads)
-            t_total += time.perf_counter() - t0
-            if passes == 0:
-                g = gpu_y[name].cpu().numpy().astype(np.float64)
-                worst = max(worst, float(np.max(np.abs(g - y[0])) / np.max(np.abs(y[0]))))
-        passes += 1
-    gbs = layer_bytes * passes / t_total / 1e9
+    for name, w, rb, x, n, k in mats:
+        y = orc.matmul_f32(Q4_K, w, rb, x, n, k, threads)
+        g = gpu_y[name].cpu().numpy().astype(np.float64)
+        worst = max(worst, float(np.max(np.abs(g - y[0])) / np.max(np.abs(y[0]))))
+    gbs, passes, t_total = timed(lambda w, rb, x, n, k: orc.matmul_f32(Q4_K, w, rb, x, n, k, threads), seconds)
+    gbs1, p1, t1 = timed(lambda w, rb, x, n, k: orc.matmul_f32(Q4_K, w, rb, x, n, k, 1), seconds / 2)
+    gbs64, p64, t64 = timed(lambda w, rb, x, n, k: orc.matmul_f64(Q4_K, w, rb, x, n, k), seconds / 2)
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "tokens_per_s": round(gbs * 1e9 / bytes_per_step, 3),
             "sample": f"layer-0 q,k,v,o,gate,up,down Q4_K GEMVs ({layer_bytes / 1e6:.1f} MB) x {passes} passes, "
                       f"{t_total:.1f} s; oracle orc_matmul_f32 (OpenMP over rows)",
-            "gpu_vs_cpu_max_rel_diff": worst}
+            "one_thread_gbs": round(gbs1, 3), "one_thread_sample": f"{p1} passes, {t1:.1f} s",
+            "f64_one_thread_gbs": round(gbs64, 3), "f64_sample": f"orc_matmul_f64, {p64} passes, {t64:.1f} s",
+            **info, "gpu_vs_cpu_max_rel_diff": worst}
 
 
 if __name__ == "__main__":

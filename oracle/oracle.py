@@ -67,6 +67,7 @@ def _declare(L: C.CDLL) -> None:
         "orc_swiglu_indexed": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
         "orc_down_indexed_ordered": (I, [I, P, SZ, SZ, P, P, P, P, I, I, I]),
         "orc_argmax": (I, [P, I]),
+        "orc_qwen2_logits": (I, [P, P, P, P, P, I, I, P, I]),
         "orc_quant_embedding": (I, [I, P, I, P, SZ, I, P]),
         "orc_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
         "orc_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),
@@ -229,6 +230,46 @@ def down_indexed_ordered(qtype, wd, d_eb, d_rb, act, expert_ids, route_w, out, h
     out = np.array(out, dtype=np.float32, copy=True)
     _ok(lib().orc_down_indexed_ordered(qtype, _p(wd), d_eb, d_rb, _p(act), _p(ids), _p(rw), _p(out),
                                        ids.size, hidden, ffn_dim), "down_indexed_ordered")
+    return out
+
+
+class Qwen2Cfg(C.Structure):
+    """orc_qwen2_cfg (qlin_oracle.h)."""
+    _fields_ = [("layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int), ("kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("wtype", C.c_int),
+                ("eps", C.c_double), ("theta", C.c_double)]
+
+
+class Qwen2Layer(C.Structure):
+    """orc_qwen2_layer (qlin_oracle.h)."""
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "attn_norm", "ffn_norm")]
+
+
+def qwen2_logits(cfg: dict, layers: list, final_norm: np.ndarray, table: np.ndarray, tokens, first: int,
+                 threads: int = 0) -> np.ndarray:
+    """The decoder twin: logits [len(tokens) - first, vocab] of positions first.., teacher-forced.
+
+    cfg: layers, hidden, n_heads, kv_heads, head_dim, ffn, vocab, wtype, eps, theta; layers: dicts of
+    numpy arrays wq, wk, wv, wo, wg, wu, wd (packed bytes) and attn_norm, ffn_norm (float32)."""
+    c = Qwen2Cfg(**cfg)
+    keep = []
+
+    def ptr(a, dtype):
+        a = np.ascontiguousarray(a, dtype=dtype)
+        keep.append(a)
+        return a.ctypes.data
+
+    arr = (Qwen2Layer * len(layers))()
+    for i, L in enumerate(layers):
+        for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
+            setattr(arr[i], n, ptr(L[n], np.uint8))
+        arr[i].attn_norm = ptr(L["attn_norm"], np.float32)
+        arr[i].ffn_norm = ptr(L["ffn_norm"], np.float32)
+    toks = np.ascontiguousarray(tokens, np.int32)
+    out = np.empty((len(toks) - first, cfg["vocab"]), np.float32)
+    threads = threads or (os.cpu_count() or 1)
+    _ok(lib().orc_qwen2_logits(C.byref(c), arr, ptr(final_norm, np.float32), ptr(table, np.uint8), _p(toks),
+                               len(toks), first, _p(out), threads), "orc_qwen2_logits")
     return out
 
 

@@ -856,3 +856,116 @@ int orc_argmax(const float *v, int n) {
         if (v[i] > best) { best = v[i]; idx = i; }
     return idx;
 }
+
+/* ---- the config-3 decoder twin (see orc_qwen2_logits in qlin_oracle.h) ---------------------- */
+
+/* y[o] = sum_k w(o, k) x[k] in double, rows over `threads` threads (scratch: one dequantized row each) */
+static int matvec_d(int type, const uint8_t *w, int out_dim, int in_dim, const double *x, double *y, int threads) {
+    const size_t rb = (size_t)(in_dim / orc_block_elems(type)) * (size_t)orc_block_bytes(type);
+    int bad = 0;
+#pragma omp parallel num_threads(threads)
+    {
+        float *s = (float *)malloc(sizeof(float) * (size_t)in_dim);
+        if (!s) {
+#pragma omp atomic write
+            bad = 1;
+        } else {
+#pragma omp for schedule(static)
+            for (int o = 0; o < out_dim; ++o) {
+                deq_row(type, w + (size_t)o * rb, in_dim, s);
+                double acc = 0.0;
+                for (int k = 0; k < in_dim; ++k) acc += (double)s[k] * x[k];
+                y[o] = acc;
+            }
+            free(s);
+        }
+    }
+    return bad ? -1 : 0;
+}
+
+/* kernel.cu:112-150: x * rsqrt(mean(x^2) + eps) * w */
+static void rms_norm_d(const double *x, const float *w, int n, double eps, double *y) {
+    double ss = 0.0;
+    for (int j = 0; j < n; ++j) ss += x[j] * x[j];
+    const double inv = 1.0 / sqrt(ss / n + eps);
+    for (int j = 0; j < n; ++j) y[j] = x[j] * inv * (double)w[j];
+}
+
+/* kernel.cu:186-226: pairs (i, i + d/2) rotated by pos / theta^(2i / d) */
+static void rope_d(double *v, int d, int pos, double theta) {
+    const int half = d / 2;
+    for (int i = 0; i < half; ++i) {
+        const double ang = (double)pos / pow(theta, (double)(2 * i) / (double)d);
+        const double c = cos(ang), sn = sin(ang), a = v[i], b = v[i + half];
+        v[i] = a * c - b * sn;
+        v[i + half] = b * c + a * sn;
+    }
+}
+
+int orc_qwen2_logits(const orc_qwen2_cfg *c, const orc_qwen2_layer *layers, const float *final_norm,
+                     const uint8_t *table, const int *tokens, int n, int first, float *logits, int threads) {
+    const int H = c->hidden, NH = c->n_heads, NKV = c->kv_heads, D = c->head_dim, F = c->ffn, V = c->vocab;
+    const int QD = NH * D, KD = NKV * D, group = NH / NKV;
+    if (n <= 0 || first < 0 || first >= n || NH % NKV || check_shape(c->wtype, H) || check_shape(c->wtype, F))
+        return -1;
+    const size_t trb = (size_t)(H / orc_block_elems(c->wtype)) * (size_t)orc_block_bytes(c->wtype);
+    double *kc = (double *)malloc(sizeof(double) * (size_t)c->layers * n * KD);
+    double *vc = (double *)malloc(sizeof(double) * (size_t)c->layers * n * KD);
+    double *h = (double *)malloc(sizeof(double) * H), *xn = (double *)malloc(sizeof(double) * H);
+    double *q = (double *)malloc(sizeof(double) * QD), *k = (double *)malloc(sizeof(double) * KD);
+    double *v = (double *)malloc(sizeof(double) * KD), *att = (double *)malloc(sizeof(double) * QD);
+    double *o = (double *)malloc(sizeof(double) * (H > F ? H : F)), *g = (double *)malloc(sizeof(double) * F);
+    double *u = (double *)malloc(sizeof(double) * F), *p = (double *)malloc(sizeof(double) * n);
+    double *lg = (double *)malloc(sizeof(double) * V);
+    float *row = (float *)malloc(sizeof(float) * H);
+    int rc = 0;
+    if (!kc || !vc || !h || !xn || !q || !k || !v || !att || !o || !g || !u || !p || !lg || !row) rc = -1;
+    for (int pos = 0; pos < n && rc == 0; ++pos) {
+        deq_row(c->wtype, table + (size_t)tokens[pos] * trb, H, row); /* the embedding row */
+        for (int j = 0; j < H; ++j) h[j] = row[j];
+        for (int l = 0; l < c->layers && rc == 0; ++l) {
+            const orc_qwen2_layer *L = layers + l;
+            double *kl = kc + (size_t)l * n * KD, *vl = vc + (size_t)l * n * KD;
+            rms_norm_d(h, L->attn_norm, H, c->eps, xn);
+            rc |= matvec_d(c->wtype, L->wq, QD, H, xn, q, threads);
+            rc |= matvec_d(c->wtype, L->wk, KD, H, xn, k, threads);
+            rc |= matvec_d(c->wtype, L->wv, KD, H, xn, v, threads);
+            for (int hh = 0; hh < NH; ++hh) rope_d(q + (size_t)hh * D, D, pos, c->theta);
+            for (int hh = 0; hh < NKV; ++hh) rope_d(k + (size_t)hh * D, D, pos, c->theta);
+            memcpy(kl + (size_t)pos * KD, k, sizeof(double) * KD);
+            memcpy(vl + (size_t)pos * KD, v, sizeof(double) * KD);
+            for (int hh = 0; hh < NH; ++hh) { /* kernel.cu:345-420, without the output gate */
+                const int kh = hh / group;
+                double mx = -INFINITY, den = 0.0;
+                for (int t = 0; t <= pos; ++t) {
+                    double s = 0.0;
+                    for (int d = 0; d < D; ++d) s += q[(size_t)hh * D + d] * kl[(size_t)t * KD + (size_t)kh * D + d];
+                    p[t] = s / sqrt((double)D);
+                    if (p[t] > mx) mx = p[t];
+                }
+                for (int t = 0; t <= pos; ++t) { p[t] = exp(p[t] - mx); den += p[t]; }
+                for (int d = 0; d < D; ++d) {
+                    double acc = 0.0;
+                    for (int t = 0; t <= pos; ++t) acc += p[t] * vl[(size_t)t * KD + (size_t)kh * D + d];
+                    att[(size_t)hh * D + d] = acc / den;
+                }
+            }
+            rc |= matvec_d(c->wtype, L->wo, H, QD, att, o, threads);
+            for (int j = 0; j < H; ++j) h[j] += o[j];
+            rms_norm_d(h, L->ffn_norm, H, c->eps, xn);
+            rc |= matvec_d(c->wtype, L->wg, F, H, xn, g, threads);
+            rc |= matvec_d(c->wtype, L->wu, F, H, xn, u, threads);
+            for (int j = 0; j < F; ++j) g[j] = g[j] / (1.0 + exp(-g[j])) * u[j]; /* kernel.cu:1289-1328 */
+            rc |= matvec_d(c->wtype, L->wd, H, F, g, o, threads);
+            for (int j = 0; j < H; ++j) h[j] += o[j];
+        }
+        if (rc == 0 && pos >= first) {
+            rms_norm_d(h, final_norm, H, c->eps, xn);
+            rc |= matvec_d(c->wtype, table, V, H, xn, lg, threads);
+            for (int j = 0; j < V; ++j) logits[(size_t)(pos - first) * V + j] = (float)lg[j];
+        }
+    }
+    free(kc); free(vc); free(h); free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u);
+    free(p); free(lg); free(row);
+    return rc;
+}

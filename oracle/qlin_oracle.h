@@ -190,6 +190,26 @@ int orc_mla_project_v(int type, const uint8_t *w, size_t row_bytes, const uint8_
 int orc_mla_absorb_context_v(const float *scores, const float *kv_b_cache, double *attn, int n_heads, int qk_nope,
                              int v_head, int pos, int max_seq);
 
+/* The CPU twin of the config-3 decoder harness (blog_amd/decoder.py): a Qwen2-architecture decoder
+ * with quantized linears, restating the layer's glue from the reference (kernel.cu:112-150 RMSNorm,
+ * 186-226 rotary pairs (i, i + d/2), 345-420 causal GQA attention; SwiGLU as quant_swiglu, 1289-1328)
+ * and the Qwen2 layer order: x -> RMSNorm -> q, k, v -> rotary -> attention -> o added to the
+ * residual -> RMSNorm -> SiLU(gate) * up -> down added to the residual; then the final RMSNorm and the
+ * tied embedding table as the output head.  No q/k/v biases.  Every sum and the whole hidden state
+ * in double.  tokens[0..n) are processed at positions 0..n-1 (teacher forcing); the logits of
+ * positions first..n-1 are written to logits [(n - first) * vocab].  Linears and the table share the
+ * type `wtype`; norm weights are f32 values.  `threads` OpenMP threads share each matrix's rows. */
+typedef struct {
+    int layers, hidden, n_heads, kv_heads, head_dim, ffn, vocab, wtype;
+    double eps, theta;
+} orc_qwen2_cfg;
+typedef struct {
+    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd; /* [out, in] rows, in = hidden (wd: ffn) */
+    const float *attn_norm, *ffn_norm;                /* [hidden] */
+} orc_qwen2_layer;
+int orc_qwen2_logits(const orc_qwen2_cfg *cfg, const orc_qwen2_layer *layers, const float *final_norm,
+                     const uint8_t *table, const int *tokens, int n, int first, float *logits, int threads);
+
 #ifdef __cplusplus
 }
 #endif
