@@ -523,7 +523,7 @@ def wl_c4(args, torch, qlin, gen):
             qlin.quantize_q8_1(x, xq, K, M)
             qlin.quant_matmul_q8_1(Q4_K, w, rb, xq, y, N, K, M)
 
-    reps = max(1, args.steps // 20)
+    reps = max(10, args.steps // 2)  # one replay is 2 launches of ~150 us: time enough of them
     us_step = graph_us(torch, qlin, step_all, reps) / len(ws)
     us_gemm = graph_us(torch, qlin, lambda: [qlin.quant_matmul_q8_1(Q4_K, w, rb, xq, y, N, K, M) for w in ws],
                        reps) / len(ws)
@@ -533,7 +533,7 @@ def wl_c4(args, torch, qlin, gen):
         "metric": "Q4_K x Q8_1 prefill GEMM TFLOP/s (M=512, K=4096, N=14336)",
         "value": round(flops / us_step / 1e6, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps * len(ws),
         "warmup": 3, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f16 (exact hi/lo split of Q8_1 values) x f16 (sc*q), f32 accumulate",
+        "vs_baseline": None, "dtype": "f16 (Q8_1 integers qx) x f16 (integers sc*q), f32 block sums scaled by d8",
         "data": "synthetic (random Q4_K blocks; activations f16-rounded N(0,1) quantized to Q8_1 in the step)",
         "config": {"workload": "c4-q4k-prefill-gemm", "m": M, "k": K, "n": N, "weight_format": "Q4_K",
                    "activation_format": "Q8_1", "algorithmic_flops_per_step": flops,

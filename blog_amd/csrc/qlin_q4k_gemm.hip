@@ -5,21 +5,28 @@
 // reference quant_matmul_q8_1_kernel for Q4_K, AI/codes/local-llm/src/backend/cuda/ops/kernel.cu:
 // 2305-2345), for m tokens of Q8_1 activations (d8 f16 | s8 f16 | int8 q[32] per 32 values).
 //
-// The products are exact on v_mfma_f32_16x16x32_f16 (up to the 2^-22 rounding of lo):
-//   A (activations): d8*qx needs at most 18 significant bits (11 of d8, 7 of q), so it is split
-//     into two fp16 halves, hi (its top 11 bits) and lo (the rest, rounded to fp16: 2^-22 of the
-//     value), and both are multiplied.
+// The block dot is taken as the reference takes it, in integers, on v_mfma_f32_16x16x32_f16:
+//   A (activations): qx, an integer of at most 8 bits, exact in fp16 (bytes (q ^ 0x80, 0x64) are the
+//     fp16 1152 + q; one packed subtraction leaves q).
 //   B (weights): sc_j*qw is an integer <= 63*15 = 945, exact in fp16.  A nibble becomes fp16 1024+q
 //     by one v_perm_b32 per two weights (bytes (q, 0x64)); one v_pk_fma_f16 per two weights then
 //     gives (1024+q)*sc - 1024*sc = q*sc, exact because the result is representable.
-// So one super-block's MFMAs sum sum_j sc_j * sum_i (d8_j qx)(qw) in f32, and d is applied once
-// per super-block instead of once per 32-block.  The min term sum_j m_j*s8_j (m_j <= 63 and s8 an
-// f16, both exact) is one more MFMA per tile, scaled by dmin.
+// One MFMA per 32-block and 16 x 16 tile gives sum_i sc_j*qw*qx exactly in f32 (|sum| < 2^22); d8_j
+// is applied to it by one fma per output element, and d once per super-block.  The min term
+// sum_j m_j*s8_j (m_j <= 63 and s8 an f16, both exact) is one more MFMA per tile, scaled by dmin.
+//
+// Two other forms measured slower.  Splitting d8*qx into fp16 hi and lo parts moves d8 into the A
+// operand (no per-block fma) but doubles the MFMAs, and its operands, full fp16 mantissas, draw
+// the matrix cores' power limit (150 us against 144 us here on the C4 shape).  The int8 MFMA on the
+// raw bytes and nibbles needs sc and d8 applied to each int32 block result, three VALU per element
+// and block (162 us).
 //
 // Tiling.  A workgroup of 8 waves computes 64 tokens x 256 weight rows; each wave owns 32 rows (two
-// 16-row tiles) for all 64 tokens (four 16-token tiles).  Per super-block the workgroup converts
-// its 64 x 256 activations once into the A-operand layout in LDS (hi and lo planes, 64 KB), and
-// each wave decodes its own weight rows straight from global memory into B operands.
+// 16-row tiles) for all 64 tokens (four 16-token tiles).  Per super-block the workgroup stages its
+// 64 x 256 activations once into the A-operand layout in LDS, and each wave decodes its own weight
+// rows straight from global memory into B operands.  The weights live in one register set whose
+// parts are reloaded with the next super-block as soon as they are decoded, and the A fragments of
+// sub-block J + 2 are read while J is multiplied.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 
@@ -30,29 +37,22 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-#ifndef QLIN_GEMM_WAVES
-#define QLIN_GEMM_WAVES 8
-#endif
-#ifndef QLIN_GEMM_NT
-#define QLIN_GEMM_NT 2
-#endif
-constexpr int kWaves = QLIN_GEMM_WAVES;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kNT = QLIN_GEMM_NT;         // 16-row weight tiles per wave
+constexpr int kNT = 2;                    // 16-row weight tiles per wave
 constexpr int kBN = kWaves * kNT * 16;    // weight rows per workgroup (256)
-#ifndef QLIN_GEMM_SB
-#define QLIN_GEMM_SB 1
-#endif
-#ifndef QLIN_GEMM_MT
-#define QLIN_GEMM_MT 4
-#endif
-constexpr int kMT = QLIN_GEMM_MT;         // 16-token tiles per workgroup
+constexpr int kMT = 4;                    // 16-token tiles per workgroup
 constexpr int kBM = kMT * 16;             // tokens per workgroup (64)
-constexpr int kPlane = 2 * kMT * 8 * 64;  // uint4s of one buffer's A planes (hi, lo): 64 KB
-constexpr int kBuf = kPlane + kMT * 64;   // plus the min-term operands [mt][lane] (lanes >= 16 stay zero)
+// One LDS buffer (uint4 units): the qx plane [mt][j][lane] (fp16 integers), then the min-term
+// operands [mt][lane] (lanes >= 16 stay zero), then the block scales d8 [mt][j][token] as floats.
+// Two buffers: 76 KB.
+constexpr int kPlane = kMT * 8 * 64;
+constexpr int kS8 = kMT * 64;
+constexpr int kD8 = kMT * 8 * 16 / 4;
+constexpr int kBuf = kPlane + kS8 + kD8;
+constexpr size_t kLdsBytes = 2 * kBuf * sizeof(uint4);
 constexpr int kSJ = kThreads / kMT / 64;  // staging waves per token tile
 constexpr int kJJ = 8 / kSJ;              // sub-blocks each staging thread converts
-constexpr size_t kLds = 2 * kBuf * sizeof(uint4);  // two buffers
 
 struct GemmArgs {
     const uint8_t *w;
@@ -90,11 +90,13 @@ __device__ __forceinline__ f16x2 splat(float v) {
     return f16x2{h, h};
 }
 
+template <int V> using ic = std::integral_constant<int, V>;
+
 __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
     extern __shared__ uint4 lds[];
-    // two buffers, each: A planes [part][mt][j][lane] then s8 operands [mt][token]
     auto plane = [&](int buf) { return lds + buf * kBuf; };
     auto s8ops = [&](int buf) { return lds + buf * kBuf + kPlane; };
+    auto d8s = [&](int buf) { return reinterpret_cast<float *>(lds + buf * kBuf + kPlane + kS8); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -111,8 +113,8 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
     const uint8_t *xrow = a.xq + static_cast<size_t>(min(tok, a.m - 1)) * a.xrb;
 
     // min-term operand entries of lane-groups 1..3 stay zero (staging writes lanes 0..15 only)
-    for (int i = tid; i < 2 * kMT * 64; i += kThreads)
-        if ((i & 63) >= 16) s8ops(i / (kMT * 64))[i % (kMT * 64)] = make_uint4(0u, 0u, 0u, 0u);
+    for (int i = tid; i < 2 * kS8; i += kThreads)
+        if ((i & 63) >= 16) s8ops(i / kS8)[i % kS8] = make_uint4(0u, 0u, 0u, 0u);
 
     f32x4 acc[kMT][kNT];
 #pragma unroll
@@ -129,15 +131,16 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
         uint32_t bh[kJJ], q0[kJJ], q1[kJJ];
     };
     // past the end a fetch reloads the last super-block (valid addresses, never used)
-    auto fetch_w = [&](WRaw &w, int sb) {
+    auto fetch_hdr = [&](WRaw &w, int sb) {
         sb = min(sb, a.nsb - 1);
 #pragma unroll
-        for (int t = 0; t < kNT; ++t) {
-            const uint8_t *p = wrow[t] + static_cast<size_t>(sb) * 144;
-            w.hdr[t] = *reinterpret_cast<const uint4 *>(p);
+        for (int t = 0; t < kNT; ++t) w.hdr[t] = *reinterpret_cast<const uint4 *>(wrow[t] + static_cast<size_t>(sb) * 144);
+    };
+    auto fetch_qs = [&](WRaw &w, int sb, int pr) {
+        sb = min(sb, a.nsb - 1);
 #pragma unroll
-            for (int pr = 0; pr < 4; ++pr) w.qs[t][pr] = *reinterpret_cast<const uint2 *>(p + 16 + 32 * pr + 8 * g);
-        }
+        for (int t = 0; t < kNT; ++t)
+            w.qs[t][pr] = *reinterpret_cast<const uint2 *>(wrow[t] + static_cast<size_t>(sb) * 144 + 16 + 32 * pr + 8 * g);
     };
     auto fetch_x = [&](XRaw &x, int sb) {
         sb = min(sb, a.nsb - 1);
@@ -150,54 +153,48 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
         }
     };
 
-    // Activations of a super-block into buffer buf: q becomes fp16 exactly (bytes (q ^ 0x80, 0x64)
-    // = 1152 + q, minus 1152), hi = f16(d8*q) and lo = fma(d8, q, -hi) = the exact residual of hi
-    // (d8*q has at most 18 significant bits, hi keeps 11, so the residual fits an fp16).
+    // Activations of a super-block into buffer buf: qx as fp16 integers, d8 as a float per (token
+    // tile, block, token), s8 into the min-term operand row.  Tokens past m repeat the last row:
+    // their D rows are never stored.
     auto stage = [&](const XRaw &x, int buf) {
         uint4 *pl = plane(buf);
         const f16x2 off = splat(-1152.0f);
-        uint32_t s8h[kJJ];
 #pragma unroll
         for (int jj = 0; jj < kJJ; ++jj) {
             const int j = kJJ * sjh + jj;
-            const f16x2 d2 = u2h((x.bh[jj] & 0xffffu) * 0x10001u);
             const uint32_t u[2] = {x.q0[jj] ^ 0x80808080u, x.q1[jj] ^ 0x80808080u};
-            uint32_t hi[4], lo[4];
+            uint32_t qh[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t sel = (e & 1) ? 0x04030402u : 0x04010400u;
-                const f16x2 q2 = u2h(__builtin_amdgcn_perm(0x64646464u, u[e >> 1], sel)) + off;
-                const f16x2 h2 = d2 * q2;
-                hi[e] = h2u(h2);
-                lo[e] = h2u(__builtin_elementwise_fma(d2, q2, -h2));
+                qh[e] = h2u(u2h(__builtin_amdgcn_perm(0x64646464u, u[e >> 1], sel)) + off);
             }
-            // tokens past m repeat the last row: their D rows are never stored
-            pl[((0 * kMT + smt) * 8 + j) * 64 + sl] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            pl[((1 * kMT + smt) * 8 + j) * 64 + sl] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            s8h[jj] = x.bh[jj] >> 16;
+            pl[(smt * 8 + j) * 64 + sl] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
+            if (sg == 0) d8s(buf)[(smt * 8 + j) * 16 + si] = f16_bits_to_f32(x.bh[jj] & 0xffffu);
         }
         // the s8 operand row of token si: halves s8_0 .. s8_7 (written by the threads of sg == 0)
         if (sg == 0) {
             uint16_t *dst = reinterpret_cast<uint16_t *>(&s8ops(buf)[smt * 64 + si]) + kJJ * sjh;
 #pragma unroll
-            for (int jj = 0; jj < kJJ; ++jj) dst[jj] = static_cast<uint16_t>(s8h[jj]);
+            for (int jj = 0; jj < kJJ; ++jj) dst[jj] = static_cast<uint16_t>(x.bh[jj] >> 16);
         }
     };
 
     // One super-block: per 16-row tile the scales, then the 8 sub-blocks' MFMAs, then the min term.
-    auto compute = [&](const WRaw &w, int buf) {
+    // Each part of w is reloaded with super-block `next` as soon as it has been used, so one register
+    // set carries the weights (the loads have the rest of the super-block to land).
+    auto compute = [&](WRaw &w, int buf, int next) {
         const uint4 *pl = plane(buf);
+        const float *d8 = d8s(buf);
         float dd[kNT], dmin[kNT];
+        uint32_t mlo[kNT], mhi[kNT];
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
             dd[t] = f16_bits_to_f32(w.hdr[t].x & 0xffffu);
             dmin[t] = f16_bits_to_f32(w.hdr[t].x >> 16);
+            mlo[t] = w.hdr[t].z;
+            mhi[t] = w.hdr[t].w;
         }
-        f32x4 D[kMT][kNT];
-#pragma unroll
-        for (int i = 0; i < kMT; ++i)
-#pragma unroll
-            for (int t = 0; t < kNT; ++t) D[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         // All 8 scales of a tile at once (kernel.cu:913-921 on whole dwords): bytes j of sl are sub-block
         // j < 4, of sh sub-block 4 + j; as fp16 pairs (sc_2i, sc_2i+1) via the bytes (v, 0x64) = 1024 + v.
         const f16x2 off = splat(-1024.0f);
@@ -214,7 +211,26 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) cp[t][i] = scp[t][i] * off;
         }
-        auto sub_block = [&](auto jc) {
+        fetch_hdr(w, next);
+        // T = sum_j d8_j * (sc_j qw . qx)_j per output over the super-block; d applied after it
+        f32x4 T[kMT][kNT];
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+#pragma unroll
+            for (int t = 0; t < kNT; ++t) T[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // A fragments of a sub-block: qx of every token tile, and d8 of the lane's 4 tokens
+        struct Frag {
+            uint4 a[kMT];
+            float4 d8[kMT];
+        };
+        auto load_frag = [&](Frag &f, int J) {
+#pragma unroll
+            for (int i = 0; i < kMT; ++i) {
+                f.a[i] = pl[(i * 8 + J) * 64 + lane];
+                f.d8[i] = *reinterpret_cast<const float4 *>(d8 + (i * 8 + J) * 16 + 4 * g);
+            }
+        };
+        auto sub_block = [&](auto jc, const Frag &f) {
             constexpr int J = decltype(jc)::value;
             uint4 B[kNT];
 #pragma unroll
@@ -223,29 +239,49 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
                 const f16x2 c2 = __builtin_shufflevector(cp[t][J >> 1], cp[t][J >> 1], J & 1, J & 1);
                 B[t] = weights_b<J>(w.qs[t][J >> 1], sc2, c2);
             }
-            // hi for every (token tile, row tile), then lo: consecutive MFMAs never feed each other
 #pragma unroll
-            for (int part = 0; part < 2; ++part)
+            for (int i = 0; i < kMT; ++i) {
+                f32x4 Dj[kNT];
 #pragma unroll
-                for (int i = 0; i < kMT; ++i) {
-                    const uint4 av = pl[((part * kMT + i) * 8 + J) * 64 + lane];
+                for (int t = 0; t < kNT; ++t) Dj[t] = mfma(f.a[i], B[t], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                const float d8r[4] = {f.d8[i].x, f.d8[i].y, f.d8[i].z, f.d8[i].w};
 #pragma unroll
-                    for (int t = 0; t < kNT; ++t) D[i][t] = mfma(av, B[t], D[i][t]);
-                }
-            // no hoisting of the next sub-block's LDS reads above these MFMAs: the registers they
-            // would hold push the kernel past its 256 VGPRs (measured 3% faster)
-#if QLIN_GEMM_SB
+                for (int t = 0; t < kNT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) T[i][t][r] = fmaf(Dj[t][r], d8r[r], T[i][t][r]);
+            }
+            // The block's scaling is pure arithmetic, which instruction selection would otherwise
+            // sink below every later sub-block, keeping all of a super-block's MFMA results live
+            // (hundreds of VGPRs spilled); consuming the sums here pins it before the next MFMAs.
+            static_assert(kMT * kNT == 8, "one operand per sum");
+            asm volatile("" ::"v"(T[0][0]), "v"(T[0][1]), "v"(T[1][0]), "v"(T[1][1]), "v"(T[2][0]), "v"(T[2][1]),
+                         "v"(T[3][0]), "v"(T[3][1]));
+            // the order as written: the next fragments' LDS reads (issued before this call) overlap
+            // these MFMAs, and nothing is hoisted above them to hold more registers
             __builtin_amdgcn_sched_barrier(0);
-#endif
         };
-        sub_block(std::integral_constant<int, 0>{});
-        sub_block(std::integral_constant<int, 1>{});
-        sub_block(std::integral_constant<int, 2>{});
-        sub_block(std::integral_constant<int, 3>{});
-        sub_block(std::integral_constant<int, 4>{});
-        sub_block(std::integral_constant<int, 5>{});
-        sub_block(std::integral_constant<int, 6>{});
-        sub_block(std::integral_constant<int, 7>{});
+        // software pipeline over the sub-blocks: fragments of J + 1 are read while J is multiplied
+        Frag f0, f1;
+        load_frag(f0, 0);
+        load_frag(f1, 1);
+        sub_block(ic<0>{}, f0);
+        load_frag(f0, 2);
+        sub_block(ic<1>{}, f1);
+        fetch_qs(w, next, 0);
+        load_frag(f1, 3);
+        sub_block(ic<2>{}, f0);
+        load_frag(f0, 4);
+        sub_block(ic<3>{}, f1);
+        fetch_qs(w, next, 1);
+        load_frag(f1, 5);
+        sub_block(ic<4>{}, f0);
+        load_frag(f0, 6);
+        sub_block(ic<5>{}, f1);
+        fetch_qs(w, next, 2);
+        load_frag(f1, 7);
+        sub_block(ic<6>{}, f0);
+        sub_block(ic<7>{}, f1);
+        fetch_qs(w, next, 3);
 
         // min term: sum_j s8_j * m_j on one more MFMA.  Only k-slots 0..7 (lane-group 0) carry s8; the
         // other lanes' A entries are zeros in LDS, so their B entries (finite mins) add nothing.
@@ -253,52 +289,41 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
             // the 8 mins of the tile, as the scales above (bytes j of ml: sub-block j < 4; of mh: 4 + j)
-            const uint32_t s1 = w.hdr[t].z, s2 = w.hdr[t].w;
             f16x2 mp[4];
-            pairs(s1 & 0x3f3f3f3fu, mp);
-            pairs(((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u), mp + 2);
+            pairs(mlo[t] & 0x3f3f3f3fu, mp);
+            pairs(((mhi[t] >> 4) & 0x0f0f0f0fu) | ((mlo[t] >> 2) & 0x30303030u), mp + 2);
             const uint4 b2 = make_uint4(h2u(mp[0]), h2u(mp[1]), h2u(mp[2]), h2u(mp[3]));
 #pragma unroll
             for (int i = 0; i < kMT; ++i) {
-                const uint4 a2 = s8[i * 64 + lane];
-                const f32x4 d2 = mfma(a2, b2, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                const f32x4 d2 = mfma(s8[i * 64 + lane], b2, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    acc[i][t][r] = fmaf(dd[t], D[i][t][r], acc[i][t][r]);
+                    acc[i][t][r] = fmaf(dd[t], T[i][t][r], acc[i][t][r]);
                     acc[i][t][r] = fmaf(-dmin[t], d2[r], acc[i][t][r]);
                 }
             }
         }
     };
 
-    // Pipeline: the operands of super-block sb + 2 are requested while sb is computed and sb + 1 is
-    // staged into the other LDS buffer; one barrier per super-block.  Two register sets in turn (a
-    // single set copied forward would make the copy wait for the loads just issued).
-    WRaw w0, w1;
-    XRaw x0, x1;
-    fetch_w(w0, 0);
-    fetch_x(x0, 0);
-    fetch_w(w1, 1);
-    fetch_x(x1, 1);
-    stage(x0, 0);
+    // Pipeline over super-blocks: sb is computed from buffer sb & 1 while its weights are replaced by
+    // sb + 1's part by part; then sb + 1's activations (loaded during sb) are staged into the other
+    // buffer, whose last reads were before the previous barrier, and sb + 2's requested.
+    WRaw w;
+    XRaw x;
+    fetch_hdr(w, 0);
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) fetch_qs(w, 0, pr);
+    fetch_x(x, 0);
+    stage(x, 0);
+    fetch_x(x, 1);
     __syncthreads();
-    // At the top of an iteration: buffer 0 holds sb's activations, w0 = sb's weights, w1 / x1 =
-    // sb + 1's raw operands (buffer 1 was last read before the previous barrier).
-    const int pairs = a.nsb >> 1;  // branch-free body, so the compiler waits for exactly what is used
-    for (int pi = 0; pi < pairs; ++pi) {
-        const int sb = 2 * pi;
-        fetch_x(x0, sb + 2);
-        compute(w0, 0);
-        stage(x1, 1);
-        fetch_w(w0, sb + 2);
-        __syncthreads();
-        fetch_x(x1, sb + 3);
-        compute(w1, 1);
-        stage(x0, 0);
-        fetch_w(w1, sb + 3);
+    for (int sb = 0; sb < a.nsb; ++sb) {
+        const int buf = sb & 1;
+        compute(w, buf, sb + 1);
+        stage(x, buf ^ 1);  // past the end: a copy of the last super-block, never read
+        fetch_x(x, sb + 2);
         __syncthreads();
     }
-    if (a.nsb & 1) compute(w0, 0);  // odd count: the last super-block is staged in buffer 0
 
     // lane (g, n) holds tokens 4g .. 4g+3 of each 16-token tile, weight row n of each 16-row tile
 #pragma unroll
@@ -335,7 +360,7 @@ hipError_t q4k_gemm_q8_1(const uint8_t *w, size_t rb, const uint8_t *xq, float *
     a.m = m;
     a.nsb = in_dim / 256;
     const dim3 grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    hipLaunchKernelGGL(q4k_gemm_kernel, grid, dim3(kThreads), kLds, s, a);
+    hipLaunchKernelGGL(q4k_gemm_kernel, grid, dim3(kThreads), kLdsBytes, s, a);
     return hipGetLastError();
 }
 

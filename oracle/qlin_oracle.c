@@ -380,9 +380,13 @@ int orc_matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t 
                     int out_dim, int in_dim, int m) {
     if (check_shape(type, in_dim) || out_dim < 0 || m < 0) return -1;
     const int bpr = in_dim / 32;
-    float *wr = (float *)malloc(sizeof(float) * (size_t)in_dim);
-    if (!wr) return -1;
+    /* rows in parallel, each output element summed in the same order whatever the thread count */
+    const int nt = omp_get_max_threads();
+    float *wall = (float *)malloc(sizeof(float) * (size_t)in_dim * (size_t)nt);
+    if (!wall) return -1;
+#pragma omp parallel for num_threads(nt) schedule(static)
     for (int o = 0; o < out_dim; ++o) {
+        float *wr = wall + (size_t)omp_get_thread_num() * (size_t)in_dim;
         const uint8_t *row = w + (size_t)o * row_bytes;
         deq_row(type, row, in_dim, wr);
         for (int r = 0; r < m; ++r) {
@@ -433,7 +437,7 @@ int orc_matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t 
             y[(size_t)r * out_dim + o] = acc;
         }
     }
-    free(wr);
+    free(wall);
     return 0;
 }
 

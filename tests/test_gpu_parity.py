@@ -361,9 +361,10 @@ def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
     assert normwise_rel_err(host(yd), ref) <= FP32
 
 
-def test_q4k_gemm_c4_shape_sampled():
-    """C4: Q4_K [14336, 4096] x Q8_1 activations [512, 4096] (f16 N(0,1) values) -> [512, 14336], checked
-    against the oracle on 72 weight rows (random ones plus both ends of the matrix)."""
+def test_q4k_gemm_c4_shape_every_row():
+    """C4: Q4_K [14336, 4096] x Q8_1 activations [512, 4096] (f16 N(0,1) values) -> [512, 14336], every
+    weight row checked against the oracle on 64 tokens: both ends of each of the 8 64-token tiles plus
+    random ones, so every workgroup row and column of the grid is covered."""
     N, K, M = 14336, 4096, 512
     rng = np.random.default_rng(81)
     rb = K // 256 * 144
@@ -374,9 +375,18 @@ def test_q4k_gemm_c4_shape_sampled():
     banner("q4k gemm C4 shape 512x4096x14336")
     yd = empty_f32(M, N)
     qlin.quant_matmul_q8_1(Q4_K, dev(w.reshape(-1)), rb, dev(xq), yd, N, K, M)
-    rows = np.unique(np.concatenate([rng.choice(N, 64, replace=False), [0, 1, 255, 256, N - 2, N - 1]]))
-    ref = orc.matmul_q8_1(Q4_K, np.ascontiguousarray(w[rows]).reshape(-1), rb, xq, len(rows), K, M)
-    assert normwise_rel_err(host(yd)[:, rows], ref) <= FP32
+    ends = np.array([[64 * t, 64 * t + 63] for t in range(M // 64)]).reshape(-1)
+    rest = rng.choice(np.setdiff1d(np.arange(M), ends), 64 - ends.size, replace=False)
+    toks = np.sort(np.concatenate([ends, rest]))
+    assert toks.size == 64 and np.unique(toks).size == 64
+    rbx = orc.q8_1_row_bytes(K)
+    xq_t = np.ascontiguousarray(xq.reshape(M, rbx)[toks]).reshape(-1)
+    ref = orc.matmul_q8_1(Q4_K, w.reshape(-1), rb, xq_t, N, K, toks.size)
+    assert normwise_rel_err(host(yd)[toks], ref) <= FP32
+    # per row as well: no row may hide behind the others' norm
+    got = host(yd)[toks]
+    row_err = np.linalg.norm(got - ref, axis=0) / np.maximum(np.linalg.norm(ref, axis=0), 1e-30)
+    assert row_err.max() <= 1e-5, (int(row_err.argmax()), float(row_err.max()))
 
 
 # ---- MoE ----------------------------------------------------------------------------------------
