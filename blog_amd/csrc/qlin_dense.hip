@@ -1,20 +1,26 @@
-// qlin_dense.hip -- quantized matmul over a few rows of f32 activations on the f32 matrix cores, gfx950.
+// qlin_dense.hip -- quantized matmul over a few rows of f32 activations on the matrix cores, gfx950.
 //
 //   y[r, o] = sum_k w(o, k) * x[r, k]          (kernel.cu:1254-1279, quant_matmul_kernel; m > 1)
 //   y[r, o] += ...                              (the gemm + add of SharedExperts.cpp:42-48)
 //   act[r, o] = g / (1 + expf(-g)) * u,  g, u the rows of the gate and up matrices
 //                                               (the gemm, gemm, silu_mul of SharedExperts.cpp:34-40)
 //
-// w(o, k) is the canonical dequantized f32 element (the bit-exact decode of kernel.cu:913-930), and
-// the products w * x are summed in f32 by v_mfma_f32_16x16x4_f32: the contraction the reference runs
-// one warp per (r, o), with the same f32 operands and only the summation order changed.
+// Q4_K (the shared experts) on v_mfma_f32_16x16x32_bf16 with the tokens as the MFMA rows.  The
+// element value of sub-block j is w = dsc*q - dm (dsc = d*sc_j, dm = dmin*m_j, kernel.cu:913-930), so
+//   sum_k w x = dsc * sum x (128 + q) - (128 dsc + dm) * sum x
+// where the nibble q enters as the exact bf16 128 + q (one v_perm_b32 per two weights) and x as the
+// bf16 pair hi = bf16(x), lo = bf16(x - hi): every product is exact and accumulates in f32.  Per
+// sub-block and 16-token tile one MFMA pair gives sum x (128 + q) for 16 weight rows, and one more
+// pair against an all-ones B gives sum x (in the same D layout); the scales are applied by two fmas
+// per output.  The other formats multiply the canonical f32 element values (decoded as the
+// reference decodes them) on v_mfma_f32_16x16x4_f32: the contraction the reference runs one warp
+// per (r, o), with the same f32 operands and only the summation order changed.
 //
-// Layout.  A workgroup owns a tile of 16 output rows and all of K; its 8 waves take the 256-element
-// chunks of K in turn (wave w: w, w + 8, ...; Q4_K super-blocks, eight 32-element blocks otherwise).  Lane l supplies output row l % 16 and token
-// l % 16 of the current 16-token tile, and k-slot g = l / 16 of each MFMA: the 8 MFMAs of 32-element
-// sub-block j cover its elements 8g .. 8g+7 in slot g, so a lane reads 8 consecutive weights and 8
-// consecutive activations per sub-block.  D holds tokens 4g .. 4g+3 of row l % 16.  The waves'
-// partials meet in LDS and are summed in wave order.  A grid row per 64 tokens.
+// Layout.  A workgroup owns a tile of 16 output rows and all of K; its 8 waves take the chunks of K in
+// turn (wave w: w, w + 8, ...; Q4_K super-blocks, eight 32-element blocks otherwise).  Lane l supplies output row l % 16 and token l % 16 of the current
+// 16-token tile, and k-slots of group g = l / 16 of each MFMA (Q4_K: elements 8g .. 8g+7 of a
+// sub-block).  D holds tokens 4g .. 4g+3 of row l % 16.  The waves' partials meet in LDS and are
+// summed in wave order.  A grid row per 64 tokens.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
@@ -53,20 +59,6 @@ __device__ __forceinline__ void load_q4k(Q4KRaw &r, const uint8_t *sb, int g) {
     }
 }
 
-// Elements 8g .. 8g+7 of sub-block j, canonical values (d * sc) * q - dmin * m.
-__device__ __forceinline__ void q4k_values(const Q4KRaw &r, int j, float (&v)[8]) {
-    int sc, mn;
-    q4k_scale_min(j, r.h.y, r.h.z, r.h.w, sc, mn);
-    const float d = f16_bits_to_f32(r.h.x & 0xffffu), dmin = f16_bits_to_f32(r.h.x >> 16);
-    const float dsc = mul_rn(d, static_cast<float>(sc)), dm = mul_rn(dmin, static_cast<float>(mn));
-    const int sh = 4 * (j & 1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t q = (r.q[2 * (j >> 1) + (i >> 2)] >> (8 * (i & 3) + sh)) & 15u;
-        v[i] = sub_rn(mul_rn(dsc, static_cast<float>(q)), dm);
-    }
-}
-
 template <int MODE>
 __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a) {
     constexpr int NW = MODE == kSwiGLU ? 2 : 1;
@@ -81,43 +73,68 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
     const int ntt = min(4, (a.m - t0 + 15) / 16);  // token tiles of this grid row
     const uint8_t *rp[2] = {a.w0 + static_cast<size_t>(row) * a.rb, a.w1 + static_cast<size_t>(row) * a.rb};
 
-    f32x4 D[NW][4];
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0 in every slot
+    // one 16-token tile at a time (a tile's weights come again from the cache for the next one)
+    for (int tt = 0; tt < ntt; ++tt) {
+        // token of this lane's A row (tokens past m read the last one; their D rows are dropped)
+        const int tok = min(t0 + tt * 16 + n, a.m - 1);
+        const float *xrow = a.x + static_cast<size_t>(tok) * K + 8 * g;
+        f32x4 D[NW];
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
+        for (int w = 0; w < NW; ++w) D[w] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // wave w takes super-blocks w, w + 8, ...; the next one's weights are requested before the
+        // current one's math
+        Q4KRaw cur[NW];
+        int sb = wave;
+        if (sb < nsb) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) D[w][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int sb = wave; sb < nsb; sb += kDWaves) {
-        Q4KRaw raw[NW];
+            for (int w = 0; w < NW; ++w) load_q4k(cur[w], rp[w] + static_cast<size_t>(sb) * 144, g);
+        }
+        while (sb < nsb) {  // uniform
+            const int sb2 = sb + kDWaves;
+            Q4KRaw nxt[NW];
+            if (sb2 < nsb) {  // uniform
 #pragma unroll
-        for (int w = 0; w < NW; ++w) load_q4k(raw[w], rp[w] + static_cast<size_t>(sb) * 144, g);
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            if (tt >= ntt) break;  // uniform
-            // token of this lane's A row (tokens past m read the last one; their D rows are dropped)
-            const int tok = min(t0 + tt * 16 + n, a.m - 1);
-            const float *xr = a.x + static_cast<size_t>(tok) * K + sb * 256 + 8 * g;
+                for (int w = 0; w < NW; ++w) load_q4k(nxt[w], rp[w] + static_cast<size_t>(sb2) * 144, g);
+            }
+            const float *xr = xrow + sb * 256;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float4 x0 = *reinterpret_cast<const float4 *>(xr + 32 * j);
                 const float4 x1 = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
-                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                uint32_t h[4], l[4];
+                split_bf16x2(x0.x, x0.y, h[0], l[0]);
+                split_bf16x2(x0.z, x0.w, h[1], l[1]);
+                split_bf16x2(x1.x, x1.y, h[2], l[2]);
+                split_bf16x2(x1.z, x1.w, h[3], l[3]);
+                const u32x4 ahi = {h[0], h[1], h[2], h[3]}, alo = {l[0], l[1], l[2], l[3]};
+                const f32x4 X = mfma(alo, ones, mfma(ahi, ones, f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
 #pragma unroll
                 for (int w = 0; w < NW; ++w) {
-                    float v[8];
-                    q4k_values(raw[w], j, v);
+                    // this lane's row: dsc and the coefficient of sum x for sub-block j
+                    int sc, mn;
+                    q4k_scale_min(j, cur[w].h.y, cur[w].h.z, cur[w].h.w, sc, mn);
+                    const float dsc = mul_rn(f16_bits_to_f32(cur[w].h.x & 0xffffu), static_cast<float>(sc));
+                    const float cx =
+                        -(128.0f * dsc + mul_rn(f16_bits_to_f32(cur[w].h.x >> 16), static_cast<float>(mn)));
+                    // elements 8g .. 8g+7 of sub-block j: the low (j even) or high nibbles of the
+                    // lane's bytes of sub-block pair j / 2
+                    const int sh = 4 * (j & 1);
+                    const u32x4 B = weights_operand2((cur[w].q[2 * (j >> 1)] >> sh) & 0x0f0f0f0fu,
+                                                     (cur[w].q[2 * (j >> 1) + 1] >> sh) & 0x0f0f0f0fu);
+                    const f32x4 Dj = mfma(alo, B, mfma(ahi, B, f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) D[w][tt] = mfma_f32(xv[i], v[i], D[w][tt]);
+                    for (int r = 0; r < 4; ++r) D[w][r] = fmaf(cx, X[r], fmaf(dsc, Dj[r], D[w][r]));
                 }
             }
+            if (sb2 >= nsb) break;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) cur[w] = nxt[w];
+            sb = sb2;
         }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) part[wave][w][tt][lane] = D[w];
     }
-
-#pragma unroll
-    for (int w = 0; w < NW; ++w)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-            if (tt < ntt) part[wave][w][tt][lane] = D[w][tt];
     __syncthreads();
 
     // outputs: row o = row0 + (i % 16), token t0 + i / 16; D element r of lane l is token 4(l/16) + r

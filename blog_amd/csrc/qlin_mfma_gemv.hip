@@ -97,6 +97,9 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #ifndef QLIN_MFMA_ROUTED_DEPTH
 #define QLIN_MFMA_ROUTED_DEPTH 1
 #endif
+#ifndef QLIN_MFMA_LONG_DEPTH
+#define QLIN_MFMA_LONG_DEPTH 1
+#endif
 // Workgroup b of G takes 16-row tiles b, b + G, b + 2G, ... (1), so that all workgroups sweep one
 // region of the weights together, rather than a contiguous slice each (0): 1.6% faster over the
 // decode step (gate/up and lm_head, the launches with several tiles per workgroup).
@@ -483,7 +486,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // of each other.
     // DEPTH 2: wave w starts with steps w and w + kWaves, both requested before the x staging
     // (Q6_K's 27-dword steps would spill with three buffers)
-    constexpr int DEPTH = ROUTED && FMT != T_Q6_K ? QLIN_MFMA_ROUTED_DEPTH : QLIN_MFMA_DEPTH;
+    constexpr int DEPTH = ROUTED && FMT != T_Q6_K ? QLIN_MFMA_ROUTED_DEPTH
+                          : (!ROUTED && XR > 2 && FMT != T_Q6_K) ? QLIN_MFMA_LONG_DEPTH : QLIN_MFMA_DEPTH;
     __shared__ int next_step;
     if (tid == 0) next_step = DEPTH * kWaves;
     if (tid < 4) s_zero[tid] = u32x4{0u, 0u, 0u, 0u};
