@@ -87,6 +87,10 @@ hipError_t dequant(int type, const uint8_t *src, void *out, int64_t n, bool to_f
 
 // Q8_1 activation quantizer (36 B per 32 values) and the weight x Q8_1 matmul.
 hipError_t quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, bool raw_sum, hipStream_t s);
+// Q8_0 / Q5_0 / Q4_0 x Q8_1 prefill GEMM on the fp16 matrix cores (qlin_qblk_gemm.hip).
+bool qblk_gemm_ok(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, int in_dim);
+hipError_t qblk_gemm_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y, int out_dim,
+                          int in_dim, int m, hipStream_t s);
 // Q4_K x Q8_1 prefill GEMM on the fp16 matrix cores (qlin_q4k_gemm.hip).
 bool q4k_gemm_ok(const uint8_t *w, size_t row_bytes, const uint8_t *xq, int in_dim);
 hipError_t q4k_gemm_q8_1(const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y, int out_dim, int in_dim,

@@ -51,6 +51,7 @@ hipError_t matmul_q8_1(int type, const uint8_t *w, size_t rb, const uint8_t *xq,
     const int64_t waves = static_cast<int64_t>(m) * out_dim;
     if (waves == 0) return hipSuccess;
     if (type == T_Q4_K && q4k_gemm_ok(w, rb, xq, in_dim)) return q4k_gemm_q8_1(w, rb, xq, y, out_dim, in_dim, m, s);
+    if (qblk_gemm_ok(type, w, rb, xq, in_dim)) return qblk_gemm_q8_1(type, w, rb, xq, y, out_dim, in_dim, m, s);
     const dim3 grid(static_cast<unsigned>((waves + 3) / 4));
     switch (type) {
         case T_Q4_0: hipLaunchKernelGGL((matmul_q8_1_kernel<T_Q4_0>), grid, dim3(256), 0, s, w, rb, xq, y, out_dim, in_dim, m); break;

@@ -349,7 +349,14 @@ def test_quantize_q8_1_bit_exact(raw):
 @pytest.mark.parametrize("qtype,out_dim,in_dim,m", [(Q4_K, 96, 1024, 7), (Q6_K, 40, 512, 3), (Q8_0, 50, 256, 4),
                                                     (Q5_0, 33, 128, 2), (Q4_0, 17, 64, 3), (Q4_K, 512, 4096, 64),
                                                     (Q4_K, 300, 768, 70), (Q4_K, 257, 256, 1),
-                                                    (Q4_K, 16, 512, 129)])
+                                                    (Q4_K, 16, 512, 129),
+                                                    # the 32-block formats' matrix-core GEMM: whole and
+                                                    # partial 8-block units (K 1408 = 5.5 units, 192 =
+                                                    # 0.75), row and token tails, one token
+                                                    (Q8_0, 300, 4096, 70), (Q5_0, 2048, 1408, 96),
+                                                    (Q4_0, 257, 192, 65), (Q8_0, 33, 64, 1), (Q5_0, 513, 2816, 17),
+                                                    # K / 32 odd: rows not 4-byte aligned, the per-element kernel
+                                                    (Q8_0, 40, 96, 5), (Q5_0, 24, 160, 3)])
 def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
     w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=61 + out_dim)
     x = qgen.random_x(m, in_dim, seed=62)
