@@ -1,5 +1,5 @@
-// qlin_qblk_gemm.hip -- Q8_0, Q5_0 and Q4_0 weights x Q8_1 activations, the prefill GEMM, on the fp16
-// matrix cores of gfx950.
+// qlin_qblk_gemm.hip -- Q8_0, Q5_0, Q4_0 and Q6_K weights x Q8_1 activations, the prefill GEMM, on
+// the fp16 matrix cores of gfx950 (Q6_K: see q6k_gemm_kernel below).
 //
 // Computes y[r, o] = sum over 32-blocks b of  dw_b * d8_b * sum_i (qw_i - c) qx_i  (the reference
 // quant_matmul_q8_1_kernel for these formats, AI/codes/local-llm/src/backend/cuda/ops/kernel.cu:
@@ -174,27 +174,112 @@ __device__ __forceinline__ uint4 weights_b(const BRaw &r, int g) {
 
 template <int V> using ic = std::integral_constant<int, V>;
 
+// The Q8_1 activations of a workgroup's 64 tokens, staged per unit of 8 blocks into two LDS buffers:
+// qx as fp16 integers in the A-operand layout and d8 as a float per (token tile, block, token);
+// blocks past the row are zeros.  Thread roles: token tile smt, slot lane sl (token si, k-group sg),
+// blocks kJJ*sjh .. +kJJ-1 of the unit.  Tokens past m repeat the last row (their D rows are never
+// stored).
+struct ActStage {
+    uint4 *lds;
+    const uint8_t *xrow;
+    int smt, sjh, sl, si, sg, nblk, nunit;
+    struct Raw {
+        uint32_t bh[kJJ], q0[kJJ], q1[kJJ];
+    };
+    __device__ ActStage(uint4 *l, const GemmArgs &a, int tid)
+        : lds(l), smt(tid / (kSJ * 64)), sjh((tid >> 6) % kSJ), sl(tid & 63), si(tid & 15), sg((tid & 63) >> 4),
+          nblk(a.nblk), nunit((a.nblk + 7) / 8) {
+        const int tok = blockIdx.y * kBM + smt * 16 + si;
+        xrow = a.xq + static_cast<size_t>(min(tok, a.m - 1)) * a.xrb;
+    }
+    __device__ uint4 *plane(int buf) const { return lds + buf * kBuf; }
+    __device__ float *d8s(int buf) const { return reinterpret_cast<float *>(lds + buf * kBuf + kPlane); }
+    __device__ void fetch(Raw &x, int u) const {
+        u = min(u, nunit - 1);
+#pragma unroll
+        for (int jj = 0; jj < kJJ; ++jj) {
+            const int b = min(u * 8 + kJJ * sjh + jj, nblk - 1);
+            const uint8_t *blk = xrow + static_cast<size_t>(b) * 36;
+            x.bh[jj] = *reinterpret_cast<const uint32_t *>(blk);
+            x.q0[jj] = *reinterpret_cast<const uint32_t *>(blk + 4 + 8 * sg);
+            x.q1[jj] = *reinterpret_cast<const uint32_t *>(blk + 8 + 8 * sg);
+        }
+    }
+    __device__ void stage(const Raw &x, int buf, int u) const {
+        uint4 *pl = plane(buf);
+        const f16x2 off = splat(-1152.0f);
+#pragma unroll
+        for (int jj = 0; jj < kJJ; ++jj) {
+            const int j = kJJ * sjh + jj;
+            const bool live = u * 8 + j < nblk;
+            const uint32_t v[2] = {x.q0[jj] ^ 0x80808080u, x.q1[jj] ^ 0x80808080u};
+            uint32_t q[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t sel = (e & 1) ? 0x04030402u : 0x04010400u;
+                q[e] = live ? h2u(u2h(__builtin_amdgcn_perm(0x64646464u, v[e >> 1], sel)) + off) : 0u;
+            }
+            pl[(smt * 8 + j) * 64 + sl] = make_uint4(q[0], q[1], q[2], q[3]);
+            if (sg == 0) d8s(buf)[(smt * 8 + j) * 16 + si] = live ? f16_bits_to_f32(x.bh[jj] & 0xffffu) : 0.0f;
+        }
+    }
+};
+
+// A fragments of block J: qx of every token tile, and d8 of the lane's 4 tokens
+struct Frag {
+    uint4 a[kMT];
+    float4 d8[kMT];
+};
+__device__ __forceinline__ void load_frag(Frag &f, const ActStage &st, int buf, int J, int lane) {
+    const uint4 *pl = st.plane(buf);
+    const float *d8 = st.d8s(buf);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) {
+        f.a[i] = pl[(i * 8 + J) * 64 + lane];
+        f.d8[i] = *reinterpret_cast<const float4 *>(d8 + (i * 8 + J) * 16 + 4 * (lane >> 4));
+    }
+}
+
+// The block's scaling is pure arithmetic, which instruction selection would otherwise sink below
+// every later block, keeping all of a unit's MFMA results live (spills); consuming the sums pins it
+// before the next block's MFMAs.
+__device__ __forceinline__ void pin(f32x4 (&T)[kMT][kNT]) {
+    static_assert(kMT * kNT == 8, "one operand per sum");
+    asm volatile("" ::"v"(T[0][0]), "v"(T[0][1]), "v"(T[1][0]), "v"(T[1][1]), "v"(T[2][0]), "v"(T[2][1]), "v"(T[3][0]),
+                 "v"(T[3][1]));
+}
+
+// lane (g, n) holds tokens 4g .. 4g+3 of each 16-token tile, weight row n of each 16-row tile
+__device__ __forceinline__ void store_tile(const GemmArgs &a, const f32x4 (&acc)[kMT][kNT], int o0, int m0, int n,
+                                           int g) {
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+        const int o = o0 + t * 16 + n;
+        if (o >= a.n) continue;
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tk = m0 + i * 16 + 4 * g + r;
+                if (tk < a.m) a.y[static_cast<size_t>(tk) * a.n + o] = acc[i][t][r];
+            }
+    }
+}
+
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
     constexpr int BB = QBlk<FMT>::bytes;
     extern __shared__ uint4 lds[];
-    auto plane = [&](int buf) { return lds + buf * kBuf; };
-    auto d8s = [&](int buf) { return reinterpret_cast<float *>(lds + buf * kBuf + kPlane); };
-
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int m0 = blockIdx.y * kBM;
     const int o0 = blockIdx.x * kBN + wave * kNT * 16;
-    const int nblk = a.nblk, nunit = (nblk + 7) / 8;
+    const ActStage st(lds, a, tid);
+    const int nblk = a.nblk, nunit = st.nunit;
 
     const uint8_t *wrow[kNT];
 #pragma unroll
     for (int t = 0; t < kNT; ++t) wrow[t] = a.w + static_cast<size_t>(min(o0 + t * 16 + n, a.n - 1)) * a.rb;
-
-    // staging role: token tile smt, slot lane sl (token si, k-group sg), blocks kJJ*sjh .. +kJJ-1
-    const int smt = tid / (kSJ * 64), sjh = (tid >> 6) % kSJ, sl = tid & 63, si = sl & 15, sg = sl >> 4;
-    const int tok = m0 + smt * 16 + si;
-    const uint8_t *xrow = a.xq + static_cast<size_t>(min(tok, a.m - 1)) * a.xrb;
 
     f32x4 T[kMT][kNT];
 #pragma unroll
@@ -206,9 +291,6 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
     struct WRaw {
         BRaw b[8][kNT];
     };
-    struct XRaw {
-        uint32_t bh[kJJ], q0[kJJ], q1[kJJ];
-    };
     // block J of unit u (past the end: the last block of the same parity, valid and never used)
     auto fetch_blk = [&](auto jc, WRaw &w, int u) {
         constexpr int J = decltype(jc)::value;
@@ -216,57 +298,10 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
 #pragma unroll
         for (int t = 0; t < kNT; ++t) w.b[J][t] = load_block<FMT, J & 1>(wrow[t] + static_cast<size_t>(b) * BB, g);
     };
-    auto fetch_x = [&](XRaw &x, int u) {
-        u = min(u, nunit - 1);
-#pragma unroll
-        for (int jj = 0; jj < kJJ; ++jj) {
-            const int b = min(u * 8 + kJJ * sjh + jj, nblk - 1);
-            const uint8_t *blk = xrow + static_cast<size_t>(b) * 36;
-            x.bh[jj] = *reinterpret_cast<const uint32_t *>(blk);
-            x.q0[jj] = *reinterpret_cast<const uint32_t *>(blk + 4 + 8 * sg);
-            x.q1[jj] = *reinterpret_cast<const uint32_t *>(blk + 8 + 8 * sg);
-        }
-    };
-
-    // Activations of unit u into buffer buf: qx as fp16 integers, d8 as a float per (token tile,
-    // block, token); blocks past the row are zeros.  Tokens past m repeat the last row: their D rows
-    // are never stored.
-    auto stage = [&](const XRaw &x, int buf, int u) {
-        uint4 *pl = plane(buf);
-        const f16x2 off = splat(-1152.0f);
-#pragma unroll
-        for (int jj = 0; jj < kJJ; ++jj) {
-            const int j = kJJ * sjh + jj;
-            const bool live = u * 8 + j < nblk;
-            const uint32_t v[2] = {x.q0[jj] ^ 0x80808080u, x.q1[jj] ^ 0x80808080u};
-            uint32_t qh[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t sel = (e & 1) ? 0x04030402u : 0x04010400u;
-                qh[e] = live ? h2u(u2h(__builtin_amdgcn_perm(0x64646464u, v[e >> 1], sel)) + off) : 0u;
-            }
-            pl[(smt * 8 + j) * 64 + sl] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
-            if (sg == 0) d8s(buf)[(smt * 8 + j) * 16 + si] = live ? f16_bits_to_f32(x.bh[jj] & 0xffffu) : 0.0f;
-        }
-    };
 
     // One unit from buffer buf: the blocks' MFMAs and scaling; each block's weights are reloaded
-    // with unit `next` right after they are decoded.
+    // with unit u + 1 right after they are decoded.
     auto compute = [&](WRaw &w, int buf, int u) {
-        const uint4 *pl = plane(buf);
-        const float *d8 = d8s(buf);
-        const int next = u + 1;
-        struct Frag {
-            uint4 a[kMT];
-            float4 d8[kMT];
-        };
-        auto load_frag = [&](Frag &f, int J) {
-#pragma unroll
-            for (int i = 0; i < kMT; ++i) {
-                f.a[i] = pl[(i * 8 + J) * 64 + lane];
-                f.d8[i] = *reinterpret_cast<const float4 *>(d8 + (i * 8 + J) * 16 + 4 * g);
-            }
-        };
         auto block = [&](auto jc, const Frag &f) {
             constexpr int J = decltype(jc)::value;
             if (u * 8 + J < nblk) {  // uniform
@@ -287,31 +322,27 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
                         for (int r = 0; r < 4; ++r) T[i][t][r] = fmaf(Dj[r] * dw[t], d8r[r], T[i][t][r]);
                     }
                 }
-                // the scaling, pinned before the next block's MFMAs (instruction selection would
-                // otherwise keep every block's results live to the end of the unit)
-                static_assert(kMT * kNT == 8, "one operand per sum");
-                asm volatile("" ::"v"(T[0][0]), "v"(T[0][1]), "v"(T[1][0]), "v"(T[1][1]), "v"(T[2][0]),
-                             "v"(T[2][1]), "v"(T[3][0]), "v"(T[3][1]));
+                pin(T);
             }
-            fetch_blk(jc, w, next);
+            fetch_blk(jc, w, u + 1);
             __builtin_amdgcn_sched_barrier(0);
         };
         // fragments of block J + 1 are read while J is multiplied
         Frag f0, f1;
-        load_frag(f0, 0);
-        load_frag(f1, 1);
+        load_frag(f0, st, buf, 0, lane);
+        load_frag(f1, st, buf, 1, lane);
         block(ic<0>{}, f0);
-        load_frag(f0, 2);
+        load_frag(f0, st, buf, 2, lane);
         block(ic<1>{}, f1);
-        load_frag(f1, 3);
+        load_frag(f1, st, buf, 3, lane);
         block(ic<2>{}, f0);
-        load_frag(f0, 4);
+        load_frag(f0, st, buf, 4, lane);
         block(ic<3>{}, f1);
-        load_frag(f1, 5);
+        load_frag(f1, st, buf, 5, lane);
         block(ic<4>{}, f0);
-        load_frag(f0, 6);
+        load_frag(f0, st, buf, 6, lane);
         block(ic<5>{}, f1);
-        load_frag(f1, 7);
+        load_frag(f1, st, buf, 7, lane);
         block(ic<6>{}, f0);
         block(ic<7>{}, f1);
     };
@@ -320,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
     // block by block; then u + 1's activations (loaded during u) are staged into the other buffer,
     // whose last reads were before the previous barrier, and u + 2's requested.
     WRaw w;
-    XRaw x;
+    ActStage::Raw x;
     fetch_blk(ic<0>{}, w, 0);
     fetch_blk(ic<1>{}, w, 0);
     fetch_blk(ic<2>{}, w, 0);
@@ -329,36 +360,191 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
     fetch_blk(ic<5>{}, w, 0);
     fetch_blk(ic<6>{}, w, 0);
     fetch_blk(ic<7>{}, w, 0);
-    fetch_x(x, 0);
-    stage(x, 0, 0);
-    fetch_x(x, 1);
+    st.fetch(x, 0);
+    st.stage(x, 0, 0);
+    st.fetch(x, 1);
     __syncthreads();
     for (int u = 0; u < nunit; ++u) {
         const int buf = u & 1;
         compute(w, buf, u);
-        stage(x, buf ^ 1, u + 1);  // past the end: zeros and copies, never read
-        fetch_x(x, u + 2);
+        st.stage(x, buf ^ 1, u + 1);  // past the end: zeros and copies, never read
+        st.fetch(x, u + 2);
         __syncthreads();
     }
+    store_tile(a, T, o0, m0, n, g);
+}
 
-    // lane (g, n) holds tokens 4g .. 4g+3 of each 16-token tile, weight row n of each 16-row tile
+// Q6_K (210-byte super-blocks: ql[128], qh[64], int8 scales[16], d f16): element l of 32-block j =
+// 4 h + g6 (h = j / 4, g6 = j % 4) is q = (nibble g6 / 2 of ql[64 h + 32 (g6 % 2) + l]) | (bits
+// 2 g6 .. 2 g6 + 1 of qh[32 h + l]) << 4, value d * sc[8 h + 2 g6 + l / 16] * (q - 32)
+// (kernel.cu:1122-1156); the block dot with Q8_1 is dw * dx * (sc0 dot(first 16) + sc1 dot(last 16))
+// (kernel.cu:2305-2402).  Lane group g holds elements 8g .. 8g+7 of a block, all under scale
+// 2 g6 + g / 2, so B = sc * (q - 32) carries the two scales of the block; |sc (q - 32)| <= 4096 is
+// not exact in fp16, so it is split as B1 = f16(sc (q - 32)) and B2 = fma(q - 32, sc, -B1), both exact
+// integers, and two MFMAs (A B1, then A B2 into the same D) give the block's integer dot exactly
+// (|dot| < 2^24); d * d8 is applied per block by a multiply and an fma per output.
+//
+// Alignment: 210 = 2 mod 4, so with 4-byte aligned rows of an even number of super-blocks, super-
+// block s starts at a multiple of 4 when s is even and 2 past one when s is odd; every 8-byte piece a
+// lane needs sits at a multiple of 8 within it and is read as 3 dwords from the aligned address at or
+// 2 before it, realigned by v_alignbyte_b32 with the super-block's offset.  Reads end at most 2 bytes
+// into the next super-block (even s: its scale and d dwords) or start at most 2 before (odd s).
+struct K6Raw {
+    uint32_t ql[4][3], qh[2][3], sd[5];
+};
+__device__ __forceinline__ void load3(uint32_t (&w)[3], const uint8_t *p) {
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+    w[0] = q[0];
+    w[1] = q[1];
+    w[2] = q[2];
+}
+__device__ __forceinline__ uint2 piece(const uint32_t (&w)[3], int off) {
+    return make_uint2(__builtin_amdgcn_alignbyte(w[1], w[0], off), __builtin_amdgcn_alignbyte(w[2], w[1], off));
+}
+
+__global__ __launch_bounds__(kThreads) void q6k_gemm_kernel(const GemmArgs a) {
+    extern __shared__ uint4 lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4, gb = g >> 1;
+    const int m0 = blockIdx.y * kBM;
+    const int o0 = blockIdx.x * kBN + wave * kNT * 16;
+    const ActStage st(lds, a, tid);
+    const int nsb = a.nblk / 8;  // super-blocks per row (even)
+
+    const uint8_t *wrow[kNT];
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-        const int o = o0 + t * 16 + n;
-        if (o >= a.n) continue;
+    for (int t = 0; t < kNT; ++t) wrow[t] = a.w + static_cast<size_t>(min(o0 + t * 16 + n, a.n - 1)) * a.rb;
+
+    f32x4 T[kMT][kNT];
 #pragma unroll
-        for (int i = 0; i < kMT; ++i)
+    for (int i = 0; i < kMT; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tk = m0 + i * 16 + 4 * g + r;
-                if (tk < a.m) a.y[static_cast<size_t>(tk) * a.n + o] = T[i][t][r];
+        for (int t = 0; t < kNT; ++t) T[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    struct WRaw {
+        K6Raw k[kNT];
+    };
+    // super-block s of the rows, past the end the last one of the same parity (valid, never used)
+    auto sbase = [&](int t, int s) {
+        s = min(s, nsb - 2 + (s & 1));
+        return wrow[t] + static_cast<size_t>(s) * 210 - 2 * (s & 1);  // the aligned address at or before
+    };
+    auto fetch_half = [&](WRaw &w, int s, int h) {
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+            const uint8_t *b = sbase(t, s);
+            load3(w.k[t].ql[2 * h], b + 64 * h + 8 * g);
+            load3(w.k[t].ql[2 * h + 1], b + 64 * h + 32 + 8 * g);
+            load3(w.k[t].qh[h], b + 128 + 32 * h + 8 * g);
+        }
+    };
+    auto fetch_sd = [&](WRaw &w, int s) {
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+            const uint32_t *q = reinterpret_cast<const uint32_t *>(sbase(t, s) + 192);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) w.k[t].sd[i] = q[i];
+        }
+    };
+
+    auto compute = [&](WRaw &w, int buf, int u) {
+        const int off = 2 * (u & 1);
+        // this unit's scales (realigned) and d, then the next unit's requested
+        uint32_t s4[kNT][4];
+        float dw[kNT];
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s4[t][i] = __builtin_amdgcn_alignbyte(w.k[t].sd[i + 1], w.k[t].sd[i], off);
+            dw[t] = f16_bits_to_f32((w.k[t].sd[4] >> (8 * off)) & 0xffffu);
+        }
+        fetch_sd(w, u + 1);
+        auto block = [&](auto jc, const Frag &f) {
+            constexpr int J = decltype(jc)::value, H = J >> 2, G6 = J & 3;
+            uint4 B1[kNT], B2[kNT];
+#pragma unroll
+            for (int t = 0; t < kNT; ++t) {
+                // scale 8 H + 2 G6 + g / 2 = byte 2 J + g / 2 of the 16, as the fp16 pair (sc, sc)
+                const uint32_t scb = (s4[t][J >> 1] >> (8 * (2 * (J & 1) + gb))) ^ 0x80u;
+                const f16x2 sc2 = u2h(__builtin_amdgcn_perm(0x64646464u, scb, 0x04000400u)) + splat(-1152.0f);
+                const uint2 l2 = piece(w.k[t].ql[2 * H + (G6 & 1)], off), h2 = piece(w.k[t].qh[H], off);
+                const uint32_t u0 = ((l2.x >> (4 * (G6 >> 1))) & 0x0f0f0f0fu) | (((h2.x >> (2 * G6)) & 0x03030303u) << 4);
+                const uint32_t u1 = ((l2.y >> (4 * (G6 >> 1))) & 0x0f0f0f0fu) | (((h2.y >> (2 * G6)) & 0x03030303u) << 4);
+                const f16x2 c32 = splat(-1056.0f);  // (q, 0x64) = 1024 + q
+                f16x2 q[4];
+                q[0] = u2h(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) + c32;
+                q[1] = u2h(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) + c32;
+                q[2] = u2h(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) + c32;
+                q[3] = u2h(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) + c32;
+                uint32_t b1[4], b2[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f16x2 p1 = q[e] * sc2;
+                    b1[e] = h2u(p1);
+                    b2[e] = h2u(__builtin_elementwise_fma(q[e], sc2, -p1));
+                }
+                B1[t] = make_uint4(b1[0], b1[1], b1[2], b1[3]);
+                B2[t] = make_uint4(b2[0], b2[1], b2[2], b2[3]);
             }
+#pragma unroll
+            for (int i = 0; i < kMT; ++i) {
+                const float d8r[4] = {f.d8[i].x, f.d8[i].y, f.d8[i].z, f.d8[i].w};
+#pragma unroll
+                for (int t = 0; t < kNT; ++t) {
+                    const f32x4 Dj = mfma(f.a[i], B2[t], mfma(f.a[i], B1[t], f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) T[i][t][r] = fmaf(Dj[r] * dw[t], d8r[r], T[i][t][r]);
+                }
+            }
+            pin(T);
+            if constexpr (J == 3) fetch_half(w, u + 1, 0);
+            if constexpr (J == 7) fetch_half(w, u + 1, 1);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        Frag f0, f1;
+        load_frag(f0, st, buf, 0, lane);
+        load_frag(f1, st, buf, 1, lane);
+        block(ic<0>{}, f0);
+        load_frag(f0, st, buf, 2, lane);
+        block(ic<1>{}, f1);
+        load_frag(f1, st, buf, 3, lane);
+        block(ic<2>{}, f0);
+        load_frag(f0, st, buf, 4, lane);
+        block(ic<3>{}, f1);
+        load_frag(f1, st, buf, 5, lane);
+        block(ic<4>{}, f0);
+        load_frag(f0, st, buf, 6, lane);
+        block(ic<5>{}, f1);
+        load_frag(f1, st, buf, 7, lane);
+        block(ic<6>{}, f0);
+        block(ic<7>{}, f1);
+    };
+
+    WRaw w;
+    ActStage::Raw x;
+    fetch_sd(w, 0);
+    fetch_half(w, 0, 0);
+    fetch_half(w, 0, 1);
+    st.fetch(x, 0);
+    st.stage(x, 0, 0);
+    st.fetch(x, 1);
+    __syncthreads();
+    for (int u = 0; u < nsb; ++u) {
+        const int buf = u & 1;
+        compute(w, buf, u);
+        st.stage(x, buf ^ 1, u + 1);
+        st.fetch(x, u + 2);
+        __syncthreads();
     }
+    store_tile(a, T, o0, m0, n, g);
 }
 
 }  // namespace
 
 bool qblk_gemm_ok(int type, const uint8_t *w, size_t rb, const uint8_t *xq, int in_dim) {
+    if (type == T_Q6_K)
+        return in_dim % 512 == 0 && rb % 4 == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0 &&
+               (reinterpret_cast<uintptr_t>(xq) & 3u) == 0;
     if (type != T_Q8_0 && type != T_Q5_0 && type != T_Q4_0) return false;
     return in_dim % 64 == 0 && rb % 4 == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0 &&
            (reinterpret_cast<uintptr_t>(xq) & 3u) == 0;
@@ -381,6 +567,7 @@ hipError_t qblk_gemm_q8_1(int type, const uint8_t *w, size_t rb, const uint8_t *
         case T_Q8_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q8_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
         case T_Q5_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q5_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
         case T_Q4_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q4_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
+        case T_Q6_K: hipLaunchKernelGGL(q6k_gemm_kernel, grid, dim3(kThreads), kLdsBytes, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

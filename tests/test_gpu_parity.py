@@ -355,6 +355,9 @@ def test_quantize_q8_1_bit_exact(raw):
                                                     # 0.75), row and token tails, one token
                                                     (Q8_0, 300, 4096, 70), (Q5_0, 2048, 1408, 96),
                                                     (Q4_0, 257, 192, 65), (Q8_0, 33, 64, 1), (Q5_0, 513, 2816, 17),
+                                                    # Q6_K on the matrix cores (K a multiple of 512): both
+                                                    # super-block parities, tails; K 768: per-element kernel
+                                                    (Q6_K, 1000, 2048, 65), (Q6_K, 513, 512, 17), (Q6_K, 24, 768, 5),
                                                     # K / 32 odd: rows not 4-byte aligned, the per-element kernel
                                                     (Q8_0, 40, 96, 5), (Q5_0, 24, 160, 3)])
 def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
