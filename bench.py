@@ -563,6 +563,73 @@ def wl_c4(args, torch, qlin, gen):
     return result
 
 
+def wl_prefill(args, torch, qlin, gen):
+    """The 32-block and Q6_K formats' matrix-core prefill GEMM (Q8_1 activations, 512 tokens, f16
+    N(0,1) values quantized in the step): DeepSeek-V2-Lite's Q6_K lm_head [102400, 2048] is the
+    headline; its Q5_0 expert down [2048, 1408] and a Qwen2.5-0.5B Q8_0 gate [4864, 896] are timed
+    alongside.  A step is quantize_q8_1 then the GEMM."""
+    M = 512
+    Q5_0 = 6
+    shapes = [("lm_head", Q6_K, 102400, 2048), ("expert_down", Q5_0, 2048, 1408), ("ffn_gate", Q8_0, 4864, 896)]
+    res = {}
+    for name, qt, N, K in shapes:
+        rb = qlin.row_bytes(qt, K)
+        w = synth_blocks(torch, qt, N, K, gen)
+        x = torch.randn(M, K, device="cuda", generator=gen).half().float()
+        xq = torch.empty(M * qlin.lib().qlin_q8_1_row_bytes(K), dtype=torch.uint8, device="cuda")
+        y = torch.empty(M, N, device="cuda")
+
+        def step(qt=qt, w=w, rb=rb, x=x, xq=xq, y=y, N=N, K=K):
+            qlin.quantize_q8_1(x, xq, K, M)
+            qlin.quant_matmul_q8_1(qt, w, rb, xq, y, N, K, M)
+
+        reps = max(10, args.steps // 2)
+        us_step = graph_us(torch, qlin, step, reps)
+        us_gemm = graph_us(torch, qlin, lambda qt=qt, w=w, rb=rb, xq=xq, y=y, N=N, K=K:
+                           qlin.quant_matmul_q8_1(qt, w, rb, xq, y, N, K, M), reps)
+        flops = 2.0 * M * N * K
+        res[name] = {"type": qt, "n": N, "k": K, "us_step": round(us_step, 2), "us_gemm": round(us_gemm, 2),
+                     "tflops_gemm": round(flops / us_gemm / 1e6, 1)}
+        log(f"prefill {name}: {us_step:.2f} us/step, GEMM {us_gemm:.2f} us ({flops / us_gemm / 1e6:.1f} TFLOP/s)")
+        if name == "lm_head":
+            head = (w, rb, x, N, K, us_step, us_gemm, flops)
+    w, rb, x, N, K, us_step, us_gemm, flops = head
+    result = {
+        "metric": "Q6_K x Q8_1 prefill GEMM TFLOP/s (DeepSeek-V2-Lite lm_head [102400, 2048], M=512)",
+        "value": round(flops / us_step / 1e6, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": max(10, args.steps // 2),
+        "warmup": 3, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (Q8_1 integers qx) x f16 (sc*(q-32) as two exact parts), f32 block sums scaled by d*d8",
+        "data": "synthetic (random Q6_K / Q5_0 / Q8_0 blocks; activations f16-rounded N(0,1) quantized to Q8_1 "
+                "in the step)",
+        "config": {"workload": "deepseek-prefill-gemm", "m": M, "k": K, "n": N, "weight_format": "Q6_K",
+                   "activation_format": "Q8_1", "algorithmic_flops_per_step": flops,
+                   "launches_per_step": ["quantize_q8_1", "quant_matmul_q8_1"], "execution": "hip graph replay",
+                   "shapes": res},
+        "roofline": {"bound": "mfma", "achieved": round(flops / us_gemm / 1e6, 1), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(flops / us_gemm / 1e6 / 2500.0, 4), "traffic": None,
+                     "kernel": "q6k_gemm_kernel (fp16 MFMA 16x16x32, two per block; peak = dense fp16)",
+                     "avg_launch_us": round(us_gemm, 3), "algorithmic_flops_per_launch": flops},
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        rows = 64
+        wh = w.view(N, -1)[:rows].contiguous().view(-1).cpu().numpy()
+        xqh = orc.quantize_q8_1(x.cpu().numpy(), K)
+        passes, t = 0, 0.0
+        while t < args.cpu_seconds:
+            t0 = time.perf_counter()
+            orc.matmul_q8_1(Q6_K, wh, rb, xqh, rows, K, M)
+            t += time.perf_counter() - t0
+            passes += 1
+        result["cpu_baseline"] = {
+            "value": round(2.0 * M * rows * K * passes / t / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
+            "kind": "port", "sample": f"{rows} of the {N} weight rows x {M} tokens x {K}, {passes} passes, "
+                                      f"{t:.1f} s; oracle orc_matmul_q8_1 (reference block-dot order, f64)"}
+    return result
+
+
 def wl_c5(args, torch, qlin, gen):
     """C5: a DeepSeek-V2-Lite MoE FFN layer for 16 decode tokens -- 64 routed experts of Q4_K gate/up
     [1408, 2048] and Q5_0 down [2048, 1408], router logits N(0,1), top-6 with scaling 1.0, plus the 2
@@ -740,7 +807,7 @@ def wl_moe_token(args, torch, qlin, gen):
 
 WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
              "c3-q8_0-decode-token": wl_c3, "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k,
-             "deepseek-moe-token": wl_moe_token}
+             "deepseek-moe-token": wl_moe_token, "deepseek-prefill-gemm": wl_prefill}
 
 
 def host_cpu() -> dict:

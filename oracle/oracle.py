@@ -62,6 +62,7 @@ def _declare(L: C.CDLL) -> None:
         "orc_q8_1_row_bytes": (SZ, [I]),
         "orc_quantize_q8_1": (None, [P, P, I, I, I]),
         "orc_matmul_q8_1": (I, [I, P, SZ, P, P, I, I, I]),
+        "orc_matmul_q8_1_mt": (I, [I, P, SZ, P, P, I, I, I, I]),
         "orc_router_topk": (None, [P, P, P, I, I, I, C.c_float]),
         "orc_swiglu": (I, [I, P, P, SZ, SZ, P, P, I, I]),
         "orc_swiglu_indexed": (I, [I, P, P, SZ, SZ, SZ, SZ, P, P, P, I, I, I]),
@@ -189,10 +190,12 @@ def quantize_q8_1(x: np.ndarray, in_dim: int, store_raw_sum: bool = False) -> np
     return out
 
 
-def matmul_q8_1(qtype: int, w: np.ndarray, rb: int, xq: np.ndarray, out_dim: int, in_dim: int, m: int) -> np.ndarray:
+def matmul_q8_1(qtype: int, w: np.ndarray, rb: int, xq: np.ndarray, out_dim: int, in_dim: int, m: int,
+                threads: int = 1) -> np.ndarray:
+    """threads: OpenMP threads over the rows (<= 0: all); the results do not depend on it."""
     xq = np.ascontiguousarray(xq, dtype=np.uint8)
     y = np.empty((m, out_dim), np.float64)
-    _ok(lib().orc_matmul_q8_1(qtype, _p(w), rb, _p(xq), _p(y), out_dim, in_dim, m), "matmul_q8_1")
+    _ok(lib().orc_matmul_q8_1_mt(qtype, _p(w), rb, _p(xq), _p(y), out_dim, in_dim, m, threads), "matmul_q8_1")
     return y
 
 

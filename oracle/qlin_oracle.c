@@ -378,13 +378,18 @@ void orc_quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, int store
  * Q8_0 / Q5_0 / Q4_0: sum of the dequantized weight times dx*qx. */
 int orc_matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y,
                     int out_dim, int in_dim, int m) {
+    return orc_matmul_q8_1_mt(type, w, row_bytes, xq, y, out_dim, in_dim, m, 1);
+}
+
+int orc_matmul_q8_1_mt(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y,
+                       int out_dim, int in_dim, int m, int threads) {
     if (check_shape(type, in_dim) || out_dim < 0 || m < 0) return -1;
     const int bpr = in_dim / 32;
     /* rows in parallel, each output element summed in the same order whatever the thread count */
-    const int nt = omp_get_max_threads();
+    const int nt = threads > 0 ? threads : omp_get_max_threads();
     float *wall = (float *)malloc(sizeof(float) * (size_t)in_dim * (size_t)nt);
     if (!wall) return -1;
-#pragma omp parallel for num_threads(nt) schedule(static)
+#pragma omp parallel for num_threads(nt) schedule(static) if (nt > 1)
     for (int o = 0; o < out_dim; ++o) {
         float *wr = wall + (size_t)omp_get_thread_num() * (size_t)in_dim;
         const uint8_t *row = w + (size_t)o * row_bytes;

@@ -113,6 +113,10 @@ void orc_quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, int store
  * double (the truth for the int8 prefill path).  Returns 0 or -1. */
 int orc_matmul_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y,
                     int out_dim, int in_dim, int m);
+/* the same with `threads` OpenMP threads over the rows (<= 0: all); every output is summed in
+ * the same order whatever the count */
+int orc_matmul_q8_1_mt(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, double *y,
+                       int out_dim, int in_dim, int m, int threads);
 
 /* MoE router: softmax over n_experts (non-finite -> -inf), k picks with strict '>' (lowest index
  * wins ties), w = p * routed_scaling, no renormalisation (kernel.cu:3463-3511). */
