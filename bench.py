@@ -630,6 +630,60 @@ def wl_prefill(args, torch, qlin, gen):
     return result
 
 
+def wl_floor(args, torch, qlin, gen):
+    """The decode step's launch structure with the kernels replaced by plain streaming reads
+    (qlin_probe_stream_read): per token M's 113 launches (per layer q/k/v, o, gate/up, down; then the
+    lm_head) each reading a distinct region of one buffer of the same size as its weights; the same 113
+    launches with nothing to read; and one launch reading all of a token's bytes.  The floor that any
+    113-launch kernel sequence over these bytes meets on this GPU."""
+    L = qlin.lib()
+    rbh, rbf = qlin.row_bytes(Q4_K, HIDDEN), qlin.row_bytes(Q4_K, FFN)
+    sizes = []
+    for _ in range(LAYERS):
+        sizes += [(HIDDEN + 2 * KV) * rbh, HIDDEN * rbh, 2 * FFN * rbh, HIDDEN * rbf]
+    sizes.append(VOCAB * rbh)
+    sizes = [(n + 255) // 256 * 256 for n in sizes]
+    total = sum(sizes)
+    buf = torch.empty(total, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    sink = torch.zeros(1, device="cuda")
+    base, sp = buf.data_ptr(), sink.data_ptr()
+
+    def launches(nbytes_of, wgs):
+        off = 0
+        for n in sizes:
+            rc = L.qlin_probe_stream_read(base + off, nbytes_of(n), wgs, sp)
+            if rc != 0:
+                raise qlin.QlinError("qlin_probe_stream_read", rc)
+            off += n
+
+    reps = max(5, args.steps // 4)
+    res = {}
+    for wgs in (1024, 2048, 4096):
+        res[f"reads_{wgs}_wg_us"] = round(graph_us(torch, qlin, lambda w=wgs: launches(lambda n: n, w), reps), 1)
+    res["empty_113_us"] = round(graph_us(torch, qlin, lambda: launches(lambda n: 0, 256), reps), 1)
+
+    def one():
+        rc = L.qlin_probe_stream_read(base, total, 4096, sp)
+        if rc != 0:
+            raise qlin.QlinError("qlin_probe_stream_read", rc)
+
+    res["one_launch_us"] = round(graph_us(torch, qlin, one, reps), 1)
+    best = min(v for k, v in res.items() if k.startswith("reads_"))
+    log(f"floor: 113 streaming launches {best:.1f} us/token, 113 empty launches {res['empty_113_us']:.1f} us, "
+        f"one launch of all {total / 1e9:.2f} GB {res['one_launch_us']:.1f} us")
+    return {
+        "metric": "decode-step streaming floor: 113 plain-read launches of M's bytes (tokens/s)",
+        "value": round(1e6 / best, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "ms_per_step": round(best / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8 (bytes read)", "data": "synthetic (a buffer of M's per-token bytes, contents irrelevant)",
+        "config": {"workload": "decode-stream-floor", "launches_per_step": len(sizes), "bytes_per_step": total,
+                   "gbs_at_floor": round(total / best / 1e3, 1),
+                   "pct_of_peak_at_floor": round(100 * total / best / 1e3 / PEAK_HBM_GBS, 2),
+                   "one_launch_gbs": round(total / res["one_launch_us"] / 1e3, 1), **res},
+    }
+
+
 def wl_c5(args, torch, qlin, gen):
     """C5: a DeepSeek-V2-Lite MoE FFN layer for 16 decode tokens -- 64 routed experts of Q4_K gate/up
     [1408, 2048] and Q5_0 down [2048, 1408], router logits N(0,1), top-6 with scaling 1.0, plus the 2
@@ -807,7 +861,8 @@ def wl_moe_token(args, torch, qlin, gen):
 
 WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
              "c3-q8_0-decode-token": wl_c3, "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k,
-             "deepseek-moe-token": wl_moe_token, "deepseek-prefill-gemm": wl_prefill}
+             "deepseek-moe-token": wl_moe_token, "deepseek-prefill-gemm": wl_prefill,
+             "decode-stream-floor": wl_floor}
 
 
 def host_cpu() -> dict:

@@ -76,6 +76,7 @@ SIGNATURES = {
     "qlin_launch_rms_norm": (I, [P, P, P, I, I, I, F, I]),
     "qlin_launch_rope_store_kv": (I, [P, P, P, P, P, I, I, I, I, I, P, F]),
     "qlin_launch_attend": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "qlin_probe_stream_read": (I, [P, SZ, I, P]),
     "qlin_launch_quant_embedding": (I, [I, P, P, P, SZ, I, I]),
     "qlin_launch_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
     "qlin_launch_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),
