@@ -125,6 +125,7 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #define QLIN_MFMA_MATMAJOR 1  // SwiGLU steps: 1 = all gate tiles, then all up tiles; 0 = tile-major
 #endif
 using plan::kMaxLds;
+using plan::kXPad;
 constexpr int kMaxXr = 10;              // float4 loads of x per thread: K <= 40 * threads
 
 // Weights per step chunk of one row, and its bytes.
@@ -221,17 +222,20 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     constexpr int XS = kSumElems<FMT>;
     const int nsb = a.nsb, K = nsb * CE;
     // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
-    // per 32 elements, in no more LDS than the bf16 layout takes (3K + K/4 against 4K + K/8 bytes).
+    // per 32 elements, in no more LDS than the bf16 layout takes (3 KP + K/4 against 4 KX + K/8 bytes).
     // Q5_0 has only this form.
     constexpr bool I8 = FMT == T_Q5_0 ||
                         ((FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0 || (FMT == T_Q6_K && QLIN_MFMA_I8_Q6K)) &&
                          (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) || (QLIN_MFMA_I8 == 3 && XR <= 2)));
     constexpr bool K32 = FMT == T_Q8_0 || FMT == T_Q5_0;  // 128-weight chunks: lane group g, block g
-    uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][K] bf16: hi, lo
-    float *xsum = reinterpret_cast<float *>(smem + 4 * K);         // [K/XS] sum(hi + lo) per XS elements
+    // The parts (digit planes) are kXPad bytes longer than K values: an A operand read gathers
+    // the same offset of 2 (3) of them, which then fall in different LDS banks.
+    const int KX = K + kXPad / 2, KP = K + kXPad;                  // bf16 part, int8 plane strides
+    uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);          // [2][KX] bf16: hi, lo
+    float *xsum = reinterpret_cast<float *>(smem + 4 * KX);        // [K/XS] sum(hi + lo) per XS elements
     float *partial = xsum + K / XS;                                // [rows][NW][nsb]
-    int8_t *planes = reinterpret_cast<int8_t *>(smem);                    // I8: [3][K]
-    float *sxp = reinterpret_cast<float *>(smem + 3 * static_cast<size_t>(K));  // I8: [K/32][2] (scale, sum)
+    int8_t *planes = reinterpret_cast<int8_t *>(smem);                    // I8: [3][KP]
+    float *sxp = reinterpret_cast<float *>(smem + 3 * static_cast<size_t>(KP));  // I8: [K/32][2] (scale, sum)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int bid = blockIdx.x;
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     const bool i8_on = (n >> 2) == g && (n & 3) < 3;
     // (Q6_K: lane group g's low-nibble group starts (g >> 1) * 128 + (g & 1) * 32 into the chunk, its
     // high-nibble group 64 further)
-    const int8_t *a8 = planes + (n & 3) * K +
+    const int8_t *a8 = planes + (n & 3) * KP +
                        (K32 ? 32 * g : FMT == T_Q6_K ? (g >> 1) * 128 + (g & 1) * 32 : 64 * g);  // when i8_on
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         const int j = n >> 1;
         // the unit's 32 x values: Q8_0 units 2b and 2b+1 are both block b
         const int xo = FMT == T_Q8_0 ? (j >> 1) * 32 : j * 32;
-        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * K + xo);
+        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * KX + xo);
         const uint8_t *zb = reinterpret_cast<const uint8_t *>(s_zero);
         a_lo = j == 2 * g ? xb : zb;
         a_lo_st = j == 2 * g ? 2 * CE : 0;
@@ -436,8 +440,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             x_digits4(xv[r], p1, p2, p3, sc, sm, sm16);
             if (i < K / 4) {
                 reinterpret_cast<uint32_t *>(planes)[i] = p1;
-                reinterpret_cast<uint32_t *>(planes + K)[i] = p2;
-                reinterpret_cast<uint32_t *>(planes + 2 * K)[i] = p3;
+                reinterpret_cast<uint32_t *>(planes + KP)[i] = p2;
+                reinterpret_cast<uint32_t *>(planes + 2 * KP)[i] = p3;
                 if constexpr (FMT == T_Q6_K) {
                     // scales per 32 [K/32], then x sums per 16 [K/16]
                     if ((i & 7) == 0) sxp[i >> 3] = sc;
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             if constexpr (XS == 32) sm += __shfl_xor(sm, 4, 64);
             if (i < K / 4) {
                 reinterpret_cast<uint2 *>(xpart)[i] = make_uint2(hp[0], hp[1]);
-                reinterpret_cast<uint2 *>(xpart + K)[i] = make_uint2(lp[0], lp[1]);
+                reinterpret_cast<uint2 *>(xpart + KX)[i] = make_uint2(lp[0], lp[1]);
                 if ((i & (XS / 4 - 1)) == 0) xsum[i / (XS / 4)] = sm;
             }
         }
@@ -719,7 +723,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
                 // Q6_K sub-block j = n >> 1 is (half j/4, group (j/2)%2 + 2 (j%2)) of 32 elements
                 const int j = n >> 1;
                 const int xo = p.sb * CE + (j >> 2) * 128 + (((j >> 1) & 1) + 2 * (j & 1)) * 32;
-                const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * K + xo);
+                const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * KX + xo);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const uint4 v = src[q];

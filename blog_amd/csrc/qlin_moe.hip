@@ -107,6 +107,62 @@ __global__ __launch_bounds__(64) void router_kernel(const float *__restrict__ lo
     }
 }
 
+// At most 64 experts: lane e holds expert e's logit, and pick r is the expert with exactly r experts
+// ahead of it (a larger logit, or an equal one at a lower index).  That is the order of router_kernel's
+// k successive wave argmaxes, found in one pass of compares against the logits in LDS instead of k
+// rounds of cross-lane reductions; the weights and the fallback for picks past the finite logits are
+// router_kernel's.
+__global__ __launch_bounds__(64) void router_rank_kernel(const float *__restrict__ logits, int *__restrict__ idx,
+                                                         float *__restrict__ wout, int ne, int k, float scaling) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float l = lane < ne ? logits[static_cast<size_t>(t) * ne + lane] : -INFINITY;
+    const float v = isfinite(l) ? l : -INFINITY;
+    const float maxv = wave_max(v);
+    __shared__ __attribute__((aligned(16))) float sv[64];
+    __shared__ __attribute__((aligned(16))) float ex[64];
+    sv[lane] = v;
+    ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;  // 0 for -inf and past ne
+    __syncthreads();
+    __shared__ float denom_s;
+    if (lane == 0) {
+        // in expert order, as router_kernel (and the reference's one thread per token) sums
+        float denom = 0.0f;
+        if (isfinite(maxv)) {
+            const int n4 = ne >> 2;
+            for (int i = 0; i < n4; ++i) {
+                const float4 q = reinterpret_cast<const float4 *>(ex)[i];
+                denom += q.x;
+                denom += q.y;
+                denom += q.z;
+                denom += q.w;
+            }
+            for (int e = 4 * n4; e < ne; ++e) denom += ex[e];
+        }
+        denom_s = denom;
+    }
+    // experts ahead of this one; past ne the logits are -inf, which are never ahead of a finite one
+    int ahead = 0;
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+        const float4 q = reinterpret_cast<const float4 *>(sv)[j];
+        ahead += (q.x > v || (q.x == v && 4 * j < lane)) + (q.y > v || (q.y == v && 4 * j + 1 < lane)) +
+                 (q.z > v || (q.z == v && 4 * j + 2 < lane)) + (q.w > v || (q.w == v && 4 * j + 3 < lane));
+    }
+    __syncthreads();
+    const float denom = denom_s;
+    const bool fin = v != -INFINITY;
+    const int nf = static_cast<int>(__popcll(__ballot(fin)));
+    if (fin && ahead < k) {
+        idx[static_cast<size_t>(t) * k + ahead] = lane;
+        wout[static_cast<size_t>(t) * k + ahead] = (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * scaling;
+    }
+    // every remaining logit is -inf: pick r falls back to expert r (or 0), with weight 0
+    for (int r = nf + lane; r < k; r += 64) {
+        idx[static_cast<size_t>(t) * k + r] = r < ne ? r : 0;
+        wout[static_cast<size_t>(t) * k + r] = 0.0f;
+    }
+}
+
 template <int T>
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu,
                                                         size_t g_eb, size_t u_eb, size_t g_rb, size_t u_rb,
@@ -229,8 +285,12 @@ hipError_t argmax(const float *logits, int n, int *out_idx, hipStream_t s) {
 hipError_t router_topk(const float *logits, int *top_idx, float *top_w, int tokens, int n_experts, int k,
                        float routed_scaling, hipStream_t s) {
     if (tokens == 0) return hipSuccess;
-    hipLaunchKernelGGL(router_kernel, dim3(tokens), dim3(64), 0, s, logits, top_idx, top_w, tokens,
-                       n_experts, k, routed_scaling);
+    if (n_experts <= 64)
+        hipLaunchKernelGGL(router_rank_kernel, dim3(tokens), dim3(64), 0, s, logits, top_idx, top_w, n_experts, k,
+                           routed_scaling);
+    else
+        hipLaunchKernelGGL(router_kernel, dim3(tokens), dim3(64), 0, s, logits, top_idx, top_w, tokens,
+                           n_experts, k, routed_scaling);
     return hipGetLastError();
 }
 

@@ -120,6 +120,7 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ ids
 #endif
 constexpr int kSWaves = 16;
 constexpr int kSThreads = kSWaves * 64;
+using plan::kXPad;
 
 // One step = 16 rows x one chunk of a row.
 //   Q4_K (gate/up): a chunk is one super-block; the A operand is the decode GEMV's block-diagonal
@@ -199,15 +200,18 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     static_assert(!SW || K4, "the SwiGLU pair is Q4_K");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int K = a.K, nblk = K / 32, nchunk = a.nchunk;
-    // staging of the pass's routes: Q4_K bf16 planes [NQ][2][K]; others slot vectors
-    // [NQ][2][nblk][tpb] (8 bf16 each); then the block sums X [NQ][nblk] and the step partials
-    // [NW][NQ][nchunk][rows of the piece]
-    // I8 (Q4_K): the routes' x as int8 digit planes [NQ][3][K] and (scale, sum) per 32 elements,
+    // staging of the pass's routes: Q4_K bf16 planes [NQ][2][KX]; others slot vectors
+    // [NQ][2][PS] (8 bf16 each, nblk * tpb of them and a pad); then the block sums X [NQ][nblk] and
+    // the step partials [NW][NQ][nchunk][rows of the piece]
+    // I8 (Q4_K): the routes' x as int8 digit planes [NQ][3][KP] and (scale, sum) per 32 elements,
     // in no more LDS than the bf16 planes (the plan is sized for those)
+    // The parts and planes are kXPad bytes longer than their values: an A-operand read gathers one
+    // offset of several of them, which then fall in different LDS banks.
     constexpr bool I8 = K4 && QLIN_STREAM_I8;
-    const size_t stage_bytes = I8   ? static_cast<size_t>(NQ) * 3 * K
-                               : K4 ? static_cast<size_t>(NQ) * 4 * K
-                                    : static_cast<size_t>(NQ) * 2 * nblk * F::tpb * 16;
+    const int KX = K + kXPad / 2, KP = K + kXPad, PS = nblk * F::tpb + kXPad / 16;
+    const size_t stage_bytes = I8   ? static_cast<size_t>(NQ) * 3 * KP
+                               : K4 ? static_cast<size_t>(NQ) * 4 * KX
+                                    : static_cast<size_t>(NQ) * 2 * PS * 16;
     uint16_t *xpart = reinterpret_cast<uint16_t *>(smem);
     uint4 *slots = reinterpret_cast<uint4 *>(smem);
     int8_t *planes = reinterpret_cast<int8_t *>(smem);
@@ -265,10 +269,10 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     const bool on_lo = (n >> 1) == 2 * g, on_hi = (n >> 1) == 2 * g + 1;
     // I8: row n is digit n & 3 (3: none) of sub-blocks 2g, 2g + 1 of lane group g = n >> 2
     const bool i8_on = (n >> 2) == g && (n & 3) < 3;
-    const int8_t *a8 = planes + (n & 3) * K + 64 * g;  // read only when i8_on
+    const int8_t *a8 = planes + (n & 3) * KP + 64 * g;  // read only when i8_on
     const uint8_t *a_lo, *a_hi;
     {
-        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * K + (n >> 1) * 32);
+        const uint8_t *xb = reinterpret_cast<const uint8_t *>(xpart + a_part * KX + (n >> 1) * 32);
         const uint8_t *zb = reinterpret_cast<const uint8_t *>(s_zero);
         a_lo = on_lo ? xb : zb;
         a_hi = on_hi ? xb : zb;
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 for (int q = 0; q < NQ; ++q) {
                     if (q >= nq) break;  // uniform
                     const i32x4 *pa = reinterpret_cast<const i32x4 *>(
-                        i8_on ? a8 + static_cast<size_t>(q) * 3 * K + p.ch * 256 : reinterpret_cast<const int8_t *>(s_zero));
+                        i8_on ? a8 + static_cast<size_t>(q) * 3 * KP + p.ch * 256 : reinterpret_cast<const int8_t *>(s_zero));
                     i32x4 de = mfma_i8(pa[0], b0, i32x4{0, 0, 0, 0});
                     de = mfma_i8(pa[1], b1, de);
                     i32x4 dq = mfma_i8(pa[2], b2, i32x4{0, 0, 0, 0});
@@ -393,8 +397,8 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
                     if (q >= nq) break;  // uniform
-                    // route q's planes start 4K bytes after route q-1's; a chunk is 512 bytes of a plane
-                    const int off = q * 4 * K + p.ch * 512;
+                    // route q's planes start 4 KX bytes after route q-1's; a chunk is 512 bytes of a plane
+                    const int off = q * 4 * KX + p.ch * 512;
                     const u32x4 *pl = reinterpret_cast<const u32x4 *>(a_lo + (on_lo ? off : 0));
                     const u32x4 *ph = reinterpret_cast<const u32x4 *>(a_hi + (on_hi ? off : 0));
                     f32x4 D = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -432,8 +436,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
 #pragma unroll
                 for (int q = 0; q < NQ; q += 2) {
                     if (q >= nq) break;  // uniform
-                    const uint4 *src = a_active ? slots + ((static_cast<size_t>(q + a_pair) * 2 + a_part) * nblk + blk) *
-                                                              F::tpb
+                    const uint4 *src = a_active ? slots + (static_cast<size_t>(q + a_pair) * 2 + a_part) * PS + blk * F::tpb
                                                 : s_zero;
                     f32x4 D = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -468,10 +471,10 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                     uint32_t p1, p2, p3;
                     float sc, sm, sm16;
                     x_digits4(v, p1, p2, p3, sc, sm, sm16);
-                    uint32_t *pq = reinterpret_cast<uint32_t *>(planes + static_cast<size_t>(q) * 3 * K);
+                    uint32_t *pq = reinterpret_cast<uint32_t *>(planes + static_cast<size_t>(q) * 3 * KP);
                     pq[c] = p1;
-                    pq[K / 4 + c] = p2;
-                    pq[K / 2 + c] = p3;
+                    pq[KP / 4 + c] = p2;
+                    pq[KP / 2 + c] = p3;
                     if ((c & 7) == 0) reinterpret_cast<float2 *>(xsum)[q * nblk + (c >> 3)] = make_float2(sc, sm);
                 }
             } else if constexpr (K4) {
@@ -492,9 +495,9 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                     sm += __shfl_xor(sm, 1, 64);
                     sm += __shfl_xor(sm, 2, 64);
                     sm += __shfl_xor(sm, 4, 64);
-                    uint16_t *xp = xpart + static_cast<size_t>(q) * 2 * K;
+                    uint16_t *xp = xpart + static_cast<size_t>(q) * 2 * KX;
                     reinterpret_cast<uint2 *>(xp)[c] = make_uint2(hp[0], hp[1]);
-                    reinterpret_cast<uint2 *>(xp + K)[c] = make_uint2(lp[0], lp[1]);
+                    reinterpret_cast<uint2 *>(xp + KX)[c] = make_uint2(lp[0], lp[1]);
                     if ((c & 7) == 0) xsum[q * nblk + (c >> 3)] = sm;
                 }
             } else {
@@ -529,11 +532,11 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                     }
 #pragma unroll
                     for (int m = 1; m < F::tpb; m <<= 1) sm += __shfl_xor(sm, m, 64);
-                    uint4 *dst = slots + (static_cast<size_t>(q) * 2 * nblk + blk) * F::tpb + t;
+                    uint4 *dst = slots + static_cast<size_t>(q) * 2 * PS + blk * F::tpb + t;
                     dst[0] = make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),
                                         hb[6] | (hb[7] << 16));
-                    dst[static_cast<size_t>(nblk) * F::tpb] = make_uint4(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16),
-                                                                         lb[4] | (lb[5] << 16), lb[6] | (lb[7] << 16));
+                    dst[PS] = make_uint4(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16), lb[4] | (lb[5] << 16),
+                                         lb[6] | (lb[7] << 16));
                     if (t == 0) xsum[q * nblk + blk] = sm;
                 }
             }

@@ -15,10 +15,15 @@ namespace qlin {
 namespace plan {
 
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per CU on gfx950
+// Padding of each staged x part (bf16 hi or lo, int8 digit plane) past its K values, in bytes: an
+// A-operand read gathers one offset of several parts, and a part length that is a multiple of the
+// LDS bank row (256 bytes) would put them all in the same banks.  16 bytes (one b128 read) shifts
+// each part by 4 banks.  Staging of a route (one x) takes 4K + 2 kXPad bytes as bf16 parts.
+constexpr int kXPad = 16;
 
 // The decode GEMV (qlin_mfma_gemv.hip): one workgroup per CU over `total` rows of nsb chunks of
-// k / nsb weights.  Dynamic LDS: x in the bf16 layout (4 bytes per element, which the int8 digit
-// planes never exceed), the x sums (one float per sum_elems elements) and one partial per (row,
+// k / nsb weights.  Dynamic LDS: x in the bf16 layout (4K + 2 kXPad bytes, which the int8 digit
+// planes, 3 (K + kXPad) bytes and their sums, never exceed), the x sums (one float per sum_elems elements) and one partial per (row,
 // matrix, chunk) of the workgroup's rows.  interleave: workgroup b takes 16-row tiles b, b + G, ...
 struct Gemv {
     int grid = 0;
@@ -32,7 +37,7 @@ inline Gemv gemv(int total, int k, int nsb, bool swiglu, int sum_elems, int cu_c
     const uint64_t steps = static_cast<uint64_t>((rows + 15) / 16) * (swiglu ? 2 : 1) * static_cast<uint64_t>(nsb);
     p.magic_exact = steps * static_cast<uint64_t>(nsb) < (uint64_t{1} << 32);
     const size_t K = static_cast<size_t>(k);
-    p.lds = 4 * K + (K / static_cast<size_t>(sum_elems)) * sizeof(float) +
+    p.lds = 4 * K + 2 * kXPad + (K / static_cast<size_t>(sum_elems)) * sizeof(float) +
             static_cast<size_t>(rows) * (swiglu ? 2 : 1) * static_cast<size_t>(nsb) * sizeof(float);
     return p;
 }
@@ -41,8 +46,9 @@ inline bool gemv_fits(const Gemv &p, size_t static_lds) {
 }
 
 // The grouped MoE streaming kernels (qlin_moe_grouped.hip): routes per pass nq (4, else 2), and the
-// tiles whose partials fit in LDS at once.  Dynamic LDS: the pass's routes' staged x (Q4_K 4 bytes
-// per element; the 32-weight formats tpb 16-byte slot vectors per block and hi / lo part), one x sum
+// tiles whose partials fit in LDS at once.  Dynamic LDS: the pass's routes' staged x (Q4_K 4K +
+// 2 kXPad bytes; the 32-weight formats tpb 16-byte slot vectors per block and hi / lo part, each part
+// kXPad bytes longer), one x sum
 // per 32 elements and route, and per tile nw * nq * nchunk * 16 partials.  The selected experts are
 // only known on the device, so a piece is sized for twice an even share of min(E, R) of them.
 struct StreamFmt {
@@ -66,8 +72,8 @@ inline Stream stream(const StreamFmt &f, bool swiglu, int rows, int K, int E, in
         const size_t st = nq == 4 ? static_nq4 : static_nq2;
         if (st >= kMaxLds) continue;
         const size_t budget = kMaxLds - st;
-        const size_t stage = f.q4k ? static_cast<size_t>(nq) * 4 * K
-                                   : static_cast<size_t>(nq) * 2 * nblk * f.tpb * 16;
+        const size_t stage = f.q4k ? static_cast<size_t>(nq) * (4 * K + 2 * kXPad)
+                                   : static_cast<size_t>(nq) * 2 * (nblk * f.tpb * 16 + kXPad);
         const size_t fixed = stage + static_cast<size_t>(nq) * nblk * sizeof(float);
         const size_t per_tile = static_cast<size_t>(nw) * nq * nchunk * 16 * sizeof(float);
         if (fixed + per_tile > budget) continue;

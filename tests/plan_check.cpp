@@ -37,13 +37,15 @@ int main() {
                         }
                     }
     CHECK(accepted > 0 && refused > 0);
-    // the edge: one row (grid 1, one 16-row tile), K = 256 n: 4K + K/32 * 4 + 16 n * 4 = 1120 n bytes
+    // the edge: one row (grid 1, one 16-row tile), K = 256 n: 4K + 2 pads + K/32 * 4 + 16 n * 4 =
+    // 1120 n + 2 kXPad bytes
     {
-        const int n_edge = static_cast<int>(kMaxLds / 1120);
+        const size_t pad = 2 * kXPad;
+        const int n_edge = static_cast<int>((kMaxLds - pad) / 1120);
         const Gemv e = gemv(1, 256 * n_edge, n_edge, false, 32, 256, true);
-        CHECK(e.lds == 1120u * n_edge);
-        CHECK(gemv_fits(e, kMaxLds - 1120 * n_edge));
-        CHECK(!gemv_fits(e, kMaxLds - 1120 * n_edge + 1));
+        CHECK(e.lds == 1120u * n_edge + pad);
+        CHECK(gemv_fits(e, kMaxLds - 1120 * n_edge - pad));
+        CHECK(!gemv_fits(e, kMaxLds - 1120 * n_edge - pad + 1));
         CHECK(!gemv_fits(gemv(1, 256 * (n_edge + 1), n_edge + 1, false, 32, 256, true), 0));
     }
     CHECK(!gemv_fits(gemv(16, 256, 1, false, 32, 256, true), kMaxLds));  // a kernel that cannot be read
@@ -62,9 +64,10 @@ int main() {
                         CHECK(p.piece >= 1);
                         CHECK(p.lds + st <= kMaxLds);
                     }
-    // Q4_K SwiGLU at the edge of four routes per pass: fixed = 4*4K + 4*K/32*4, per tile 2*4*nchunk*64
+    // Q4_K SwiGLU at the edge of four routes per pass: fixed = 4*(4K + 2 pads) + 4*K/32*4, per tile
+    // 2*4*nchunk*64
     {
-        auto need4 = [](int K) { return 16L * K + K / 2 + 2L * 4 * (K / 256) * 64; };
+        auto need4 = [](int K) { return 16L * K + 8L * kXPad + K / 2 + 2L * 4 * (K / 256) * 64; };
         int K = 256;
         while (need4(K + 256) <= static_cast<long>(kMaxLds)) K += 256;
         const size_t st_fit = kMaxLds - need4(K);

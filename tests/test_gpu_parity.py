@@ -401,19 +401,24 @@ def test_q4k_gemm_c4_shape_every_row():
 
 # ---- MoE ----------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("ne", [64, 100, 256])
-def test_router_topk(ne):
-    rng = np.random.default_rng(71 + ne)
+# up to 64 experts take the one-pass rank kernel, more the k-round argmax kernel
+@pytest.mark.parametrize("ne,k", [(4, 6), (8, 6), (63, 6), (64, 6), (64, 8), (100, 6), (256, 6)])
+def test_router_topk(ne, k):
+    rng = np.random.default_rng(71 + ne + k)
     logits = rng.standard_normal((16, ne)).astype(np.float32)
-    logits[3, :] = 0.5                 # all tied: 0..5 in order
-    logits[4, 7] = np.nan
-    logits[5, :] = np.nan              # nothing finite
-    logits[6, [9, 4, ne - 4]] = 9.0    # tie at the top
-    logits[7, ne - 1] = np.inf         # non-finite -> -inf
-    idx_d = torch.zeros((16, 6), dtype=torch.int32, device="cuda")
-    w_d = empty_f32(16, 6)
-    qlin.call("qlin_launch_moe_router_topk", dev(logits), idx_d, w_d, 16, ne, 6, 1.0)
-    idx_r, w_r = orc.router_topk(logits, 6, 1.0)
+    logits[3, :] = 0.5                                   # all tied: 0..k-1 in order
+    logits[4, 7 % ne] = np.nan
+    logits[5, :] = np.nan                                # nothing finite
+    logits[6, [9 % ne, 4 % ne, ne - 4 if ne > 4 else 1]] = 9.0   # tie at the top
+    logits[7, ne - 1] = np.inf                           # non-finite -> -inf
+    logits[8, :] = -np.inf                               # two finite: the rest fall back to expert r
+    logits[8, [ne - 1, ne // 2]] = [0.25, 0.75]
+    logits[9, :] = rng.integers(-2, 3, ne).astype(np.float32)  # many ties
+    scaling = 1.5
+    idx_d = torch.zeros((16, k), dtype=torch.int32, device="cuda")
+    w_d = empty_f32(16, k)
+    qlin.call("qlin_launch_moe_router_topk", dev(logits), idx_d, w_d, 16, ne, k, scaling)
+    idx_r, w_r = orc.router_topk(logits, k, scaling)
     assert np.array_equal(host(idx_d), idx_r)
     assert np.allclose(host(w_d), w_r, rtol=1e-5, atol=1e-7)
 
