@@ -31,6 +31,9 @@ constexpr int kGroup = 4;  // routes of one expert per pass of the per-element k
 constexpr int kMaxExperts = 1024;
 constexpr int kRouteBits = 21;  // routes per call < 2^21: the expert scan packs (count, selected)
 constexpr int kIdsChunk = 4096;
+// The gate/up streaming launch groups the routes itself (in LDS) up to these sizes.
+constexpr int kFuseRoutes = 1024;
+constexpr int kFuseExperts = 256;
 
 struct Groups {
     int *offset;  // [E + 1] first position of expert e in list
@@ -159,6 +162,11 @@ struct StreamArgs {
     float *out;              // gate/up: act [R, rows]; down: per-route results [R, rows]
     int rows, K, nchunk, tpe;  // rows per expert, inner dimension, chunks per row, 16-row tiles per expert
     int piece;                 // tiles whose step partials fit in LDS at once
+    // grouping in the kernel (GRP): the routes' expert ids, their count and the expert count; the
+    // groups are built in LDS from these, and workgroup 0 writes them to gr for the later launches
+    const int *ids;
+    int R, ne;
+    Groups gr;
 };
 
 // 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
@@ -192,7 +200,7 @@ __device__ __forceinline__ int64_t tile_cost(int cnt) {
 }
 
 // SW: gate and up matrices with SiLU(gate) * up out (Q4_K); otherwise one matrix, its dot out.
-template <int FMT, int NQ, bool SW>
+template <int FMT, int NQ, bool SW, bool GRP>
 __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     using F = StepFmt<FMT>;
     constexpr bool K4 = FMT == T_Q4_K;  // super-block steps, block-diagonal A
@@ -224,14 +232,99 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int nsel = *a.nsel;
-    if (nsel == 0) return;  // uniform
     if (tid < 8) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);  // before the barriers below
+
+    // GRP: the routes grouped by expert here, as group_kernel does (a stable counting sort, invalid
+    // ids left out), into LDS: one launch and two dependent reads (the count, then the records) fewer
+    // before the first weights are requested.  The ids are staged in the (still unused) x staging area.
+    __shared__ int s_list[GRP ? kFuseRoutes : 1];
+    __shared__ int4 s_seg[GRP ? kFuseExperts : 1];
+    __shared__ int s_scan[kSWaves];
+    __shared__ int s_off[GRP ? kFuseExperts : 1];
+    __shared__ int s_nsel;
+    if constexpr (GRP) {
+        const int R = a.R, E = a.ne;
+        int *sids = reinterpret_cast<int *>(smem);
+        const int4 *sids4 = reinterpret_cast<const int4 *>(smem);
+        for (int i = tid; i < ((R + 15) & ~15); i += kSThreads) sids[i] = i < R ? a.ids[i] : -1;
+        __syncthreads();
+        // routes i .. i + 15 (below lim) with expert e
+        auto count16 = [&](int i, int e, int lim = 0x7fffffff) {
+            int c = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int4 v = sids4[i / 4 + j];
+                const int b = i + 4 * j;
+                c += (v.x == e && b < lim) + (v.y == e && b + 1 < lim) + (v.z == e && b + 2 < lim) +
+                     (v.w == e && b + 3 < lim);
+            }
+            return c;
+        };
+        int c = 0;
+        if (tid < E)
+            for (int i = 0; i < R; i += 16) c += count16(i, tid);
+        // exclusive scan over the experts of count | selected << kRouteBits: the first list
+        // position of each expert and the records of the selected ones
+        const int v = tid < E ? c | (static_cast<int>(c > 0) << kRouteBits) : 0;
+        int inc = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int t = __shfl_up(inc, d, 64);
+            if (lane >= d) inc += t;
+        }
+        const int nw = (E + 63) / 64;  // the waves that hold experts
+        if (lane == 63 && wave < nw) s_scan[wave] = inc;
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < min(wave, nw); ++w) before += s_scan[w];
+        const int excl = before + inc - v;
+        constexpr int kMask = (1 << kRouteBits) - 1;
+        const int pos0 = excl & kMask;
+        if (tid < E) s_off[tid] = pos0;
+        if (tid < E && c > 0) s_seg[excl >> kRouteBits] = make_int4(tid, pos0, c, 0);
+        if (tid == 0) {
+            int total = 0;
+            for (int w = 0; w < nw; ++w) total += s_scan[w];
+            s_nsel = total >> kRouteBits;
+            if (blockIdx.x == 0) {
+                a.gr.offset[E] = total & kMask;
+                *a.gr.nsel = total >> kRouteBits;
+            }
+        }
+        if (blockIdx.x == 0 && tid < E) a.gr.offset[tid] = pos0;
+        __syncthreads();
+        // route r goes after the earlier routes of its expert (thread r counts them)
+        if (tid < R) {
+            const int e = sids[tid];
+            if (e >= 0 && e < E) {
+                int rank = 0;
+                const int full = tid & ~15;
+                for (int i = 0; i < full; i += 16) rank += count16(i, e);
+                rank += count16(full, e, tid);
+                s_list[s_off[e] + rank] = tid;
+            }
+        }
+        __syncthreads();  // the groups are complete; the staging area is free again
+        if (blockIdx.x == 0) {
+            const int nsel = s_nsel;
+            for (int i = tid; i < R; i += kSThreads) a.gr.list[i] = s_list[i];  // past the valid routes: unread
+            if (tid < nsel) a.gr.seg[tid] = s_seg[tid];
+        }
+    }
+    const int *lst = GRP ? s_list : a.list;
+    const int4 *segs = GRP ? s_seg : a.seg;
+    // (otherwise the records' counts are read with the number of them, not after it: the entries
+    // past that number are not used)
+    int seg_cnt = 0;
+    if (!GRP && tid < a.ne) seg_cnt = a.seg[tid].z;
+    const int nsel = GRP ? s_nsel : *a.nsel;
+    if (nsel == 0) return;  // uniform
 
     // Each workgroup takes an equal share of the total cost, in tiles: tile t of selected expert s
     // starts at cost s_pref[s] + t * tile_cost and belongs to the workgroup whose range holds that.
     {
-        const int64_t v = tid < nsel ? static_cast<int64_t>(a.tpe) * tile_cost<FMT, NQ>(a.seg[tid].z) : 0;
+        const int64_t v =
+            tid < nsel ? static_cast<int64_t>(a.tpe) * tile_cost<FMT, NQ>(GRP ? segs[tid].z : seg_cnt) : 0;
         int64_t inc = v;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
@@ -295,7 +388,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     for (int s = uni(s_first); s < nsel; ++s) {
         const int64_t ps = uni(s_pref[s]);
         if (ps >= c1) break;
-        const int4 sg = a.seg[s];
+        const int4 sg = segs[s];
         const int e = uni(sg.x), beg = uni(sg.y), cnt = uni(sg.z);
         const int64_t ct = tile_cost<FMT, NQ>(cnt);
         const int lt0 = static_cast<int>(max(ceil_div(c0 - ps, ct), int64_t{0}));
@@ -466,7 +559,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 const int per = K / 4;  // float4s per route, a multiple of 64: whole waves per route
                 for (int it = tid; it < nq * per; it += kSThreads) {
                     const int q = it / per, c = it - q * per;
-                    const int route = a.list[beg + q0 + q];
+                    const int route = lst[beg + q0 + q];
                     const float4 v = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(route / a.x_div) * K)[c];
                     uint32_t p1, p2, p3;
                     float sc, sm, sm16;
@@ -481,7 +574,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 const int per = K / 4;  // float4s per route, a multiple of 64: whole waves per route
                 for (int it = tid; it < nq * per; it += kSThreads) {
                     const int q = it / per, c = it - q * per;
-                    const int route = a.list[beg + q0 + q];
+                    const int route = lst[beg + q0 + q];
                     const float4 v = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(route / a.x_div) * K)[c];
                     uint32_t hp[2], lp[2];  // (element 2i, 2i + 1) as bf16 pairs
                     float sm = 0.0f;
@@ -506,7 +599,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 const int per = nblk * F::tpb;
                 for (int it = tid; it < nq * per; it += kSThreads) {
                     const int q = it / per, rem = it - q * per, blk = rem / F::tpb, t = rem - blk * F::tpb;
-                    const int route = a.list[beg + q0 + q];
+                    const int route = lst[beg + q0 + q];
                     const float4 *xr = reinterpret_cast<const float4 *>(
                         a.x + static_cast<size_t>(route / a.x_div) * K + blk * 32);
                     float xe[8];
@@ -566,7 +659,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                         v0 += pq[ch * pstride];
                         if constexpr (SW) v1 += pq[(static_cast<size_t>(NQ) * nchunk + ch) * pstride];
                     }
-                    const int route = a.list[beg + q0 + q];
+                    const int route = lst[beg + q0 + q];
                     a.out[static_cast<size_t>(route) * a.rows + r0 + lr] = SW ? v0 / (1.0f + expf(-v0)) * v1 : v0;
                 }
                 pt0 += a.piece;
@@ -780,11 +873,11 @@ using plan::kMaxLds;
 
 // The static LDS of one streaming-kernel instantiation, as compiled (cost prefix, scan totals,
 // zero operands, step counter), read once; kMaxLds if it cannot be read, so no plan takes it.
-template <int FMT, int NQ, bool SW>
+template <int FMT, int NQ, bool SW, bool GRP>
 size_t stream_static_lds() {
     static const size_t v = [] {
         hipFuncAttributes fa{};
-        return hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&stream_kernel<FMT, NQ, SW>)) == hipSuccess
+        return hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&stream_kernel<FMT, NQ, SW, GRP>)) == hipSuccess
                    ? fa.sharedSizeBytes
                    : kMaxLds;
     }();
@@ -796,22 +889,22 @@ size_t stream_static_lds() {
 // kernels take the call.
 using StreamPlan = plan::Stream;
 
-template <int FMT, bool SW>
+template <int FMT, bool SW, bool GRP = false>
 StreamPlan stream_plan(int rows, int K, int E, int R) {
     using F = StepFmt<FMT>;
     const plan::StreamFmt f{F::ce, FMT == T_Q4_K, F::tpb};
-    return plan::stream(f, SW, rows, K, E, R, device_info().cu_count, stream_static_lds<FMT, 4, SW>(),
-                        stream_static_lds<FMT, 2, SW>());
+    return plan::stream(f, SW, rows, K, E, R, device_info().cu_count, stream_static_lds<FMT, 4, SW, GRP>(),
+                        stream_static_lds<FMT, 2, SW, GRP>());
 }
 
-template <int FMT, int NQ, bool SW>
+template <int FMT, int NQ, bool SW, bool GRP>
 hipError_t launch_stream_nq(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((stream_kernel<FMT, NQ, SW>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
+    hipLaunchKernelGGL((stream_kernel<FMT, NQ, SW, GRP>), dim3(p.grid), dim3(kSThreads), p.lds, s, a);
     return hipGetLastError();
 }
-template <int FMT, bool SW>
+template <int FMT, bool SW, bool GRP = false>
 hipError_t launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s) {
-    return p.nq == 4 ? launch_stream_nq<FMT, 4, SW>(p, a, s) : launch_stream_nq<FMT, 2, SW>(p, a, s);
+    return p.nq == 4 ? launch_stream_nq<FMT, 4, SW, GRP>(p, a, s) : launch_stream_nq<FMT, 2, SW, GRP>(p, a, s);
 }
 
 // The streaming down kernel reads Q5_0 / Q8_0 4-block chunks as aligned dwords (88 and 136 bytes,
@@ -831,8 +924,9 @@ bool down_stream_ok(int type, const uint8_t *w, size_t eb, size_t rb, int ffn) {
 // the batched decode on this array instead of a workspace of their own.  Each GPU the library runs
 // on holds its own copy until the process ends, and every call on that GPU shares it: calls that
 // overlap on one GPU race.  Nothing in it has to start at zero: each call writes every word of it
-// that it reads (group_kernel the offsets, lists and selected experts; the streaming launches the
-// activations and route results they hand on).
+// that it reads (group_kernel, or workgroup 0 of the gate/up launch that groups the routes itself,
+// the offsets, lists and selected experts; the streaming launches the activations and route
+// results they hand on).
 namespace {
 static __device__ __align__(256) uint8_t scratch[kMoeStaticScratchBytes];
 }  // namespace
@@ -892,13 +986,23 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
     p += align256(static_cast<size_t>(R) * ffn * sizeof(float));
     float *yr = reinterpret_cast<float *>(p);
 
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, ids, R, E, gr);
-
-    const StreamPlan up = stream_plan<T_Q4_K, true>(ffn, K, E, R);
+    // The gate/up streaming launch groups the routes itself when they fit its LDS arrays and its
+    // staging area holds the ids; otherwise group_kernel writes the groups first.
+    StreamPlan up = R <= kFuseRoutes && E <= kFuseExperts ? stream_plan<T_Q4_K, true, true>(ffn, K, E, R)
+                                                          : StreamPlan{};
+    const bool grp = up.ok && up.lds >= static_cast<size_t>((R + 15) & ~15) * sizeof(int);
+    if (!grp) {
+        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, ids, R, E, gr);
+        up = stream_plan<T_Q4_K, true>(ffn, K, E, R);
+    }
     if (up.ok) {
-        const StreamArgs ua{wg,  wu,  g_eb, g_rb,   x,         k,          gr.list, gr.seg,
-                            gr.nsel, act, ffn, K, K / 256, (ffn + 15) / 16, up.piece};
-        const hipError_t e = launch_stream<T_Q4_K, true>(up, ua, s);
+        StreamArgs ua{wg,  wu,  g_eb, g_rb,   x,         k,          gr.list, gr.seg,
+                      gr.nsel, act, ffn, K, K / 256, (ffn + 15) / 16, up.piece};
+        ua.ids = ids;
+        ua.R = R;
+        ua.ne = E;
+        ua.gr = gr;
+        const hipError_t e = grp ? launch_stream<T_Q4_K, true, true>(up, ua, s) : launch_stream<T_Q4_K, true>(up, ua, s);
         if (e != hipSuccess) return e;
     } else {
         const UpArgs ua{wg, wu, g_eb, g_rb, x, gr, act, ffn, K, k};
@@ -914,8 +1018,9 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
     }
     if (dn.ok) {
         const int nchunk = ffn / (d_type == T_Q4_K ? 256 : 128);
-        const StreamArgs da{wd,      wd, d_eb,   d_rb, act,    1,                  gr.list, gr.seg,
-                            gr.nsel, yr, hidden, ffn,  nchunk, (hidden + 15) / 16, dn.piece};
+        StreamArgs da{wd,      wd, d_eb,   d_rb, act,    1,                  gr.list, gr.seg,
+                      gr.nsel, yr, hidden, ffn,  nchunk, (hidden + 15) / 16, dn.piece};
+        da.ne = E;
         const hipError_t e = d_type == T_Q5_0   ? launch_stream<T_Q5_0, false>(dn, da, s)
                              : d_type == T_Q8_0 ? launch_stream<T_Q8_0, false>(dn, da, s)
                                                 : launch_stream<T_Q4_K, false>(dn, da, s);

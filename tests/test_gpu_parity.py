@@ -664,6 +664,20 @@ def test_moe_grouped_skewed_routing():
     assert normwise_rel_err(got, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("E,tokens,k", [(300, 40, 4), (64, 300, 4)])
+def test_moe_grouped_beyond_in_kernel_grouping(E, tokens, k):
+    """More experts (300) or routes (1200) than the gate/up launch groups in its own LDS: the separate
+    grouping launch writes the groups, and the streaming launches read them."""
+    ffn, hid = 256, 256
+    wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(Q4_K, Q5_0, E, ffn, hid, tokens, k, 361 + E)
+    ids[1, 0] = -1
+    out0 = np.zeros((tokens, hid), np.float32)
+    banner(f"moe grouped beyond in-kernel grouping E={E} R={tokens * k}")
+    got = _run_grouped(Q4_K, Q5_0, wg, wu, wdn, E, ffn, hid, x, ids, rw, out0)
+    ref = _moe_batch_ref(Q4_K, Q5_0, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(got, ref) <= 1e-4
+
+
 def test_moe_grouped_wide_input_two_routes_per_pass():
     """in_dim 10240: four routes' staged activations would not fit in LDS, so gate/up runs two routes
     per pass; every expert has more than two routes (4 experts, 8 tokens x 2 routes)."""
