@@ -9,6 +9,7 @@
 #include <cstdint>
 
 #include "qlin.h"
+#include "qlin_decoder.h"
 #include "qlin_internal.hpp"
 
 namespace qlin {
@@ -171,6 +172,48 @@ int qlin_launch_quant_gemv_multi(int type, int n_mats, const uint8_t *const *wei
     int rc = check_f32(x, work);
     if (rc || !work) return rc;
     return launched(qlin::gemv_multi(type, weights, ys, out_dims, n_mats, rb, x, in_dim, stream()));
+}
+
+int qlin_launch_rms_norm_quant_gemv_multi(int type, int n_mats, const uint8_t *const *weights, size_t rb,
+                                          const float *x, const uint16_t *norm_weight, int norm_type, float eps,
+                                          int one_plus, float *const *ys, const int *out_dims, int in_dim) {
+    if (n_mats < 0 || (norm_type != 0 && norm_type != 1)) return QLIN_ERR_SHAPE;
+    if (n_mats > qlin::kMaxStreamMats) return QLIN_ERR_LIMIT;
+    if (n_mats == 0) return QLIN_OK;
+    if (!weights || !ys || !out_dims) return QLIN_ERR_NULL;
+    bool work = false;
+    int total = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        int rc = check_weight(type, weights[i], rb, out_dims[i], in_dim);
+        if (rc) return rc;
+        if ((rc = check_f32(ys[i], out_dims[i] > 0))) return rc;
+        work = work || out_dims[i] > 0;
+        total += out_dims[i];
+    }
+    int rc = check_f32(x, work);
+    if (rc || !work) return rc;
+    if (!norm_weight) return QLIN_ERR_NULL;
+    if (!aligned(norm_weight, 2)) return QLIN_ERR_ALIGN;
+    if (!qlin::mfma_ok(type, weights, n_mats, rb, x, total, in_dim, false)) return QLIN_ERR_LIMIT;
+    const qlin::RmsNorm norm{norm_weight, norm_type, eps, one_plus};
+    return launched(qlin::mfma_gemv(type, weights, ys, out_dims, n_mats, rb, x, in_dim, false, stream(), &norm));
+}
+
+int qlin_launch_rms_norm_quant_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x,
+                                      const uint16_t *norm_weight, int norm_type, float eps, int one_plus,
+                                      float *act, int ffn_dim, int in_dim) {
+    if (norm_type != 0 && norm_type != 1) return QLIN_ERR_SHAPE;
+    int rc = check_weight(type, wg, rb, ffn_dim, in_dim);
+    if (rc || (rc = check_weight(type, wu, rb, ffn_dim, in_dim))) return rc;
+    const bool work = ffn_dim > 0;
+    if ((rc = check_f32(x, work)) || (rc = check_f32(act, work))) return rc;
+    if (!work) return QLIN_OK;
+    if (!norm_weight) return QLIN_ERR_NULL;
+    if (!aligned(norm_weight, 2)) return QLIN_ERR_ALIGN;
+    const uint8_t *gu[2] = {wg, wu};
+    if (!qlin::mfma_ok(type, gu, 2, rb, x, ffn_dim, in_dim, true)) return QLIN_ERR_LIMIT;
+    const qlin::RmsNorm norm{norm_weight, norm_type, eps, one_plus};
+    return launched(qlin::mfma_swiglu(type, wg, wu, rb, x, act, ffn_dim, in_dim, stream(), &norm));
 }
 
 size_t qlin_q8_1_row_bytes(int in_dim) {

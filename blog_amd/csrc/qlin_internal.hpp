@@ -31,13 +31,23 @@ hipError_t q4k_stream_gemv(const uint8_t *const *w, float *const *y, const int *
 hipError_t q4k_stream_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
                              int ffn_dim, int in_dim, hipStream_t s);
 
-// Matrix-core decode kernels (m == 1) for Q4_K, Q4_0, Q8_0, Q5_0 and Q6_K, same contracts as the streaming ones.
+// An RMSNorm applied to x as the decode kernels stage it: x[j] * rsqrt(mean x^2 + eps) * w[j], w bf16
+// (type 0) or f16 (1), plus one if one_plus.
+struct RmsNorm {
+    const uint16_t *w;
+    int type;
+    float eps;
+    int one_plus;
+};
+// Matrix-core decode kernels (m == 1) for Q4_K, Q4_0, Q8_0, Q5_0 and Q6_K, same contracts as the streaming ones;
+// with norm, x is first normalized (in the staging, not in memory).
 bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
              bool swiglu);
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat,
-                     size_t row_bytes, const float *x, int in_dim, bool add, hipStream_t s);
+                     size_t row_bytes, const float *x, int in_dim, bool add, hipStream_t s,
+                     const RmsNorm *norm = nullptr);
 hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
-                       int ffn_dim, int in_dim, hipStream_t s);
+                       int ffn_dim, int in_dim, hipStream_t s, const RmsNorm *norm = nullptr);
 // The routed-expert forms (qlin_mfma_gemv.hip): route r's weights are expert ids[r]'s (negative: none).
 // SwiGLU: act[r, o] = silu(Wg[e_r] x) (Wu[e_r] x), 0 for no expert.  Down: out[h] += the routes' dots
 // Wd[e_r][h] . act[r] added in route order as fmaf(dot, rw[r], total).  mfma_routed_ok takes the

@@ -165,6 +165,11 @@ struct MfmaArgs {
     size_t eb;
     int routes, route_rows, cpr;
     uint32_t route_magic, cpr_magic;
+    // RMSNorm of x fused into the staging (norm_w non-null; the plain launches only): x is used as
+    // x[j] * rsqrt(mean x^2 + eps) * w[j], w bf16 (norm_type 0) or f16 (1), plus one if one_plus
+    const uint16_t *norm_w;
+    int norm_type, norm_one_plus;
+    float norm_eps;
 };
 
 constexpr int kMaxRoutes = 16;  // routes of one routed launch (top-k of one token)
@@ -421,6 +426,43 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     float4 xv[XR];
 #pragma unroll
     for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
+    if (!ROUTED && a.norm_w) {  // uniform
+        // the norm weights are requested with x; the sum of squares over the workgroup (each thread
+        // its float4s in order, then the wave, then the waves in order)
+        uint32_t nw[XR][4];
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const uint16_t *np = a.norm_w + 4 * min(tid + r * kThreads, K / 4 - 1);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) nw[r][c] = np[c];
+        }
+        __shared__ float s_ss[kWaves];
+        float ss = 0.0f;
+#pragma unroll
+        for (int r = 0; r < XR; ++r)
+            if (tid + r * kThreads < K / 4)
+                ss += xv[r].x * xv[r].x + xv[r].y * xv[r].y + xv[r].z * xv[r].z + xv[r].w * xv[r].w;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) s_ss[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) tot += s_ss[w];
+        const float inv = rsqrtf(tot / static_cast<float>(K) + a.norm_eps);
+        auto nv = [&](uint32_t b) {
+            const float v = a.norm_type == 0 ? __builtin_bit_cast(float, b << 16)
+                                             : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+            return a.norm_one_plus ? v + 1.0f : v;
+        };
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            xv[r].x = xv[r].x * inv * nv(nw[r][0]);
+            xv[r].y = xv[r].y * inv * nv(nw[r][1]);
+            xv[r].z = xv[r].z * inv * nv(nw[r][2]);
+            xv[r].w = xv[r].w * inv * nv(nw[r][3]);
+        }
+    }
     if constexpr (ROUTED) {
         // the routes' experts (and down weights): every weight address depends on them
         if (tid < a.routes) {
@@ -1109,9 +1151,18 @@ bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t rb, const float
     return prepare(type, a, k, swiglu, false).ok;
 }
 
+void set_norm(MfmaArgs &a, const RmsNorm *norm) {
+    if (!norm) return;
+    a.norm_w = norm->w;
+    a.norm_type = norm->type;
+    a.norm_one_plus = norm->one_plus;
+    a.norm_eps = norm->eps;
+}
+
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat, size_t rb,
-                     const float *x, int k, bool add, hipStream_t s) {
+                     const float *x, int k, bool add, hipStream_t s, const RmsNorm *norm) {
     MfmaArgs a = base_args(type, rb, x, k);
+    set_norm(a, norm);
     int total = 0;
     for (int i = 0; i < nmat; ++i) {
         a.w[i] = w[i];
@@ -1127,9 +1178,10 @@ hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const i
 }
 
 hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x, float *act, int ffn,
-                       int k, hipStream_t s) {
+                       int k, hipStream_t s, const RmsNorm *norm) {
     if (ffn == 0) return hipSuccess;
     MfmaArgs a = base_args(type, rb, x, k);
+    set_norm(a, norm);
     a.w[0] = wg;
     a.w[1] = wu;
     a.y[0] = act;

@@ -76,6 +76,8 @@ SIGNATURES = {
     "qlin_launch_rms_norm": (I, [P, P, P, I, I, I, F, I]),
     "qlin_launch_rope_store_kv": (I, [P, P, P, P, P, I, I, I, I, I, P, F]),
     "qlin_launch_attend": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "qlin_launch_rms_norm_quant_gemv_multi": (I, [I, I, P, SZ, P, P, I, F, I, P, P, I]),
+    "qlin_launch_rms_norm_quant_swiglu": (I, [I, P, P, SZ, P, P, I, F, I, P, I, I]),
     "qlin_probe_stream_read": (I, [P, SZ, I, P]),
     "qlin_launch_quant_embedding": (I, [I, P, P, P, SZ, I, I]),
     "qlin_launch_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
@@ -195,6 +197,16 @@ def quant_gemv_multi(qtype, ws, rb, x, ys, out_dims, in_dim):
     ya = (C.c_void_p * n)(*[ptr(y) for y in ys])
     da = (C.c_int * n)(*out_dims)
     call("qlin_launch_quant_gemv_multi", qtype, n, C.addressof(wa), rb, x, C.addressof(ya), C.addressof(da), in_dim)
+
+
+def rms_norm_quant_gemv_multi(qtype, ws, rb, x, norm_w, norm_type, eps, one_plus, ys, out_dims, in_dim):
+    """quant_gemv_multi of rms_norm(x), in one launch (lists of tensors / device addresses)."""
+    n = len(ws)
+    wa = (C.c_void_p * n)(*[ptr(w) for w in ws])
+    ya = (C.c_void_p * n)(*[ptr(y) for y in ys])
+    da = (C.c_int * n)(*out_dims)
+    call("qlin_launch_rms_norm_quant_gemv_multi", qtype, n, C.addressof(wa), rb, x, norm_w, norm_type, eps, one_plus,
+         C.addressof(ya), C.addressof(da), in_dim)
 
 
 def quant_swiglu(qtype, wg, wu, g_rb, u_rb, x, act, ffn_dim, in_dim):

@@ -24,6 +24,17 @@
  * (else QLIN_ERR_LIMIT); n_heads a multiple of kv_heads and head_dim of 4 (else QLIN_ERR_SHAPE);
  * qlin_launch_attend reads q, the caches and attn as 16-byte vectors (16-byte aligned, else
  * QLIN_ERR_ALIGN).
+ *
+ * The RMSNorm fused into the decode linear that consumes it (no counterpart in the reference, whose
+ * decode step runs launch_rms_norm and then launch_quant_gemv / launch_quant_swiglu on its output):
+ *   qlin_launch_rms_norm_quant_gemv_multi  qlin_launch_quant_gemv_multi (one row, n_mats matrices that
+ *                              share x) of rms_norm(x), the norm's arguments as qlin_launch_rms_norm's;
+ *   qlin_launch_rms_norm_quant_swiglu      qlin_launch_quant_swiglu (gate and up of one row stride) of
+ *                              rms_norm(x).
+ * The decode kernels normalize x as they stage it (the normalized vector is not written), in one
+ * launch instead of two.  They take the shapes of the matrix-core decode kernels (every format, in_dim
+ * a multiple of 256, or 128 for Q8_0 and Q5_0, x 16-byte aligned); other shapes return
+ * QLIN_ERR_LIMIT, for the two-launch form.
  */
 #ifndef QLIN_DECODER_H
 #define QLIN_DECODER_H
@@ -42,6 +53,12 @@ int qlin_launch_rope_store_kv(float *q, const float *k, const float *v, float *k
                               float rope_theta);
 int qlin_launch_attend(const float *q, const float *key_cache, const float *value_cache, float *attn, int rows,
                        int n_heads, int kv_heads, int head_dim, int max_seq_len, const int *start_pos_dev);
+int qlin_launch_rms_norm_quant_gemv_multi(int type, int n_mats, const uint8_t *const *weights, size_t row_bytes,
+                                          const float *x, const uint16_t *norm_weight, int norm_type, float eps,
+                                          int one_plus, float *const *ys, const int *out_dims, int in_dim);
+int qlin_launch_rms_norm_quant_swiglu(int type, const uint8_t *w_gate, const uint8_t *w_up, size_t row_bytes,
+                                      const float *x, const uint16_t *norm_weight, int norm_type, float eps,
+                                      int one_plus, float *act, int ffn_dim, int in_dim);
 
 #ifdef __cplusplus
 }

@@ -141,6 +141,86 @@ def test_rms_norm(rows, hidden, wtype, one_plus):
     assert normwise_rel_err(host(out), ref) <= 1e-6
 
 
+def _norm_weights(rng, hidden, wtype):
+    w16 = (rng.standard_normal(hidden) * 0.5 + 1).astype(np.float16)
+    if wtype == 0:
+        bits = (w16.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        return bits, (bits.astype(np.uint32) << 16).view(np.float32)
+    return w16.view(np.uint16), w16.astype(np.float32)
+
+
+def _rms_ref(x, wv, one_plus):
+    x64 = x.astype(np.float64)
+    return (x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * (wv.astype(np.float64) + one_plus)).astype(np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype,hidden,outs,wtype,one_plus", [
+    (qgen.Q8_0, 896, [896, 128, 128], 0, 0),      # C3's q/k/v
+    (qgen.Q8_0, 896, [151936], 0, 0),             # C3's tied head
+    (qgen.Q4_K, 3584, [3584, 512, 512], 1, 1),
+    (qgen.Q6_K, 1024, [300], 0, 1),
+    (qgen.Q5_0, 1152, [200], 1, 0),
+    (qgen.Q4_0, 768, [40, 88], 0, 0)])
+def test_rms_norm_fused_gemv(qtype, hidden, outs, wtype, one_plus):
+    """The RMSNorm inside the decode GEMV's staging: y = W rms_norm(x), against the oracle's product
+    with the normalized x, and against the two launches it replaces."""
+    torch = _gpu()
+    from gpu_util import banner, dev, empty_f32, host
+    from blog_amd import qlin
+    rng = np.random.default_rng(hidden + len(outs))
+    x = (rng.standard_normal(hidden) * 3).astype(np.float32)
+    bits, wv = _norm_weights(rng, hidden, wtype)
+    mats = [qgen.random_matrix(qtype, n, hidden, seed=500 + i) for i, n in enumerate(outs)]
+    rb = mats[0][1]
+    ys = [empty_f32(n) for n in outs]
+    banner(f"rms_norm fused gemv type={qtype} hidden={hidden} outs={outs}")
+    qlin.rms_norm_quant_gemv_multi(qtype, [dev(w) for w, _, _ in mats], rb, dev(x), dev(bits), wtype, 1e-6,
+                                   one_plus, ys, outs, hidden)
+    xn = _rms_ref(x, wv, one_plus)
+    xn_d, ys2 = empty_f32(1, hidden), [empty_f32(n) for n in outs]
+    qlin.call("qlin_launch_rms_norm", dev(x), xn_d, dev(bits), wtype, 1, hidden, 1e-6, one_plus)
+    qlin.quant_gemv_multi(qtype, [dev(w) for w, _, _ in mats], rb, xn_d, ys2, outs, hidden)
+    for (w, _, _), y, y2, n in zip(mats, ys, ys2, outs):
+        ref = orc.matmul_f64(qtype, w, rb, xn[None, :], n, hidden)[0]
+        assert normwise_rel_err(host(y), ref) <= 1e-5
+        assert normwise_rel_err(host(y), host(y2)) <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype,hidden,ffn", [(qgen.Q8_0, 896, 4864), (qgen.Q4_K, 3584, 18944), (qgen.Q4_0, 512, 100)])
+def test_rms_norm_fused_swiglu(qtype, hidden, ffn):
+    torch = _gpu()
+    from gpu_util import banner, dev, empty_f32, host
+    from blog_amd import qlin
+    rng = np.random.default_rng(hidden + ffn)
+    x = (rng.standard_normal(hidden) * 3).astype(np.float32)
+    bits, wv = _norm_weights(rng, hidden, 0)
+    wg, rb, _ = qgen.random_matrix(qtype, ffn, hidden, seed=520)
+    wu, _, _ = qgen.random_matrix(qtype, ffn, hidden, seed=521)
+    act = empty_f32(ffn)
+    banner(f"rms_norm fused swiglu type={qtype} hidden={hidden} ffn={ffn}")
+    qlin.call("qlin_launch_rms_norm_quant_swiglu", qtype, dev(wg), dev(wu), rb, dev(x), dev(bits), 0, 1e-6, 0, act,
+              ffn, hidden)
+    ref = orc.swiglu(qtype, wg, wu, rb, rb, _rms_ref(x, wv, 0), ffn, hidden)
+    assert normwise_rel_err(host(act), ref) <= 1e-4
+
+
+@pytest.mark.gpu
+def test_rms_norm_fused_unsupported_shape():
+    """An in_dim the matrix-core decode kernels do not take is refused, not run."""
+    torch = _gpu()
+    from gpu_util import dev, empty_f32
+    from blog_amd import qlin
+    w, rb, _ = qgen.random_matrix(qgen.Q8_0, 16, 96, seed=530)
+    x = np.ones(96, np.float32)
+    bits = np.full(96, 0x3f80, np.uint16)
+    y = empty_f32(16)
+    rc = qlin.status("qlin_launch_rms_norm_quant_swiglu", qgen.Q8_0, dev(w), dev(w), rb, dev(x), dev(bits), 0, 1e-6,
+                     0, y, 16, 96)
+    assert rc == 5  # QLIN_ERR_LIMIT
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,start", [(1, 0), (1, 37), (32, 0), (5, 250), (3, 509), (1, 600)])
 def test_rope_store_and_attend(rows, start):

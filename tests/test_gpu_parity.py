@@ -678,6 +678,25 @@ def test_moe_grouped_beyond_in_kernel_grouping(E, tokens, k):
     assert normwise_rel_err(got, ref) <= 1e-4
 
 
+def test_moe_grouped_unaligned_output():
+    """An output 4 bytes past a 16-byte boundary."""
+    E, ffn, hid, tokens, k = 8, 256, 256, 4, 2
+    wg, wu, grb, geb, wdn, drb, deb, x, ids, rw = _moe_batch(Q4_K, Q5_0, E, ffn, hid, tokens, k, 371)
+    ids[2, 1] = -1
+    out0 = np.random.default_rng(11).standard_normal((tokens, hid)).astype(np.float32)
+    nbytes = qlin.lib().qlin_moe_grouped_workspace_bytes(tokens, k, E, ffn, hid)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
+    wsp = (ws.data_ptr() + 255) // 256 * 256
+    buf = dev(np.concatenate([np.zeros(1, np.float32), out0.ravel()]))
+    out_d = buf[1:]
+    assert out_d.data_ptr() % 16 == 4
+    banner("moe grouped unaligned output")
+    qlin.call("qlin_moe_routed_decode_grouped", Q4_K, dev(wg), dev(wu), wg.size, Q5_0, dev(wdn), wdn.size, E,
+              ffn, hid, hid, dev(x), dev(ids), dev(rw), wsp, nbytes, out_d, tokens, k)
+    ref = _moe_batch_ref(Q4_K, Q5_0, wg, wu, grb, geb, wdn, drb, deb, x, ids, rw, out0, ffn, hid)
+    assert normwise_rel_err(host(out_d).reshape(tokens, hid) - out0, ref - out0) <= 1e-4
+
+
 def test_moe_grouped_wide_input_two_routes_per_pass():
     """in_dim 10240: four routes' staged activations would not fit in LDS, so gate/up runs two routes
     per pass; every expert has more than two routes (4 experts, 8 tokens x 2 routes)."""
