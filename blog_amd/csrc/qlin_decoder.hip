@@ -107,12 +107,22 @@ constexpr int kAttnThreads = 256;
 // the softmax.  Output: thread (class c, float4 column d4) adds the weighted value rows of positions
 // c, c + C, ... (C = 256 / (head_dim / 4) classes), 8 rows' loads in flight at a time; the classes'
 // sums are added in class order.
+// ROPE (one decode row): the rotary embedding and the cache store of rope_store_kernel done here as
+// well -- q and the row's key rotated into LDS, the row's position scored and weighted from LDS (so
+// no workgroup reads the cache row written in this launch), and the first query head of each key
+// head's group writing the rotated key and the value into the caches for the later rows.  Every value
+// is computed as the two kernels compute it, in the same order.
+template <bool ROPE>
 __global__ __launch_bounds__(kAttnThreads) void attend_kernel(const float *__restrict__ q, const float *__restrict__ kc,
                                                               const float *__restrict__ vc, float *__restrict__ out,
                                                               int n_heads, int kv_heads, int hd, int max_seq,
-                                                              const int *__restrict__ start_pos) {
+                                                              const int *__restrict__ start_pos,
+                                                              const float *__restrict__ k_row,
+                                                              const float *__restrict__ v_row, float *__restrict__ kc_w,
+                                                              float *__restrict__ vc_w, float theta) {
     extern __shared__ float4 smem4[];
     __shared__ float red[kAttnThreads / 64];
+    __shared__ float4 s_krow[ROPE ? 64 : 1], s_vrow[ROPE ? 64 : 1];  // the row's key and value (head_dim <= 256)
     const int n4 = hd / 4;
     float4 *qs = smem4;                                       // [n4]
     float *sc = reinterpret_cast<float *>(smem4 + n4);        // [max(max_seq, 4 * ... class sums)]
@@ -123,22 +133,56 @@ __global__ __launch_bounds__(kAttnThreads) void attend_kernel(const float *__res
     const float4 *kb = reinterpret_cast<const float4 *>(kc) + static_cast<size_t>(kh) * n4;
     const float4 *vb = reinterpret_cast<const float4 *>(vc) + static_cast<size_t>(kh) * n4;
     const float4 *qh = reinterpret_cast<const float4 *>(q) + (static_cast<size_t>(row) * n_heads + h) * n4;
-    for (int d = tid; d < n4; d += kAttnThreads) qs[d] = qh[d];
-    __syncthreads();
+    if constexpr (ROPE) {
+        // pairs (i, i + hd/2) rotated by pos / theta^(2i / hd), as rope_store_kernel
+        const int half = hd / 2;
+        float *qf = reinterpret_cast<float *>(qs), *kf = reinterpret_cast<float *>(s_krow);
+        const float *qsrc = reinterpret_cast<const float *>(qh);
+        const float *ksrc = k_row + static_cast<size_t>(kh) * hd, *vsrc = v_row + static_cast<size_t>(kh) * hd;
+        if (tid < half) {
+            const float inv_freq = 1.0f / powf(theta, static_cast<float>(2 * tid) / static_cast<float>(hd));
+            const float angle = static_cast<float>(pos) * inv_freq;
+            const float c = cosf(angle), sn = sinf(angle);
+            const float q1 = qsrc[tid], q2 = qsrc[tid + half], k1 = ksrc[tid], k2 = ksrc[tid + half];
+            qf[tid] = q1 * c - q2 * sn;
+            qf[tid + half] = q2 * c + q1 * sn;
+            kf[tid] = k1 * c - k2 * sn;
+            kf[tid + half] = k2 * c + k1 * sn;
+        }
+        for (int d = tid; d < hd; d += kAttnThreads) reinterpret_cast<float *>(s_vrow)[d] = vsrc[d];
+        __syncthreads();
+        if (h % (n_heads / kv_heads) == 0) {
+            const size_t dst = (static_cast<size_t>(pos) * kv_heads + kh) * hd;
+            for (int d = tid; d < hd; d += kAttnThreads) {
+                kc_w[dst + d] = reinterpret_cast<const float *>(s_krow)[d];
+                vc_w[dst + d] = reinterpret_cast<const float *>(s_vrow)[d];
+            }
+        }
+    } else {
+        for (int d = tid; d < n4; d += kAttnThreads) qs[d] = qh[d];
+        __syncthreads();
+    }
     const float scale = rsqrtf(static_cast<float>(hd));
     float mx = -INFINITY;
     for (int j = tid; j < n; j += kAttnThreads) {
         const float4 *kj = kb + static_cast<size_t>(j) * stride4;
         float dot = 0.0f;
-        for (int c = 0; c < n4; c += 16) {
-            float4 kv[16];
+        if (ROPE && j == pos) {
+            for (int c = 0; c < n4; ++c) {
+                const float4 a = qs[c], kv = s_krow[c];
+                dot += a.x * kv.x + a.y * kv.y + a.z * kv.z + a.w * kv.w;
+            }
+        } else {
+            for (int c = 0; c < n4; c += 16) {
+                float4 kv[16];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) kv[u] = c + u < n4 ? kj[c + u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int u = 0; u < 16; ++u) kv[u] = c + u < n4 ? kj[c + u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                if (c + u < n4) {
-                    const float4 a = qs[c + u];
-                    dot += a.x * kv[u].x + a.y * kv[u].y + a.z * kv[u].z + a.w * kv[u].w;
+                for (int u = 0; u < 16; ++u) {
+                    if (c + u < n4) {
+                        const float4 a = qs[c + u];
+                        dot += a.x * kv[u].x + a.y * kv[u].y + a.z * kv[u].z + a.w * kv[u].w;
+                    }
                 }
             }
         }
@@ -163,7 +207,9 @@ __global__ __launch_bounds__(kAttnThreads) void attend_kernel(const float *__res
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int j = j0 + u * C;
-                vv[u] = j < n ? vb[static_cast<size_t>(j) * stride4 + d4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                vv[u] = j >= n                 ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                        : (ROPE && j == pos) ? s_vrow[d4]
+                                             : vb[static_cast<size_t>(j) * stride4 + d4];
                 pp[u] = j < n ? sc[j] : 0.0f;
             }
 #pragma unroll
@@ -249,8 +295,27 @@ int qlin_launch_attend(const float *q, const float *key_cache, const float *valu
     const size_t slots = static_cast<size_t>(qlin::kAttnThreads) * 4;
     const size_t lds = static_cast<size_t>(head_dim) * sizeof(float) +
                        (static_cast<size_t>(max_seq_len) > slots ? max_seq_len : slots) * sizeof(float);
-    hipLaunchKernelGGL(qlin::attend_kernel, dim3(rows, n_heads), dim3(qlin::kAttnThreads), lds, qlin::current_stream(),
-                       q, key_cache, value_cache, attn, n_heads, kv_heads, head_dim, max_seq_len, start_pos_dev);
+    hipLaunchKernelGGL(qlin::attend_kernel<false>, dim3(rows, n_heads), dim3(qlin::kAttnThreads), lds,
+                       qlin::current_stream(), q, key_cache, value_cache, attn, n_heads, kv_heads, head_dim,
+                       max_seq_len, start_pos_dev, nullptr, nullptr, nullptr, nullptr, 0.0f);
+    return qlin::launched(hipGetLastError());
+}
+
+int qlin_launch_rope_attend(const float *q, const float *k, const float *v, float *key_cache, float *value_cache,
+                            float *attn, int n_heads, int kv_heads, int head_dim, int max_seq_len,
+                            const int *start_pos_dev, float rope_theta) {
+    int rc = check_heads(1, n_heads, kv_heads, head_dim, max_seq_len);
+    if (rc) return rc;
+    if (!q || !k || !v || !key_cache || !value_cache || !attn || !start_pos_dev) return QLIN_ERR_NULL;
+    if (!qlin::al16(q) || !qlin::al4(k) || !qlin::al4(v) || !qlin::al16(key_cache) || !qlin::al16(value_cache) ||
+        !qlin::al16(attn) || !qlin::al4(start_pos_dev))
+        return QLIN_ERR_ALIGN;
+    const size_t slots = static_cast<size_t>(qlin::kAttnThreads) * 4;
+    const size_t lds = static_cast<size_t>(head_dim) * sizeof(float) +
+                       (static_cast<size_t>(max_seq_len) > slots ? max_seq_len : slots) * sizeof(float);
+    hipLaunchKernelGGL(qlin::attend_kernel<true>, dim3(1, n_heads), dim3(qlin::kAttnThreads), lds,
+                       qlin::current_stream(), q, key_cache, value_cache, attn, n_heads, kv_heads, head_dim,
+                       max_seq_len, start_pos_dev, k, v, key_cache, value_cache, rope_theta);
     return qlin::launched(hipGetLastError());
 }
 

@@ -90,12 +90,13 @@ class Qwen2Decoder:
     positions in all."""
 
     def __init__(self, torch, cfg: Qwen2Config, weights: dict, max_seq: int = 512, max_prompt: int = 64,
-                 fuse_norm: bool = True):
+                 fuse: bool = True):
         self.torch, self.cfg, self.w = torch, cfg, weights
         self.max_seq, self.max_prompt = max_seq, max_prompt
         # decode steps: each RMSNorm inside the launch of the linear that consumes it (the matrix-core
-        # decode kernels take in_dim in whole 128-weight chunks for Q8_0)
-        self.fuse_norm = fuse_norm and cfg.hidden % 128 == 0
+        # decode kernels take in_dim in whole 128-weight chunks for Q8_0), and the rotary embedding with
+        # the cache store inside the attention launch
+        self.fuse = fuse and cfg.hidden % 128 == 0
         dev, f32, i32 = "cuda", torch.float32, torch.int32
         H, F, P = cfg.hidden, cfg.ffn, max_prompt
         self.rb_h = qlin.row_bytes(cfg.wtype, H)
@@ -133,7 +134,7 @@ class Qwen2Decoder:
         H, F, QD, KD = c.hidden, c.ffn, c.q_dim, c.kv_dim
         h, xn, q, k, v, attn, act = (t(self.h), t(self.xn), t(self.q), t(self.k), t(self.v), t(self.attn),
                                      t(self.act))
-        fuse = rows == 1 and self.fuse_norm
+        fuse = rows == 1 and self.fuse
         for i, W in enumerate(self.w["layers"]):
             if fuse:
                 qlin.rms_norm_quant_gemv_multi(c.wtype, [W["wq"], W["wk"], W["wv"]], self.rb_h, h, W["attn_norm"], 0,
@@ -145,10 +146,15 @@ class Qwen2Decoder:
                 self._norm(h, xn, W["attn_norm"], rows)
                 for name, y, n in (("wq", q, QD), ("wk", k, KD), ("wv", v, KD)):
                     self._ok("matmul", L.qlin_launch_quant_matmul(c.wtype, t(W[name]), self.rb_h, xn, y, n, H, rows))
-            self._ok("rope", L.qlin_launch_rope_store_kv(q, k, v, t(self.kc[i]), t(self.vc[i]), rows, c.n_heads,
-                                                         c.kv_heads, c.head_dim, self.max_seq, pos_ptr, c.theta))
-            self._ok("attend", L.qlin_launch_attend(q, t(self.kc[i]), t(self.vc[i]), attn, rows, c.n_heads,
-                                                    c.kv_heads, c.head_dim, self.max_seq, pos_ptr))
+            if fuse:
+                self._ok("rope_attend", L.qlin_launch_rope_attend(q, k, v, t(self.kc[i]), t(self.vc[i]), attn,
+                                                                  c.n_heads, c.kv_heads, c.head_dim, self.max_seq,
+                                                                  pos_ptr, c.theta))
+            else:
+                self._ok("rope", L.qlin_launch_rope_store_kv(q, k, v, t(self.kc[i]), t(self.vc[i]), rows, c.n_heads,
+                                                             c.kv_heads, c.head_dim, self.max_seq, pos_ptr, c.theta))
+                self._ok("attend", L.qlin_launch_attend(q, t(self.kc[i]), t(self.vc[i]), attn, rows, c.n_heads,
+                                                        c.kv_heads, c.head_dim, self.max_seq, pos_ptr))
             self._ok("o", L.qlin_launch_quant_matmul_add(c.wtype, t(W["wo"]), self.rb_q, attn, h, H, QD, rows))
             if fuse:
                 self._ok("norm_swiglu", L.qlin_launch_rms_norm_quant_swiglu(c.wtype, t(W["wg"]), t(W["wu"]), self.rb_h,
@@ -168,7 +174,7 @@ class Qwen2Decoder:
         """Final norm of residual row `row`, the tied output head, and the greedy pick into token."""
         c, L, t = self.cfg, self.L, c_ptr
         hr = t(self.h) + 4 * row * c.hidden
-        if self.fuse_norm and hr % 16 == 0:
+        if self.fuse and hr % 16 == 0:
             qlin.rms_norm_quant_gemv_multi(c.wtype, [self.w["table"]], self.rb_h, hr, self.w["final_norm"], 0, c.eps, 0,
                                            [self.logits], [c.vocab], c.hidden)
         else:

@@ -76,6 +76,7 @@ SIGNATURES = {
     "qlin_launch_rms_norm": (I, [P, P, P, I, I, I, F, I]),
     "qlin_launch_rope_store_kv": (I, [P, P, P, P, P, I, I, I, I, I, P, F]),
     "qlin_launch_attend": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "qlin_launch_rope_attend": (I, [P, P, P, P, P, P, I, I, I, I, P, F]),
     "qlin_launch_rms_norm_quant_gemv_multi": (I, [I, I, P, SZ, P, P, I, F, I, P, P, I]),
     "qlin_launch_rms_norm_quant_swiglu": (I, [I, P, P, SZ, P, P, I, F, I, P, I, I]),
     "qlin_probe_stream_read": (I, [P, SZ, I, P]),

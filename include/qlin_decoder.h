@@ -35,6 +35,11 @@
  * launch instead of two.  They take the shapes of the matrix-core decode kernels (every format, in_dim
  * a multiple of 256, or 128 for Q8_0 and Q5_0, x 16-byte aligned); other shapes return
  * QLIN_ERR_LIMIT, for the two-launch form.
+ *   qlin_launch_rope_attend    qlin_launch_rope_store_kv then qlin_launch_attend for one row (a decode
+ *                              step), in one launch, with the same results: the rotated key and the
+ *                              value are stored in the caches at the row's position as before, but q is
+ *                              left as it is (the rotated q lives only in the launch).  Alignment as
+ *                              qlin_launch_attend's for q, the caches and attn; k and v 4-byte aligned.
  */
 #ifndef QLIN_DECODER_H
 #define QLIN_DECODER_H
@@ -53,6 +58,9 @@ int qlin_launch_rope_store_kv(float *q, const float *k, const float *v, float *k
                               float rope_theta);
 int qlin_launch_attend(const float *q, const float *key_cache, const float *value_cache, float *attn, int rows,
                        int n_heads, int kv_heads, int head_dim, int max_seq_len, const int *start_pos_dev);
+int qlin_launch_rope_attend(const float *q, const float *k, const float *v, float *key_cache, float *value_cache,
+                            float *attn, int n_heads, int kv_heads, int head_dim, int max_seq_len,
+                            const int *start_pos_dev, float rope_theta);
 int qlin_launch_rms_norm_quant_gemv_multi(int type, int n_mats, const uint8_t *const *weights, size_t row_bytes,
                                           const float *x, const uint16_t *norm_weight, int norm_type, float eps,
                                           int one_plus, float *const *ys, const int *out_dims, int in_dim);

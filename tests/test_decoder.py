@@ -141,6 +141,57 @@ def test_rms_norm(rows, hidden, wtype, one_plus):
     assert normwise_rel_err(host(out), ref) <= 1e-6
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("start,D", [(0, 64), (37, 64), (300, 64), (600, 64), (5, 128), (200, 256)])
+def test_rope_attend_one_row(start, D):
+    """The decode row's rotary embedding, cache store and attention in one launch: the same caches and
+    the same output, bit for bit, as qlin_launch_rope_store_kv followed by qlin_launch_attend (a
+    position past the cache clamped to its last slot); q itself is left unrotated."""
+    torch = _gpu()
+    from gpu_util import banner, dev, empty_f32, host
+    from blog_amd import qlin
+    NH, NKV, S, theta = 14, 2, 512, 1e6
+    rng = np.random.default_rng(start * 7 + D)
+    q = rng.standard_normal((1, NH * D)).astype(np.float32)
+    k = rng.standard_normal((1, NKV * D)).astype(np.float32)
+    v = rng.standard_normal((1, NKV * D)).astype(np.float32)
+    kc0 = rng.standard_normal((S, NKV * D)).astype(np.float32)
+    vc0 = rng.standard_normal((S, NKV * D)).astype(np.float32)
+    pos = torch.tensor([start], dtype=torch.int32, device="cuda")
+    banner(f"rope_attend start={start} D={D}")
+    qa, kca, vca, attn_a = dev(q), dev(kc0), dev(vc0), empty_f32(1, NH * D)
+    qlin.call("qlin_launch_rope_store_kv", qa, dev(k), dev(v), kca, vca, 1, NH, NKV, D, S, pos, theta)
+    qlin.call("qlin_launch_attend", qa, kca, vca, attn_a, 1, NH, NKV, D, S, pos)
+    qb, kcb, vcb, attn_b = dev(q), dev(kc0), dev(vc0), empty_f32(1, NH * D)
+    qlin.call("qlin_launch_rope_attend", qb, dev(k), dev(v), kcb, vcb, attn_b, NH, NKV, D, S, pos, theta)
+    assert np.array_equal(host(attn_b), host(attn_a))
+    assert np.array_equal(host(kcb), host(kca))
+    assert np.array_equal(host(vcb), host(vca))
+    assert np.array_equal(host(qb), q)
+
+
+@pytest.mark.gpu
+def test_c3_decode_fused_matches_unfused():
+    """The decode step with its norms inside the linears and the rotary embedding inside the attention
+    gives the two-launch decoder's logits and tokens."""
+    torch = _gpu()
+    from gpu_util import banner
+    from blog_amd.decoder import Qwen2Config, Qwen2Decoder, make_weights
+    cfg = Qwen2Config()
+    w = make_weights(torch, cfg, seed=11)
+    prompt = torch.randint(0, cfg.vocab, (8,), dtype=torch.int32, device="cuda",
+                           generator=torch.Generator(device="cuda").manual_seed(3))
+    out = []
+    for fuse in (True, False):
+        banner(f"c3 decoder fuse={fuse}")
+        dec = Qwen2Decoder(torch, cfg, w, max_seq=64, max_prompt=8, fuse=fuse)
+        logits = torch.zeros(16, cfg.vocab, device="cuda")
+        toks = dec.generate(prompt, 16, logits_out=logits)
+        out.append((toks, logits.cpu().numpy()))
+    assert out[0][0] == out[1][0]
+    assert max(normwise_rel_err(a, b) for a, b in zip(out[0][1], out[1][1])) <= 1e-5
+
+
 def _norm_weights(rng, hidden, wtype):
     w16 = (rng.standard_normal(hidden) * 0.5 + 1).astype(np.float16)
     if wtype == 0:
