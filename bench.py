@@ -714,9 +714,10 @@ def wl_c5(args, torch, qlin, gen):
 
     def step_grouped():
         for wg, wu, wd, sg, su, sd in mats:
-            qlin.call("qlin_launch_moe_router_topk", logits, ids, rw, tokens, E, k, 1.0)
-            qlin.call("qlin_moe_routed_decode_grouped", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, x, ids,
-                      rw, wsp, nws, out, tokens, k)
+            # the router's picks and the grouped routed decode in one call (the routing runs in its
+            # gate/up launch)
+            qlin.call("qlin_moe_routed_decode_grouped_logits", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, x,
+                      logits, 1.0, ids, rw, wsp, nws, out, tokens, k)
             qlin.call("qlin_launch_quant_swiglu_rows", Q4_K, sg, su, s_rb, s_rb, x, sacts, sffn, hid, tokens)
             qlin.call("qlin_launch_quant_matmul_add", Q4_K, sd, sd_rb, sacts, out, hid, sffn, tokens)
 
@@ -746,12 +747,13 @@ def wl_c5(args, torch, qlin, gen):
         "config": {"workload": "c5-moe-grouped", "experts": E, "ffn": ffn, "hidden": hid, "tokens": tokens,
                    "top_k": k, "gate_up": "Q4_K", "down": "Q5_0", "shared_ffn": sffn, "shared": "Q4_K",
                    "distinct_experts": distinct, "algorithmic_bytes_per_step": nbytes,
-                   "launches_per_step": "router_topk + moe_routed_decode_grouped (group, gate/up, down, "
-                                        "combine) + quant_swiglu_rows + quant_matmul_add (shared experts)",
+                   "launches_per_step": "moe_routed_decode_grouped_logits (gate/up with the routing and "
+                                        "grouping, down, combine) + quant_swiglu_rows + quant_matmul_add "
+                                        "(shared experts)",
                    "per_token_facade_us_per_step": round(us_tok, 2), "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(nbytes / us / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "whole step (router_kernel, group_kernel, stream_kernel<Q4_K> gate/up, "
+                     "kernel": "whole step (stream_kernel<Q4_K> gate/up with the router and the grouping, "
                                "stream_kernel<Q5_0> down, combine_kernel, q4k_dense_kernel SwiGLU and add)",
                      "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": nbytes},
     }

@@ -669,11 +669,11 @@ size_t qlin_moe_grouped_workspace_bytes(int tokens, int k, int n_experts, int ff
     return qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden_size);
 }
 
-int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
-                                   int down_type, const uint8_t *down, size_t down_bytes, int n_experts, int ffn_dim,
-                                   int in_dim, int hidden, const float *x, const int *ids, const float *rw,
-                                   void *workspace, size_t workspace_bytes, float *out, int tokens, int k) {
-    // the per-token facade's rules (TensorTool.cpp:277-305) plus the batch's own
+// The batched decode's checks: the per-token facade's rules (TensorTool.cpp:277-305) plus the batch's own.
+static int grouped_check(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes, int down_type,
+                         const uint8_t *down, size_t down_bytes, int n_experts, int ffn_dim, int in_dim, int hidden,
+                         const float *x, const int *ids, const float *rw, const void *workspace,
+                         size_t workspace_bytes, const float *out, int tokens, int k) {
     if (down_type != QLIN_TYPE_Q4_K && down_type != QLIN_TYPE_Q6_K && down_type != QLIN_TYPE_Q5_0 &&
         down_type != QLIN_TYPE_Q8_0)
         return QLIN_ERR_UNSUPPORTED_TYPE;
@@ -694,7 +694,21 @@ int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8
         (rc = check_weight(gu_type, up, g_rb, ffn_dim, in_dim)))
         return rc;
     if ((rc = check_f32(x, work)) || (rc = check_f32(out, work)) || (rc = check_f32(rw, work))) return rc;
-    if (!work) return QLIN_OK;
+    if (work && !aligned(ids, 4)) return QLIN_ERR_ALIGN;
+    return QLIN_OK;
+}
+
+int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                   int down_type, const uint8_t *down, size_t down_bytes, int n_experts, int ffn_dim,
+                                   int in_dim, int hidden, const float *x, const int *ids, const float *rw,
+                                   void *workspace, size_t workspace_bytes, float *out, int tokens, int k) {
+    int rc = grouped_check(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts, ffn_dim, in_dim,
+                           hidden, x, ids, rw, workspace, workspace_bytes, out, tokens, k);
+    if (rc || tokens == 0 || k == 0) return rc;
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const size_t d_rb = d_eb / static_cast<size_t>(hidden);
     if (qlin::moe_grouped_up_ok(gu_type, gate, up, g_eb, g_rb, x, in_dim, ffn_dim, n_experts, tokens * k))
         return launched(qlin::moe_grouped(gu_type, gate, up, g_eb, g_rb, down_type, down, d_eb, d_rb, n_experts,
                                           ffn_dim, in_dim, hidden, x, ids, rw, workspace, out, tokens, k, stream()));
@@ -712,6 +726,33 @@ int qlin_moe_routed_decode_grouped(int gu_type, const uint8_t *gate, const uint8
         if (e != hipSuccess) return QLIN_ERR_LAUNCH;
     }
     return QLIN_OK;
+}
+
+int qlin_moe_routed_decode_grouped_logits(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                          int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
+                                          int ffn_dim, int in_dim, int hidden, const float *x,
+                                          const float *router_logits, float routed_scaling, int *ids, float *rw,
+                                          void *workspace, size_t workspace_bytes, float *out, int tokens, int k) {
+    int rc = grouped_check(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts, ffn_dim, in_dim,
+                           hidden, x, ids, rw, workspace, workspace_bytes, out, tokens, k);
+    if (rc || tokens == 0 || k == 0) return rc;
+    if (n_experts > 256) return QLIN_ERR_LIMIT;  // the router's limit
+    if ((rc = check_f32(router_logits, true))) return rc;
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    if (qlin::moe_grouped_up_ok(gu_type, gate, up, g_eb, g_rb, x, in_dim, ffn_dim, n_experts, tokens * k)) {
+        const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+        const size_t d_rb = d_eb / static_cast<size_t>(hidden);
+        const qlin::MoeRouter router{router_logits, routed_scaling, ids, rw};
+        return launched(qlin::moe_grouped(gu_type, gate, up, g_eb, g_rb, down_type, down, d_eb, d_rb, n_experts,
+                                          ffn_dim, in_dim, hidden, x, nullptr, nullptr, workspace, out, tokens, k,
+                                          stream(), &router));
+    }
+    // other layouts: the router, then the batched call's per-token path
+    if ((rc = qlin_launch_moe_router_topk(router_logits, ids, rw, tokens, n_experts, k, routed_scaling))) return rc;
+    return qlin_moe_routed_decode_grouped(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts,
+                                          ffn_dim, in_dim, hidden, x, ids, rw, workspace, workspace_bytes, out, tokens,
+                                          k);
 }
 
 int qlin_moe_routed_decode_grouped_noalloc(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,

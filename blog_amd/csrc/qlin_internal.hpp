@@ -147,10 +147,20 @@ void *moe_static_scratch();
 bool moe_grouped_shape_ok(int n_experts, int64_t routes);
 bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
                        const float *x, int in_dim, int ffn_dim, int n_experts, int routes);
+// The router's inputs and outputs when the batched decode also routes (logits [tokens, n_experts] in,
+// ids and weights [tokens, k] out, as router_topk writes them).
+struct MoeRouter {
+    const float *logits;
+    float scaling;
+    int *ids;
+    float *w;
+};
+// router non-null: ids and rw are ignored, the routes are router_topk's of the logits (inside the gate/up
+// launch for n_experts <= 64 when its LDS allows, else one router launch first).
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int n_experts, int ffn_dim, int in_dim,
                        int hidden, const float *x, const int *ids, const float *rw, void *workspace, float *out,
-                       int tokens, int k, hipStream_t s);
+                       int tokens, int k, hipStream_t s, const MoeRouter *router = nullptr);
 
 // Quantized embedding rows and the MLA latent-absorption products over kv_b (qlin_embed_mla.hip).
 hipError_t quant_embedding(int type, const int *ids, float *out, const uint8_t *table, size_t row_bytes, int hidden,

@@ -163,11 +163,20 @@ struct StreamArgs {
     int rows, K, nchunk, tpe;  // rows per expert, inner dimension, chunks per row, 16-row tiles per expert
     int piece;                 // tiles whose step partials fit in LDS at once
     // grouping in the kernel (GRP): the routes' expert ids, their count and the expert count; the
-    // groups are built in LDS from these, and workgroup 0 writes them to gr for the later launches
+    // groups are built in LDS from these, and workgroup 0 writes them to gr for the later launches.
+    // With logits (n_experts <= 64) the kernel also routes: the ids are the router's picks, which
+    // workgroup 0 writes to ids_out and w_out (weights times scaling) as router_topk does.
     const int *ids;
     int R, ne;
     Groups gr;
+    const float *logits;
+    float scaling;
+    int *ids_out;
+    float *w_out;
 };
+// LDS of the in-kernel router, after the staged ids: per wave the 64 logits, their exponentials and
+// the denominator (132 floats, a multiple of 16 bytes)
+constexpr int kRouteWaveFloats = 132;
 
 // 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
 // shared by the 16 waves of a CU: both helpers take 32-bit arithmetic when the operands allow
@@ -243,11 +252,74 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     __shared__ int s_off[GRP ? kFuseExperts : 1];
     __shared__ int s_nsel;
     if constexpr (GRP) {
-        const int R = a.R, E = a.ne;
+        const int R = a.R, E = a.ne, R16 = (R + 15) & ~15;
         int *sids = reinterpret_cast<int *>(smem);
         const int4 *sids4 = reinterpret_cast<const int4 *>(smem);
-        for (int i = tid; i < ((R + 15) & ~15); i += kSThreads) sids[i] = i < R ? a.ids[i] : -1;
-        __syncthreads();
+        if (a.logits) {  // uniform
+            // router_rank_kernel's picks, one token per wave at a time (E <= 64: lane e holds expert e)
+            const int k = a.x_div, T = R / k;
+            float *sv = reinterpret_cast<float *>(smem) + R16 + wave * kRouteWaveFloats, *ex = sv + 64, *dn = ex + 64;
+            for (int i = R + tid; i < R16; i += kSThreads) sids[i] = -1;
+            for (int t0 = 0; t0 < T; t0 += kSWaves) {  // the same trip count in every wave: barriers below
+                const int t = t0 + wave;
+                const bool live = t < T;  // uniform per wave
+                const float l = live && lane < E ? a.logits[static_cast<size_t>(t) * E + lane] : -INFINITY;
+                const float v = isfinite(l) ? l : -INFINITY;
+                const float maxv = wave_max(v);
+                sv[lane] = v;
+                ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;
+                __syncthreads();
+                if (lane == 0) {
+                    // in expert order, as router_rank_kernel sums (past E the exponentials are 0, and adding
+                    // them leaves the sum as it is); the 64 values are read at once
+                    float denom = 0.0f;
+                    if (isfinite(maxv)) {
+                        float4 q[16];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) q[i] = reinterpret_cast<const float4 *>(ex)[i];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            denom += q[i].x;
+                            denom += q[i].y;
+                            denom += q[i].z;
+                            denom += q[i].w;
+                        }
+                    }
+                    dn[0] = denom;
+                }
+                int ahead = 0;
+#pragma unroll 4
+                for (int j = 0; j < 16; ++j) {
+                    const float4 q = reinterpret_cast<const float4 *>(sv)[j];
+                    ahead += (q.x > v || (q.x == v && 4 * j < lane)) + (q.y > v || (q.y == v && 4 * j + 1 < lane)) +
+                             (q.z > v || (q.z == v && 4 * j + 2 < lane)) + (q.w > v || (q.w == v && 4 * j + 3 < lane));
+                }
+                __syncthreads();
+                const float denom = dn[0];
+                const bool fin = v != -INFINITY;
+                const int nf = static_cast<int>(__popcll(__ballot(fin)));
+                if (live && fin && ahead < k) {
+                    const size_t o = static_cast<size_t>(t) * k + ahead;
+                    sids[o] = lane;
+                    if (blockIdx.x == 0) {
+                        a.ids_out[o] = lane;
+                        a.w_out[o] = (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * a.scaling;
+                    }
+                }
+                for (int r = nf + lane; live && r < k; r += 64) {  // every remaining logit -inf: expert r, weight 0
+                    const size_t o = static_cast<size_t>(t) * k + r;
+                    sids[o] = r < E ? r : 0;
+                    if (blockIdx.x == 0) {
+                        a.ids_out[o] = r < E ? r : 0;
+                        a.w_out[o] = 0.0f;
+                    }
+                }
+                __syncthreads();  // this round's scratch is read; the next round rewrites it
+            }
+        } else {
+            for (int i = tid; i < R16; i += kSThreads) sids[i] = i < R ? a.ids[i] : -1;
+            __syncthreads();
+        }
         // routes i .. i + 15 (below lim) with expert e
         auto count16 = [&](int i, int e, int lim = 0x7fffffff) {
             int c = 0;
@@ -261,8 +333,10 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             return c;
         };
         int c = 0;
-        if (tid < E)
+        if (tid < E) {
+#pragma unroll 4
             for (int i = 0; i < R; i += 16) c += count16(i, tid);
+        }
         // exclusive scan over the experts of count | selected << kRouteBits: the first list
         // position of each expert and the records of the selected ones
         const int v = tid < E ? c | (static_cast<int>(c > 0) << kRouteBits) : 0;
@@ -299,6 +373,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             if (e >= 0 && e < E) {
                 int rank = 0;
                 const int full = tid & ~15;
+#pragma unroll 4
                 for (int i = 0; i < full; i += 16) rank += count16(i, e);
                 rank += count16(full, e, tid);
                 s_list[s_off[e] + rank] = tid;
@@ -331,10 +406,13 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             const int64_t t = __shfl_up(inc, d, 64);
             if (lane >= d) inc += t;
         }
-        if (lane == 63) s_wave[wave] = inc;
-        __syncthreads();
+        // (up to 64 selected experts, wave 0 holds every cost: no sums across waves)
+        const int nw = (nsel + 63) / 64;
+        if (nw > 1 && lane == 63 && wave < nw) s_wave[wave] = inc;
+        if (nw > 1) __syncthreads();  // uniform
         int64_t before = 0;
-        for (int w = 0; w < wave; ++w) before += s_wave[w];
+        if (nw > 1)
+            for (int w = 0; w < min(wave, nw); ++w) before += s_wave[w];
         if (tid == 0) s_pref[0] = 0;
         if (tid < nsel) s_pref[tid + 1] = before + inc;
         __syncthreads();
@@ -968,10 +1046,14 @@ bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t eb
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int E, int ffn, int K, int hidden,
                        const float *x, const int *ids, const float *rw, void *ws, float *out, int tokens, int k,
-                       hipStream_t s) {
+                       hipStream_t s, const MoeRouter *router) {
     (void)gu_type;  // Q4_K (moe_grouped_up_ok)
     const int R = tokens * k;
     if (R == 0 || hidden == 0) return hipSuccess;
+    if (router) {
+        ids = router->ids;
+        rw = router->w;
+    }
     uint8_t *p = static_cast<uint8_t *>(ws);
     Groups gr;
     gr.offset = reinterpret_cast<int *>(p);
@@ -988,9 +1070,17 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
 
     // The gate/up streaming launch groups the routes itself when they fit its LDS arrays and its
     // staging area holds the ids; otherwise group_kernel writes the groups first.
+    // With router logits and at most 64 experts it routes as well (its LDS then also holds each wave's
+    // logits); otherwise the router runs first, as its own launch.
     StreamPlan up = R <= kFuseRoutes && E <= kFuseExperts ? stream_plan<T_Q4_K, true, true>(ffn, K, E, R)
                                                           : StreamPlan{};
-    const bool grp = up.ok && up.lds >= static_cast<size_t>((R + 15) & ~15) * sizeof(int);
+    const size_t ids_lds = static_cast<size_t>((R + 15) & ~15) * sizeof(int);
+    const bool grp = up.ok && up.lds >= ids_lds;
+    const bool route_here = router && grp && E <= 64 && up.lds >= ids_lds + kSWaves * kRouteWaveFloats * sizeof(float);
+    if (router && !route_here) {
+        const hipError_t e = router_topk(router->logits, router->ids, router->w, tokens, E, k, router->scaling, s);
+        if (e != hipSuccess) return e;
+    }
     if (!grp) {
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, ids, R, E, gr);
         up = stream_plan<T_Q4_K, true>(ffn, K, E, R);
@@ -1002,6 +1092,12 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
         ua.R = R;
         ua.ne = E;
         ua.gr = gr;
+        if (route_here) {
+            ua.logits = router->logits;
+            ua.scaling = router->scaling;
+            ua.ids_out = router->ids;
+            ua.w_out = router->w;
+        }
         const hipError_t e = grp ? launch_stream<T_Q4_K, true, true>(up, ua, s) : launch_stream<T_Q4_K, true>(up, ua, s);
         if (e != hipSuccess) return e;
     } else {

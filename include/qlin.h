@@ -254,6 +254,19 @@ int qlin_moe_routed_decode_grouped(int gate_up_type, const uint8_t *gate_exps, c
                                    const float *x, const int *expert_ids, const float *route_weights,
                                    void *workspace, size_t workspace_bytes, float *out, int tokens, int k);
 
+/* No counterpart in the reference: qlin_launch_moe_router_topk of router_logits [tokens, n_experts]
+ * followed by qlin_moe_routed_decode_grouped with its picks, in one call.  expert_ids and
+ * route_weights [tokens, k] receive the router's picks and weights (times routed_scaling) exactly as
+ * qlin_launch_moe_router_topk writes them; up to 64 experts the routing runs inside the batched
+ * decode's gate/up launch (one launch fewer), otherwise as its own launch first.  Arguments and limits
+ * otherwise as qlin_moe_routed_decode_grouped's, and n_experts <= 256 (else QLIN_ERR_LIMIT). */
+int qlin_moe_routed_decode_grouped_logits(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                          size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                          size_t down_bytes, int n_experts, int ffn_dim, int in_dim, int hidden_size,
+                                          const float *x, const float *router_logits, float routed_scaling,
+                                          int *expert_ids, float *route_weights, void *workspace,
+                                          size_t workspace_bytes, float *out, int tokens, int k);
+
 /* No counterpart in the reference: qlin_moe_routed_decode_grouped for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops that forbid it).  The same arguments
  * without the workspace: the call runs on a scratch array the library keeps on each GPU for the

@@ -678,6 +678,38 @@ def test_moe_grouped_beyond_in_kernel_grouping(E, tokens, k):
     assert normwise_rel_err(got, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("E,tokens,k,ffn,hid", [(64, 16, 6, 1408, 2048), (8, 24, 4, 256, 512), (100, 16, 6, 256, 256),
+                                                (64, 300, 4, 256, 256)])
+def test_moe_grouped_from_router_logits(E, tokens, k, ffn, hid):
+    """The router and the batched decode in one call: up to 64 experts (and 1024 routes) the gate/up
+    launch picks the routes itself.  Its ids are the router's exactly (ties, NaN, +inf, rows with only
+    two finite logits), its weights the router's, and the output the per-token reference's."""
+    wg, wu, grb, geb, wdn, drb, deb, x, _, _ = _moe_batch(Q4_K, Q5_0, E, ffn, hid, tokens, k, 381 + E + tokens)
+    rng = np.random.default_rng(391 + E)
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    logits[1, :] = 0.5
+    logits[2, 3] = np.nan
+    logits[3, :] = -np.inf
+    logits[3, [E - 1, E // 2]] = [0.25, 0.75]
+    logits[4, E - 2] = np.inf
+    logits[5, :] = rng.integers(-2, 3, E).astype(np.float32)
+    ids_r, rw_r = orc.router_topk(logits, k, 1.25)
+    nbytes = qlin.lib().qlin_moe_grouped_workspace_bytes(tokens, k, E, ffn, hid)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
+    wsp = (ws.data_ptr() + 255) // 256 * 256
+    out0 = np.random.default_rng(13).standard_normal((tokens, hid)).astype(np.float32)
+    out_d = dev(out0)
+    ids_d = torch.full((tokens, k), -7, dtype=torch.int32, device="cuda")
+    rw_d = empty_f32(tokens, k)
+    banner(f"moe grouped from logits E={E} tokens={tokens} k={k}")
+    qlin.call("qlin_moe_routed_decode_grouped_logits", Q4_K, dev(wg), dev(wu), wg.size, Q5_0, dev(wdn), wdn.size, E,
+              ffn, hid, hid, dev(x), dev(logits), 1.25, ids_d, rw_d, wsp, nbytes, out_d, tokens, k)
+    assert np.array_equal(host(ids_d), ids_r)
+    assert np.allclose(host(rw_d), rw_r, rtol=1e-5, atol=1e-7)
+    ref = _moe_batch_ref(Q4_K, Q5_0, wg, wu, grb, geb, wdn, drb, deb, x, ids_r, host(rw_d), out0, ffn, hid)
+    assert normwise_rel_err(host(out_d) - out0, ref - out0) <= 1e-4
+
+
 def test_moe_grouped_unaligned_output():
     """An output 4 bytes past a 16-byte boundary."""
     E, ffn, hid, tokens, k = 8, 256, 256, 4, 2
