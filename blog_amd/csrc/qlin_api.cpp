@@ -502,6 +502,47 @@ int qlin_moe_routed_decode_indexed(int gu_type, const uint8_t *gate, const uint8
                                                             hidden, ffn_dim);
 }
 
+int qlin_moe_routed_decode_indexed_logits(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                          int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
+                                          int ffn_dim, int in_dim, int hidden, const float *x,
+                                          const float *router_logits, float routed_scaling, int *ids, float *rw,
+                                          float *act, float *out, int k) {
+    // qlin_moe_routed_decode_indexed's checks (ids and rw are written here), all before anything runs
+    if (!ids || !rw || !router_logits) return QLIN_ERR_NULL;
+    if (down_type != QLIN_TYPE_Q4_K && down_type != QLIN_TYPE_Q6_K && down_type != QLIN_TYPE_Q5_0 &&
+        down_type != QLIN_TYPE_Q8_0)
+        return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (gu_type != QLIN_TYPE_Q4_K && gu_type != QLIN_TYPE_Q6_K) return QLIN_ERR_UNSUPPORTED_TYPE;
+    if (n_experts <= 0 || ffn_dim <= 0 || in_dim <= 0 || hidden <= 0 || k < 0) return QLIN_ERR_SHAPE;
+    if (n_experts > 256) return QLIN_ERR_LIMIT;  // the router's limit
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const size_t d_rb = d_eb / static_cast<size_t>(hidden);
+    if (!act) return QLIN_ERR_NULL;
+    int rc = check_weight(down_type, down, d_rb, hidden, ffn_dim);
+    if (rc || (rc = check_weight(gu_type, gate, g_rb, ffn_dim, in_dim)) ||
+        (rc = check_weight(gu_type, up, g_rb, ffn_dim, in_dim)))
+        return rc;
+    if ((rc = check_f32(out, true)) || (rc = check_f32(rw, true)) || (rc = check_f32(x, true)) ||
+        (rc = check_f32(act, true)) || (rc = check_f32(router_logits, true)))
+        return rc;
+    if (!aligned(ids, 4)) return QLIN_ERR_ALIGN;
+    if (k == 0) return QLIN_OK;
+    if (n_experts <= 64 && qlin::mfma_routed_ok(gu_type, true, gate, up, g_eb, g_rb, x, k, ffn_dim, in_dim)) {
+        // the routing in the gate/up launch (its workgroup 0 writes ids and rw), then the down launch
+        const qlin::MoeRouter router{router_logits, routed_scaling, ids, rw};
+        const hipError_t e = qlin::mfma_swiglu_routed(gu_type, gate, up, g_eb, g_rb, x, nullptr, act, k, ffn_dim,
+                                                      in_dim, stream(), &router, n_experts);
+        if (e != hipSuccess) return QLIN_ERR_LAUNCH;
+        return qlin_launch_quant_down_f32_indexed_accum_ordered(down_type, down, d_eb, d_rb, act, ids, rw, out, k,
+                                                                hidden, ffn_dim);
+    }
+    if ((rc = qlin_launch_moe_router_topk(router_logits, ids, rw, 1, n_experts, k, routed_scaling))) return rc;
+    return qlin_moe_routed_decode_indexed(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts,
+                                          ffn_dim, in_dim, hidden, x, ids, rw, act, out, k);
+}
+
 static bool embed_mla_type(int t) {
     return t == QLIN_TYPE_Q4_K || t == QLIN_TYPE_Q6_K || t == QLIN_TYPE_Q5_0 || t == QLIN_TYPE_Q8_0;
 }

@@ -139,4 +139,60 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// ---- router top-k of one token by one wave (at most 64 experts) --------------------------------
+// Lane e holds expert e's logit (non-finite as -inf).  Pick r is the expert with exactly r experts
+// ahead of it -- a larger logit, or an equal one at a lower index -- which is the order of k
+// successive argmaxes that prefer the lower index, the reference's strict-'>' first maximum.  Picks
+// past the finite logits fall back to expert r (0 past ne) with weight 0; a pick's weight is
+// exp(l - max) / (the exponentials summed in expert order) times scaling.
+// Every wave of the workgroup calls this in step (it holds two workgroup barriers); only waves with
+// live set read logits (row of ne floats), use the LDS and put their picks, through
+// put(r, expert, weight).  sv, ex: 64 floats each, 16-byte aligned, and dn: one float, of LDS that no
+// other live wave uses (waves without live set touch none of it).
+template <class Put>
+__device__ __forceinline__ void route_token_rank(bool live, const float *row, int ne, int k, float scaling, float *sv,
+                                                 float *ex, float *dn, Put put) {
+    const int lane = threadIdx.x & 63;
+    const float l = live && lane < ne ? row[lane] : -INFINITY;
+    const float v = isfinite(l) ? l : -INFINITY;
+    const float maxv = wave_max(v);
+    if (live) {
+        sv[lane] = v;
+        ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;  // 0 for -inf and past ne
+    }
+    __syncthreads();
+    if (live && lane == 0) {
+        // in expert order; past ne the exponentials are 0 and leave the sum as it is
+        float denom = 0.0f;
+        if (isfinite(maxv)) {
+            float4 q[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[i] = reinterpret_cast<const float4 *>(ex)[i];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                denom += q[i].x;
+                denom += q[i].y;
+                denom += q[i].z;
+                denom += q[i].w;
+            }
+        }
+        *dn = denom;
+    }
+    int ahead = 0;  // past ne the logits are -inf, never ahead of a finite one
+    if (live) {
+#pragma unroll 4
+        for (int j = 0; j < 16; ++j) {
+            const float4 q = reinterpret_cast<const float4 *>(sv)[j];
+            ahead += (q.x > v || (q.x == v && 4 * j < lane)) + (q.y > v || (q.y == v && 4 * j + 1 < lane)) +
+                     (q.z > v || (q.z == v && 4 * j + 2 < lane)) + (q.w > v || (q.w == v && 4 * j + 3 < lane));
+        }
+    }
+    __syncthreads();
+    const float denom = live ? *dn : 0.0f;
+    const bool fin = v != -INFINITY;
+    const int nf = static_cast<int>(__popcll(__ballot(fin)));
+    if (live && fin && ahead < k) put(ahead, lane, (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * scaling);
+    for (int r = nf + lane; live && r < k; r += 64) put(r, r < ne ? r : 0, 0.0f);
+}
+
 }  // namespace qlin

@@ -31,6 +31,14 @@ hipError_t q4k_stream_gemv(const uint8_t *const *w, float *const *y, const int *
 hipError_t q4k_stream_swiglu(const uint8_t *wg, const uint8_t *wu, size_t row_bytes, const float *x, float *act,
                              int ffn_dim, int in_dim, hipStream_t s);
 
+// The router's inputs and outputs when a MoE decode also routes (logits [tokens, n_experts] in, ids
+// and weights [tokens, k] out, as router_topk writes them).
+struct MoeRouter {
+    const float *logits;
+    float scaling;
+    int *ids;
+    float *w;
+};
 // An RMSNorm applied to x as the decode kernels stage it: x[j] * rsqrt(mean x^2 + eps) * w[j], w bf16
 // (type 0) or f16 (1), plus one if one_plus.
 struct RmsNorm {
@@ -54,9 +62,11 @@ hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t ro
 // SwiGLU's (rows = ffn, k = in_dim) or the down projection's (rows = hidden, k = ffn) shape.
 bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1, size_t expert_bytes,
                     size_t row_bytes, const float *x, int routes, int rows, int k);
+// router: the routes are router_topk's picks of the token's logits (n_experts <= 64), made in the
+// launch and written to router->ids / router->w; ids is then not read.
 hipError_t mfma_swiglu_routed(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
                               const float *x, const int *ids, float *act, int routes, int ffn_dim, int in_dim,
-                              hipStream_t s);
+                              hipStream_t s, const MoeRouter *router = nullptr, int n_experts = 0);
 hipError_t mfma_down_routed(int type, const uint8_t *wd, size_t expert_bytes, size_t row_bytes, const float *act,
                             const int *ids, const float *rw, float *out, int routes, int hidden, int ffn_dim,
                             hipStream_t s);
@@ -147,14 +157,6 @@ void *moe_static_scratch();
 bool moe_grouped_shape_ok(int n_experts, int64_t routes);
 bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
                        const float *x, int in_dim, int ffn_dim, int n_experts, int routes);
-// The router's inputs and outputs when the batched decode also routes (logits [tokens, n_experts] in,
-// ids and weights [tokens, k] out, as router_topk writes them).
-struct MoeRouter {
-    const float *logits;
-    float scaling;
-    int *ids;
-    float *w;
-};
 // router non-null: ids and rw are ignored, the routes are router_topk's of the logits (inside the gate/up
 // launch for n_experts <= 64 when its LDS allows, else one router launch first).
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,

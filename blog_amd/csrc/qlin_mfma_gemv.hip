@@ -170,6 +170,14 @@ struct MfmaArgs {
     const uint16_t *norm_w;
     int norm_type, norm_one_plus;
     float norm_eps;
+    // Routed SwiGLU from router logits (logits non-null, ne <= 64): wave 0 picks the token's routes
+    // (route_token_rank) instead of reading ids, and workgroup 0 writes the picks and their weights
+    // (times scaling) to ids_out and rw_out for the down launch.
+    const float *logits;
+    int ne;
+    float scaling;
+    int *ids_out;
+    float *rw_out;
 };
 
 constexpr int kMaxRoutes = 16;  // routes of one routed launch (top-k of one token)
@@ -465,7 +473,23 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     }
     if constexpr (ROUTED) {
         // the routes' experts (and down weights): every weight address depends on them
-        if (tid < a.routes) {
+        bool routed_here = false;
+        if constexpr (SWIGLU) {
+            if (a.logits) {  // uniform: wave 0 routes the token (the only live wave: its LDS alone)
+                __shared__ __attribute__((aligned(16))) float s_rv[64], s_rex[64];
+                __shared__ float s_rdn;
+                route_token_rank(wave == 0, a.logits, a.ne, a.routes, a.scaling, s_rv, s_rex, &s_rdn,
+                                 [&](int r, int e, float w) {
+                                     s_ids[r] = e;
+                                     if (blockIdx.x == 0) {
+                                         a.ids_out[r] = e;
+                                         a.rw_out[r] = w;
+                                     }
+                                 });
+                routed_here = true;
+            }
+        }
+        if (!routed_here && tid < a.routes) {
             s_ids[tid] = a.ids[tid];
             if constexpr (!SWIGLU) s_rw[tid] = a.rw[tid];
         }
@@ -1213,8 +1237,16 @@ bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1,
 }
 
 hipError_t mfma_swiglu_routed(int type, const uint8_t *wg, const uint8_t *wu, size_t eb, size_t rb, const float *x,
-                              const int *ids, float *act, int routes, int ffn, int k, hipStream_t s) {
+                              const int *ids, float *act, int routes, int ffn, int k, hipStream_t s,
+                              const MoeRouter *router, int n_experts) {
     MfmaArgs a = swiglu_routed_args(type, wg, wu, eb, rb, x, ids, act, routes, ffn, k);
+    if (router) {
+        a.logits = router->logits;
+        a.ne = n_experts;
+        a.scaling = router->scaling;
+        a.ids_out = router->ids;
+        a.rw_out = router->w;
+    }
     return launch(type, a, k, true, true, s);
 }
 

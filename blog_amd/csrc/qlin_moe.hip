@@ -107,60 +107,19 @@ __global__ __launch_bounds__(64) void router_kernel(const float *__restrict__ lo
     }
 }
 
-// At most 64 experts: lane e holds expert e's logit, and pick r is the expert with exactly r experts
-// ahead of it (a larger logit, or an equal one at a lower index).  That is the order of router_kernel's
-// k successive wave argmaxes, found in one pass of compares against the logits in LDS instead of k
-// rounds of cross-lane reductions; the weights and the fallback for picks past the finite logits are
+// At most 64 experts, one wave per token (route_token_rank): the order of router_kernel's k successive
+// wave argmaxes, found in one pass of compares against the logits in LDS instead of k rounds of
+// cross-lane reductions; the weights and the fallback for picks past the finite logits are
 // router_kernel's.
 __global__ __launch_bounds__(64) void router_rank_kernel(const float *__restrict__ logits, int *__restrict__ idx,
                                                          float *__restrict__ wout, int ne, int k, float scaling) {
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float l = lane < ne ? logits[static_cast<size_t>(t) * ne + lane] : -INFINITY;
-    const float v = isfinite(l) ? l : -INFINITY;
-    const float maxv = wave_max(v);
-    __shared__ __attribute__((aligned(16))) float sv[64];
-    __shared__ __attribute__((aligned(16))) float ex[64];
-    sv[lane] = v;
-    ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;  // 0 for -inf and past ne
-    __syncthreads();
-    __shared__ float denom_s;
-    if (lane == 0) {
-        // in expert order, as router_kernel (and the reference's one thread per token) sums
-        float denom = 0.0f;
-        if (isfinite(maxv)) {
-            const int n4 = ne >> 2;
-            for (int i = 0; i < n4; ++i) {
-                const float4 q = reinterpret_cast<const float4 *>(ex)[i];
-                denom += q.x;
-                denom += q.y;
-                denom += q.z;
-                denom += q.w;
-            }
-            for (int e = 4 * n4; e < ne; ++e) denom += ex[e];
-        }
-        denom_s = denom;
-    }
-    // experts ahead of this one; past ne the logits are -inf, which are never ahead of a finite one
-    int ahead = 0;
-#pragma unroll 4
-    for (int j = 0; j < 16; ++j) {
-        const float4 q = reinterpret_cast<const float4 *>(sv)[j];
-        ahead += (q.x > v || (q.x == v && 4 * j < lane)) + (q.y > v || (q.y == v && 4 * j + 1 < lane)) +
-                 (q.z > v || (q.z == v && 4 * j + 2 < lane)) + (q.w > v || (q.w == v && 4 * j + 3 < lane));
-    }
-    __syncthreads();
-    const float denom = denom_s;
-    const bool fin = v != -INFINITY;
-    const int nf = static_cast<int>(__popcll(__ballot(fin)));
-    if (fin && ahead < k) {
-        idx[static_cast<size_t>(t) * k + ahead] = lane;
-        wout[static_cast<size_t>(t) * k + ahead] = (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * scaling;
-    }
-    // every remaining logit is -inf: pick r falls back to expert r (or 0), with weight 0
-    for (int r = nf + lane; r < k; r += 64) {
-        idx[static_cast<size_t>(t) * k + r] = r < ne ? r : 0;
-        wout[static_cast<size_t>(t) * k + r] = 0.0f;
-    }
+    __shared__ __attribute__((aligned(16))) float sv[64], ex[64];
+    __shared__ float dn;
+    const size_t t = blockIdx.x;
+    route_token_rank(true, logits + t * ne, ne, k, scaling, sv, ex, &dn, [&](int r, int e, float w) {
+        idx[t * k + r] = e;
+        wout[t * k + r] = w;
+    });
 }
 
 template <int T>

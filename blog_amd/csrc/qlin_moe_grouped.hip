@@ -260,60 +260,17 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
             const int k = a.x_div, T = R / k;
             float *sv = reinterpret_cast<float *>(smem) + R16 + wave * kRouteWaveFloats, *ex = sv + 64, *dn = ex + 64;
             for (int i = R + tid; i < R16; i += kSThreads) sids[i] = -1;
-            for (int t0 = 0; t0 < T; t0 += kSWaves) {  // the same trip count in every wave: barriers below
+            for (int t0 = 0; t0 < T; t0 += kSWaves) {  // the same trip count in every wave: barriers inside
                 const int t = t0 + wave;
-                const bool live = t < T;  // uniform per wave
-                const float l = live && lane < E ? a.logits[static_cast<size_t>(t) * E + lane] : -INFINITY;
-                const float v = isfinite(l) ? l : -INFINITY;
-                const float maxv = wave_max(v);
-                sv[lane] = v;
-                ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;
-                __syncthreads();
-                if (lane == 0) {
-                    // in expert order, as router_rank_kernel sums (past E the exponentials are 0, and adding
-                    // them leaves the sum as it is); the 64 values are read at once
-                    float denom = 0.0f;
-                    if (isfinite(maxv)) {
-                        float4 q[16];
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) q[i] = reinterpret_cast<const float4 *>(ex)[i];
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            denom += q[i].x;
-                            denom += q[i].y;
-                            denom += q[i].z;
-                            denom += q[i].w;
-                        }
-                    }
-                    dn[0] = denom;
-                }
-                int ahead = 0;
-#pragma unroll 4
-                for (int j = 0; j < 16; ++j) {
-                    const float4 q = reinterpret_cast<const float4 *>(sv)[j];
-                    ahead += (q.x > v || (q.x == v && 4 * j < lane)) + (q.y > v || (q.y == v && 4 * j + 1 < lane)) +
-                             (q.z > v || (q.z == v && 4 * j + 2 < lane)) + (q.w > v || (q.w == v && 4 * j + 3 < lane));
-                }
-                __syncthreads();
-                const float denom = dn[0];
-                const bool fin = v != -INFINITY;
-                const int nf = static_cast<int>(__popcll(__ballot(fin)));
-                if (live && fin && ahead < k) {
-                    const size_t o = static_cast<size_t>(t) * k + ahead;
-                    sids[o] = lane;
-                    if (blockIdx.x == 0) {
-                        a.ids_out[o] = lane;
-                        a.w_out[o] = (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * a.scaling;
-                    }
-                }
-                for (int r = nf + lane; live && r < k; r += 64) {  // every remaining logit -inf: expert r, weight 0
-                    const size_t o = static_cast<size_t>(t) * k + r;
-                    sids[o] = r < E ? r : 0;
-                    if (blockIdx.x == 0) {
-                        a.ids_out[o] = r < E ? r : 0;
-                        a.w_out[o] = 0.0f;
-                    }
-                }
+                route_token_rank(t < T, a.logits + static_cast<size_t>(t) * E, E, k, a.scaling, sv, ex, dn,
+                                 [&](int r, int e, float w) {
+                                     const size_t o = static_cast<size_t>(t) * k + r;
+                                     sids[o] = e;
+                                     if (blockIdx.x == 0) {
+                                         a.ids_out[o] = e;
+                                         a.w_out[o] = w;
+                                     }
+                                 });
                 __syncthreads();  // this round's scratch is read; the next round rewrites it
             }
         } else {

@@ -69,6 +69,7 @@ SIGNATURES = {
     "qlin_launch_dequantize_to_f32": (I, [I, P, P, I64]),
     "qlin_gemm": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_moe_routed_decode_indexed": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, P, I]),
+    "qlin_moe_routed_decode_indexed_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, F, P, P, P, P, I]),
     "qlin_moe_grouped_workspace_bytes": (SZ, [I, I, I, I, I]),
     "qlin_moe_routed_decode_grouped": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, SZ, P, I, I]),
     "qlin_moe_routed_decode_grouped_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, F, P, P, P, SZ, P, I, I]),

@@ -241,6 +241,20 @@ int qlin_moe_routed_decode_indexed(int gate_up_type, const uint8_t *gate_exps, c
                                    int hidden_size, const float *x, const int *expert_ids,
                                    const float *route_weights, float *act_scratch, float *out, int k);
 
+/* No counterpart in the reference: qlin_launch_moe_router_topk of one token's router_logits
+ * [n_experts] followed by qlin_moe_routed_decode_indexed with its picks, in one call.  expert_ids and
+ * route_weights [k] receive the router's picks and weights (times routed_scaling) exactly as
+ * qlin_launch_moe_router_topk writes them; up to 64 experts, where the routed matrix-core SwiGLU takes
+ * the layout, that launch picks the routes itself (one launch fewer), otherwise the router runs first.
+ * Arguments and checks otherwise as qlin_moe_routed_decode_indexed's, and n_experts <= 256 (else
+ * QLIN_ERR_LIMIT). */
+int qlin_moe_routed_decode_indexed_logits(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                          size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                          size_t down_bytes, int n_experts, int ffn_dim, int in_dim, int hidden_size,
+                                          const float *x, const float *router_logits, float routed_scaling,
+                                          int *expert_ids, float *route_weights, float *act_scratch, float *out,
+                                          int k);
+
 /* No reference counterpart (the reference decodes one token at a time): moe_routed_decode_indexed
  * for a batch of tokens, each selected expert's weights read once for all the routes that chose it.
  * x [tokens, in_dim], expert_ids / route_weights [tokens, k], out [tokens, hidden_size] (+=); per

@@ -568,6 +568,43 @@ def test_moe_facade_deepseek_shape():
     assert normwise_rel_err(host(out_d), ref) <= 1e-4
 
 
+@pytest.mark.parametrize("E,k,ffn,hid,special", [(64, 6, 1408, 2048, None), (64, 6, 256, 512, "ties"),
+                                                (48, 4, 256, 512, "nan"), (8, 6, 256, 256, "two_finite"),
+                                                (100, 6, 256, 256, None)])
+def test_moe_facade_from_router_logits(E, k, ffn, hid, special):
+    """The router and the per-token routed decode in one call: up to 64 experts the routed gate/up
+    launch picks the routes itself.  Its ids are the router's exactly, its weights the router's, and
+    the output the indexed path's reference."""
+    wg, grb, geb = _experts(Q4_K, E, ffn, hid, 111 + E)
+    wu, _, _ = _experts(Q4_K, E, ffn, hid, 112 + E)
+    wdn, drb, deb = _experts(Q5_0, E, hid, ffn, 113 + E)
+    x = qgen.random_x(1, hid, seed=114)[0]
+    rng = np.random.default_rng(115 + k)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    if special == "ties":
+        logits[0, :] = rng.integers(-1, 2, E).astype(np.float32)
+    elif special == "nan":
+        logits[0, [3, 7]] = [np.nan, np.inf]
+    elif special == "two_finite":
+        logits[0, :] = -np.inf
+        logits[0, [E - 1, 2]] = [0.5, 0.25]
+    ids_r, rw_r = orc.router_topk(logits, k, 0.75)
+    ids_r, rw_r = ids_r[0], rw_r[0]
+    out0 = np.random.default_rng(116).standard_normal(hid).astype(np.float32)
+    out_d = dev(out0)
+    act_d = empty_f32(k, ffn)
+    ids_d = torch.full((k,), -5, dtype=torch.int32, device="cuda")
+    rw_d = empty_f32(k)
+    banner(f"moe facade from logits E={E} k={k} {special}")
+    qlin.call("qlin_moe_routed_decode_indexed_logits", Q4_K, dev(wg), dev(wu), wg.size, Q5_0, dev(wdn), wdn.size, E,
+              ffn, hid, hid, dev(x), dev(logits), 0.75, ids_d, rw_d, act_d, out_d, k)
+    assert np.array_equal(host(ids_d), ids_r)
+    assert np.allclose(host(rw_d), rw_r, rtol=1e-5, atol=1e-7)
+    act_ref = orc.swiglu_indexed(Q4_K, wg, wu, geb, geb, grb, grb, x, ids_r, ffn, hid)
+    ref = orc.down_indexed_ordered(Q5_0, wdn, deb, drb, act_ref, ids_r, host(rw_d), out0, hid, ffn)
+    assert normwise_rel_err(host(out_d) - out0, ref - out0) <= 1e-4
+
+
 def _moe_batch(gu_type, dn_type, E, ffn, hid, tokens, k, seed):
     wg, grb, geb = _experts(gu_type, E, ffn, hid, seed)
     wu, _, _ = _experts(gu_type, E, ffn, hid, seed + 1)
