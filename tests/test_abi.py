@@ -169,6 +169,77 @@ def test_moe_grouped_validation():
     assert run(tokens=0, wsb=0) == OK  # nothing to do
 
 
+def test_moe_from_logits_validation():
+    """The routing forms: the indexed or batched call's rules, the router's expert limit, and the logits,
+    ids and weights required; nothing to do returns before any launch."""
+    need = qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 64, 1408, 2048)
+    g = dict(gate=FAKE, up=FAKE, gub=64 * 1408 * 1152, down=FAKE, db=64 * 2048 * 968, ne=64, ffn=1408, ind=2048,
+             hid=2048, x=FAKE, lg=FAKE, ids=FAKE, rw=FAKE, ws=FAKE, wsb=need, out=FAKE, tokens=16, k=6)
+
+    def grouped(gu=12, dt=6, **kw):
+        v = {**g, **kw}
+        return qlin.status("qlin_moe_routed_decode_grouped_logits", gu, v["gate"], v["up"], v["gub"], dt, v["down"],
+                           v["db"], v["ne"], v["ffn"], v["ind"], v["hid"], v["x"], v["lg"], 1.0, v["ids"], v["rw"],
+                           v["ws"], v["wsb"], v["out"], v["tokens"], v["k"])
+    assert grouped(dt=2) == UNSUP
+    assert grouped(lg=0) == NULL
+    assert grouped(ids=0) == NULL
+    assert grouped(rw=0) == NULL
+    assert grouped(ne=257, gub=257 * 1408 * 1152, db=257 * 2048 * 968,
+                   wsb=qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 257, 1408, 2048)) == LIMIT
+    assert grouped(wsb=need - 1) == LIMIT
+    assert grouped(tokens=0, wsb=0) == OK
+
+    t = dict(gate=FAKE, up=FAKE, gub=64 * 1408 * 1152, down=FAKE, db=64 * 2048 * 968, ne=64, ffn=1408, ind=2048,
+             hid=2048, x=FAKE, lg=FAKE, ids=FAKE, rw=FAKE, act=FAKE, out=FAKE, k=6)
+
+    def token(gu=12, dt=6, **kw):
+        v = {**t, **kw}
+        return qlin.status("qlin_moe_routed_decode_indexed_logits", gu, v["gate"], v["up"], v["gub"], dt, v["down"],
+                           v["db"], v["ne"], v["ffn"], v["ind"], v["hid"], v["x"], v["lg"], 1.0, v["ids"], v["rw"],
+                           v["act"], v["out"], v["k"])
+    assert token(ids=0) == NULL
+    assert token(lg=0) == NULL
+    assert token(act=0) == NULL
+    assert token(x=0) == NULL
+    assert token(dt=2) == UNSUP
+    assert token(gu=8) == UNSUP
+    assert token(ne=257, gub=257 * 1408 * 1152, db=257 * 2048 * 968) == LIMIT
+    assert token(dt=12) == SHAPE       # Q4_K down with ffn 1408: not a multiple of 256
+    assert token(ids=FAKE + 2) == ALIGN
+    assert token(k=0) == OK
+
+
+def test_fused_decoder_launch_validation():
+    """The norm fused into the decode GEMV and SwiGLU, and the rotary embedding fused into attention."""
+    x, w, nw = FAKE, FAKE, FAKE
+    # qlin_launch_rms_norm_quant_gemv_multi(type, n, weights[], rb, x, norm_w, norm_type, eps, one_plus, ys[], dims[], k)
+    import ctypes as C
+    wa = (C.c_void_p * 1)(w)
+    ya = (C.c_void_p * 1)(FAKE)
+    da = (C.c_int * 1)(16)
+    multi = lambda nt=0, k=96, nwp=nw: qlin.status(
+        "qlin_launch_rms_norm_quant_gemv_multi", 8, 1, C.addressof(wa), 102, x, nwp, nt, 1e-6, 0, C.addressof(ya),
+        C.addressof(da), k)
+    assert multi(nt=2) == SHAPE
+    assert multi(nwp=0) == NULL
+    assert multi(nwp=FAKE + 1) == ALIGN
+    assert multi() == LIMIT            # in_dim 96: not whole 128-weight chunks for the matrix-core kernels
+    sw = lambda nt=0, k=96, nwp=nw: qlin.status("qlin_launch_rms_norm_quant_swiglu", 8, w, w, 102, x, nwp, nt, 1e-6, 0,
+                                                FAKE, 16, k)
+    assert sw(nt=2) == SHAPE
+    assert sw(nwp=0) == NULL
+    assert sw() == LIMIT
+    # qlin_launch_rope_attend(q, k, v, kc, vc, attn, n_heads, kv_heads, head_dim, max_seq, pos, theta)
+    ra = lambda q=FAKE, nh=14, nkv=2, hd=64, ms=512: qlin.status("qlin_launch_rope_attend", q, FAKE, FAKE, FAKE, FAKE,
+                                                                 FAKE, nh, nkv, hd, ms, FAKE, 1e6)
+    assert ra(nh=15) == SHAPE
+    assert ra(hd=512) == LIMIT
+    assert ra(ms=1 << 16) == LIMIT
+    assert ra(q=0) == NULL
+    assert ra(q=FAKE + 4) == ALIGN
+
+
 def test_swiglu_and_down_validation():
     assert qlin.status("qlin_launch_quant_swiglu_indexed", 12, FAKE, FAKE, 100, 100, 144, 144, FAKE, FAKE, FAKE,
                        2, 1, 256) == ROWB
