@@ -125,6 +125,34 @@ __device__ __forceinline__ float block_value(const uint8_t *b, int e) {
     else return q40_value(b, e);
 }
 
+// ---- prefill GEMM tile order ---------------------------------------------------------------------
+// The tile (weight tile bx of nx, token tile by of ny) of workgroup L of a one-dimensional grid of
+// nx * ny.  Workgroups go to the 8 XCDs in turn (L % 8), and each XCD has its own L2: XCD x takes
+// weight tiles x, x + 8, ... and runs a weight tile's ny token tiles one after another, so each
+// weight tile is fetched once into the L2 that all its workgroups read.  Weight tiles past the last
+// multiple of 8 follow in the same token-tile-minor order.
+#ifndef QLIN_GEMM_XCD
+#define QLIN_GEMM_XCD 1
+#endif
+__device__ __forceinline__ void gemm_tile(int nx, int ny, int &bx, int &by) {
+#if QLIN_GEMM_XCD
+    const int L = blockIdx.x, nx8 = nx & ~7, head = nx8 * ny;
+    if (L < head) {
+        const int i = L >> 3, u = i / ny;
+        bx = u * 8 + (L & 7);
+        by = i - u * ny;
+    } else {
+        const int r = L - head, u = r / ny;
+        bx = nx8 + u;
+        by = r - u * ny;
+    }
+#else
+    bx = blockIdx.x;
+    by = blockIdx.y;
+#endif
+}
+inline dim3 gemm_grid(int nx, int ny) { return QLIN_GEMM_XCD ? dim3(nx * ny) : dim3(nx, ny); }
+
 // ---- wave64 reductions ------------------------------------------------------------------------
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -100,8 +100,10 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const GemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.y * kBM;
-    const int o0 = blockIdx.x * kBN + wave * kNT * 16;
+    int bx, by;
+    gemm_tile((a.n + kBN - 1) / kBN, (a.m + kBM - 1) / kBM, bx, by);
+    const int m0 = by * kBM;
+    const int o0 = bx * kBN + wave * kNT * 16;
 
     const uint8_t *wrow[kNT];
 #pragma unroll
@@ -359,7 +361,7 @@ hipError_t q4k_gemm_q8_1(const uint8_t *w, size_t rb, const uint8_t *xq, float *
     a.n = out_dim;
     a.m = m;
     a.nsb = in_dim / 256;
-    const dim3 grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
+    const dim3 grid = gemm_grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
     hipLaunchKernelGGL(q4k_gemm_kernel, grid, dim3(kThreads), kLdsBytes, s, a);
     return hipGetLastError();
 }

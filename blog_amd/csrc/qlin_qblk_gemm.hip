@@ -186,10 +186,10 @@ struct ActStage {
     struct Raw {
         uint32_t bh[kJJ], q0[kJJ], q1[kJJ];
     };
-    __device__ ActStage(uint4 *l, const GemmArgs &a, int tid)
+    __device__ ActStage(uint4 *l, const GemmArgs &a, int tid, int m0)
         : lds(l), smt(tid / (kSJ * 64)), sjh((tid >> 6) % kSJ), sl(tid & 63), si(tid & 15), sg((tid & 63) >> 4),
           nblk(a.nblk), nunit((a.nblk + 7) / 8) {
-        const int tok = blockIdx.y * kBM + smt * 16 + si;
+        const int tok = m0 + smt * 16 + si;
         xrow = a.xq + static_cast<size_t>(min(tok, a.m - 1)) * a.xrb;
     }
     __device__ uint4 *plane(int buf) const { return lds + buf * kBuf; }
@@ -272,9 +272,11 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
     extern __shared__ uint4 lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.y * kBM;
-    const int o0 = blockIdx.x * kBN + wave * kNT * 16;
-    const ActStage st(lds, a, tid);
+    int bx, by;
+    gemm_tile((a.n + kBN - 1) / kBN, (a.m + kBM - 1) / kBM, bx, by);
+    const int m0 = by * kBM;
+    const int o0 = bx * kBN + wave * kNT * 16;
+    const ActStage st(lds, a, tid, m0);
     const int nblk = a.nblk, nunit = st.nunit;
 
     const uint8_t *wrow[kNT];
@@ -406,9 +408,11 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_kernel(const GemmArgs a) {
     extern __shared__ uint4 lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4, gb = g >> 1;
-    const int m0 = blockIdx.y * kBM;
-    const int o0 = blockIdx.x * kBN + wave * kNT * 16;
-    const ActStage st(lds, a, tid);
+    int bx, by;
+    gemm_tile((a.n + kBN - 1) / kBN, (a.m + kBM - 1) / kBM, bx, by);
+    const int m0 = by * kBM;
+    const int o0 = bx * kBN + wave * kNT * 16;
+    const ActStage st(lds, a, tid, m0);
     const int nsb = a.nblk / 8;  // super-blocks per row (even)
 
     const uint8_t *wrow[kNT];
@@ -562,7 +566,7 @@ hipError_t qblk_gemm_q8_1(int type, const uint8_t *w, size_t rb, const uint8_t *
     a.n = out_dim;
     a.m = m;
     a.nblk = in_dim / 32;
-    const dim3 grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
+    const dim3 grid = gemm_grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
     switch (type) {
         case T_Q8_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q8_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
         case T_Q5_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q5_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
