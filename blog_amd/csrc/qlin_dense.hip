@@ -28,6 +28,9 @@
 namespace qlin {
 namespace {
 
+#ifndef QLIN_DENSE_XFIRST
+#define QLIN_DENSE_XFIRST 1
+#endif
 constexpr int kDWaves = 8, kDThreads = kDWaves * 64;
 constexpr int kDTokens = 64;  // tokens per grid row (4 tiles of 16)
 
@@ -91,17 +94,38 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
             for (int w = 0; w < NW; ++w) load_q4k(cur[w], rp[w] + static_cast<size_t>(sb) * 144, g);
         }
         while (sb < nsb) {  // uniform
+#if QLIN_DENSE_XFIRST
+            // the super-block's x first, then the next weights: a wait for x then never waits for
+            // the weight prefetch (the memory counter completes in issue order), and the 16 loads
+            // share one round trip instead of one per few sub-blocks
+            const float *xr = xrow + sb * 256;
+            float4 xs[16];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xs[2 * j] = *reinterpret_cast<const float4 *>(xr + 32 * j);
+                xs[2 * j + 1] = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#endif
             const int sb2 = sb + kDWaves;
             Q4KRaw nxt[NW];
             if (sb2 < nsb) {  // uniform
 #pragma unroll
                 for (int w = 0; w < NW; ++w) load_q4k(nxt[w], rp[w] + static_cast<size_t>(sb2) * 144, g);
             }
+#if QLIN_DENSE_XFIRST
+            __builtin_amdgcn_sched_barrier(0);
+#else
             const float *xr = xrow + sb * 256;
+#endif
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
+#if QLIN_DENSE_XFIRST
+                const float4 x0 = xs[2 * j], x1 = xs[2 * j + 1];
+#else
                 const float4 x0 = *reinterpret_cast<const float4 *>(xr + 32 * j);
                 const float4 x1 = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
+#endif
                 uint32_t h[4], l[4];
                 split_bf16x2(x0.x, x0.y, h[0], l[0]);
                 split_bf16x2(x0.z, x0.w, h[1], l[1]);
