@@ -814,4 +814,78 @@ int qlin_moe_routed_decode_grouped_noalloc(int gu_type, const uint8_t *gate, con
                                           tokens, k);
 }
 
+size_t qlin_moe_ffn_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size, int shared_ffn) {
+    if (shared_ffn < 0) return 0;
+    const size_t routed = qlin_moe_grouped_workspace_bytes(tokens, k, n_experts, ffn_dim, hidden_size);
+    if (routed == 0) return 0;
+    return routed + ((static_cast<size_t>(tokens) * static_cast<size_t>(shared_ffn) * sizeof(float) + 255) & ~size_t{255});
+}
+
+// MoE::forward's routed and shared experts (MoE.cpp:29-52, after the norm, before the residual add):
+// the batched routed decode from the logits, then the shared experts' SwiGLU and down-add.  When the
+// shared down-add takes the m > 1 matrix-core kernel, that launch also applies the routed combine
+// (one launch fewer); either way out gets (out + routed) + shared, as the three calls give it.
+int qlin_moe_ffn_decode_grouped_logits(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                       int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
+                                       int ffn_dim, int in_dim, int hidden, int shared_type, const uint8_t *shared_gate,
+                                       const uint8_t *shared_up, size_t shared_gate_up_rb, const uint8_t *shared_down,
+                                       size_t shared_down_rb, int shared_ffn, const float *x,
+                                       const float *router_logits, float routed_scaling, int *ids, float *rw,
+                                       void *workspace, size_t workspace_bytes, float *out, int tokens, int k) {
+    if (shared_ffn < 0) return QLIN_ERR_SHAPE;
+    int rc = grouped_check(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts, ffn_dim, in_dim,
+                           hidden, x, ids, rw, workspace, workspace_bytes, out, tokens, k);
+    if (rc) return rc;
+    if (n_experts > 256) return QLIN_ERR_LIMIT;  // the router's limit
+    const bool shared = shared_ffn > 0;
+    if (shared) {
+        if ((rc = check_weight(shared_type, shared_gate, shared_gate_up_rb, shared_ffn, in_dim)) ||
+            (rc = check_weight(shared_type, shared_up, shared_gate_up_rb, shared_ffn, in_dim)) ||
+            (rc = check_weight(shared_type, shared_down, shared_down_rb, hidden, shared_ffn)))
+            return rc;
+    }
+    if (tokens == 0) return QLIN_OK;
+    if (!x || !out || (shared && !workspace)) return QLIN_ERR_NULL;
+    if ((rc = check_f32(x, true)) || (rc = check_f32(out, true))) return rc;
+    if (shared && workspace_bytes < qlin_moe_ffn_workspace_bytes(tokens, k, n_experts, ffn_dim, hidden, shared_ffn))
+        return QLIN_ERR_LIMIT;
+    if (shared && (reinterpret_cast<uintptr_t>(workspace) & 255u)) return QLIN_ERR_ALIGN;
+    if (k > 0 && (rc = check_f32(router_logits, true))) return rc;
+    // the shared activations [tokens, shared_ffn] follow the routed part's workspace
+    float *sact = shared ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) +
+                                                     qlin::moe_grouped_workspace(tokens, k, n_experts, ffn_dim, hidden))
+                         : nullptr;
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const bool fuse = k > 0 && shared && tokens > 1 &&
+                      qlin::moe_grouped_up_ok(gu_type, gate, up, g_eb, g_rb, x, in_dim, ffn_dim, n_experts, tokens * k) &&
+                      qlin::dense_ok(shared_type, shared_down, nullptr, shared_down_rb, sact, shared_ffn);
+    if (fuse) {
+        const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+        const size_t d_rb = d_eb / static_cast<size_t>(hidden);
+        const qlin::MoeRouter router{router_logits, routed_scaling, ids, rw};
+        qlin::RouteCombine routed{};
+        hipError_t e = qlin::moe_grouped(gu_type, gate, up, g_eb, g_rb, down_type, down, d_eb, d_rb, n_experts, ffn_dim,
+                                         in_dim, hidden, x, nullptr, nullptr, workspace, out, tokens, k, stream(),
+                                         &router, &routed);
+        if (e != hipSuccess) return launched(e);
+        if ((rc = qlin_launch_quant_swiglu_rows(shared_type, shared_gate, shared_up, shared_gate_up_rb,
+                                                shared_gate_up_rb, x, sact, shared_ffn, in_dim, tokens)))
+            return rc;
+        return launched(qlin::dense_matmul(shared_type, shared_down, nullptr, shared_down_rb, sact, out, hidden,
+                                           shared_ffn, tokens, 1, stream(), &routed));
+    }
+    if (k > 0 && (rc = qlin_moe_routed_decode_grouped_logits(gu_type, gate, up, gate_up_bytes, down_type, down,
+                                                             down_bytes, n_experts, ffn_dim, in_dim, hidden, x,
+                                                             router_logits, routed_scaling, ids, rw, workspace,
+                                                             workspace_bytes, out, tokens, k)))
+        return rc;
+    if (!shared) return QLIN_OK;
+    if ((rc = qlin_launch_quant_swiglu_rows(shared_type, shared_gate, shared_up, shared_gate_up_rb, shared_gate_up_rb,
+                                            x, sact, shared_ffn, in_dim, tokens)))
+        return rc;
+    return qlin_launch_quant_matmul_add(shared_type, shared_down, shared_down_rb, sact, out, hidden, shared_ffn,
+                                        tokens);
+}
+
 }  // extern "C"

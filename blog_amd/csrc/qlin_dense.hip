@@ -42,7 +42,46 @@ struct DenseArgs {
     const float *x;
     float *y;
     int n, k, m;
+    RouteCombine c;  // kAdd: a batched MoE decode's deferred combine (c.yr non-null), added before the product
 };
+
+// The deferred combine's routed total of (token t, row h): the routes in route order from 0, as the
+// combine launch forms it (qlin_moe_grouped.hip).
+__device__ __forceinline__ float routed_total(const RouteCombine &c, int t, int h, int hidden) {
+    constexpr int kLoadsFirst = 16;
+    float total = 0.0f;
+    if (c.k <= kLoadsFirst) {  // uniform
+        // every route's id, weight and result requested at once (one round trip), then the same sum
+        // (a route without an expert has no result written; its value is read but not used)
+        int e[kLoadsFirst];
+        float y[kLoadsFirst], w[kLoadsFirst];
+#pragma unroll
+        for (int r = 0; r < kLoadsFirst; ++r) {
+            if (r < c.k) {
+                const int route = t * c.k + r;
+                e[r] = c.ids[route];
+                w[r] = c.rw[route];
+                y[r] = c.yr[static_cast<size_t>(route) * hidden + h];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kLoadsFirst; ++r)
+            if (r < c.k && e[r] >= 0 && e[r] < c.n_experts) total = fmaf(y[r], w[r], total);
+        return total;
+    }
+    for (int r = 0; r < c.k; ++r) {
+        const int route = t * c.k + r, e = c.ids[route];
+        if (e < 0 || e >= c.n_experts) continue;
+        total = fmaf(c.yr[static_cast<size_t>(route) * hidden + h], c.rw[route], total);
+    }
+    return total;
+}
+// y = (y + routed total) + v: the combine launch's y += total, then the plain add
+__device__ __forceinline__ void add_out(const DenseArgs &a, float *yo, int t, int h, float v) {
+    float y = *yo;
+    if (a.c.yr) y += routed_total(a.c, t, h, a.n);  // uniform
+    *yo = y + v;
+}
 
 // The raw bytes a lane needs of one Q4_K super-block: the header (d, dmin, 12 scale bytes) and,
 // for each pair c of sub-blocks, qs bytes 32c + 8g .. 32c + 8g + 7 (low nibbles: sub-block 2c,
@@ -175,7 +214,7 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
         }
         float *yo = a.y + static_cast<size_t>(t) * a.n + row0 + o;
         if constexpr (MODE == kSwiGLU) *yo = v0 / (1.0f + expf(-v0)) * v1;
-        else if constexpr (MODE == kAdd) *yo += v0;
+        else if constexpr (MODE == kAdd) add_out(a, yo, t, row0 + o, v0);
         else *yo = v0;
     }
 }
@@ -316,7 +355,7 @@ __global__ __launch_bounds__(kDThreads) void dense_generic_kernel(const DenseArg
         }
         float *yo = a.y + static_cast<size_t>(t) * a.n + row0 + o;
         if constexpr (MODE == kSwiGLU) *yo = v0 / (1.0f + expf(-v0)) * v1;
-        else if constexpr (MODE == kAdd) *yo += v0;
+        else if constexpr (MODE == kAdd) add_out(a, yo, t, row0 + o, v0);
         else *yo = v0;
     }
 }
@@ -344,9 +383,10 @@ bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t rb, const f
 }
 
 hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t rb, const float *x, float *y, int n,
-                        int k, int m, int mode, hipStream_t s) {
+                        int k, int m, int mode, hipStream_t s, const RouteCombine *combine) {
     if (n == 0 || m == 0) return hipSuccess;
-    const DenseArgs a{w0, w1 ? w1 : w0, rb, x, y, n, k, m};
+    DenseArgs a{w0, w1 ? w1 : w0, rb, x, y, n, k, m, RouteCombine{}};
+    if (combine && mode == kAdd) a.c = *combine;
     const dim3 grid((n + 15) / 16, (m + kDTokens - 1) / kDTokens);
     switch (type) {
         case T_Q4_K: break;

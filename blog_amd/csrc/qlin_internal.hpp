@@ -39,6 +39,16 @@ struct MoeRouter {
     int *ids;
     float *w;
 };
+// The routed part of a batched MoE decode handed to a later launch instead of the combine launch:
+// per-route results yr [tokens * k, hidden] and the routes' ids and weights [tokens, k].  A launch
+// that applies it adds, per (token t, hidden row h), the routes in route order as the combine does:
+// total = fmaf(yr[t k + r][h], rw[t k + r], total) over the routes with 0 <= id < n_experts, from 0.
+struct RouteCombine {
+    const float *yr;
+    const int *ids;
+    const float *rw;
+    int k, n_experts;
+};
 // An RMSNorm applied to x as the decode kernels stage it: x[j] * rsqrt(mean x^2 + eps) * w[j], w bf16
 // (type 0) or f16 (1), plus one if one_plus.
 struct RmsNorm {
@@ -74,8 +84,10 @@ hipError_t mfma_down_routed(int type, const uint8_t *wd, size_t expert_bytes, si
 // Q4_K over m > 1 rows of f32 activations on the f32 matrix cores (qlin_dense.hip): mode 0 stores
 // y[r, o], 1 adds into it, 2 writes act[r, o] = silu(gate . x_r) * (up . x_r) with w1 the up matrix.
 bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, const float *x, int in_dim);
+// mode 1 (y +=) with combine: y = (y + the routed total) + the product, as the combine launch and then
+// the plain mode 1 give it
 hipError_t dense_matmul(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, const float *x, float *y,
-                        int out_dim, int in_dim, int m, int mode, hipStream_t s);
+                        int out_dim, int in_dim, int m, int mode, hipStream_t s, const RouteCombine *combine = nullptr);
 
 // MLA over the Q8_1 latent cache (qlin_mla_latent.hip); pos is read from d_pos on the device.
 hipError_t mla_store_latent_q8_1(const float *kv_cache, uint8_t *cache, int kv_lora, int qk_rope, size_t row_bytes,
@@ -158,11 +170,13 @@ bool moe_grouped_shape_ok(int n_experts, int64_t routes);
 bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
                        const float *x, int in_dim, int ffn_dim, int n_experts, int routes);
 // router non-null: ids and rw are ignored, the routes are router_topk's of the logits (inside the gate/up
-// launch for n_experts <= 64 when its LDS allows, else one router launch first).
+// launch for n_experts <= 64 when its LDS allows, else one router launch first).  defer non-null: out is
+// not touched; the combine is left to the caller, whose launch applies *defer (filled here).
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int n_experts, int ffn_dim, int in_dim,
                        int hidden, const float *x, const int *ids, const float *rw, void *workspace, float *out,
-                       int tokens, int k, hipStream_t s, const MoeRouter *router = nullptr);
+                       int tokens, int k, hipStream_t s, const MoeRouter *router = nullptr,
+                       RouteCombine *defer = nullptr);
 
 // Quantized embedding rows and the MLA latent-absorption products over kv_b (qlin_embed_mla.hip).
 hipError_t quant_embedding(int type, const int *ids, float *out, const uint8_t *table, size_t row_bytes, int hidden,

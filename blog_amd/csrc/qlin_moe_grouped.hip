@@ -1003,7 +1003,7 @@ bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t eb
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int E, int ffn, int K, int hidden,
                        const float *x, const int *ids, const float *rw, void *ws, float *out, int tokens, int k,
-                       hipStream_t s, const MoeRouter *router) {
+                       hipStream_t s, const MoeRouter *router, RouteCombine *defer) {
     (void)gu_type;  // Q4_K (moe_grouped_up_ok)
     const int R = tokens * k;
     if (R == 0 || hidden == 0) return hipSuccess;
@@ -1088,6 +1088,10 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
             case T_Q6_K: hipLaunchKernelGGL(down_kernel<T_Q6_K>, dgrid, dim3(256), 0, s, da); break;
             default: return hipErrorInvalidValue;
         }
+    }
+    if (defer) {
+        *defer = RouteCombine{yr, ids, rw, k, E};
+        return hipGetLastError();
     }
     const int64_t outs = static_cast<int64_t>(tokens) * hidden;
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s, yr, ids, rw,

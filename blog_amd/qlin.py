@@ -73,6 +73,9 @@ SIGNATURES = {
     "qlin_moe_grouped_workspace_bytes": (SZ, [I, I, I, I, I]),
     "qlin_moe_routed_decode_grouped": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, SZ, P, I, I]),
     "qlin_moe_routed_decode_grouped_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, F, P, P, P, SZ, P, I, I]),
+    "qlin_moe_ffn_workspace_bytes": (SZ, [I, I, I, I, I, I]),
+    "qlin_moe_ffn_decode_grouped_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, I, P, P, SZ, P, SZ, I, P, P, F, P, P,
+                                               P, SZ, P, I, I]),
     "qlin_moe_routed_decode_grouped_noalloc": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, I, I]),
     # include/qlin_decoder.h
     "qlin_launch_rms_norm": (I, [P, P, P, I, I, I, F, I]),

@@ -281,6 +281,30 @@ int qlin_moe_routed_decode_grouped_logits(int gate_up_type, const uint8_t *gate_
                                           int *expert_ids, float *route_weights, void *workspace,
                                           size_t workspace_bytes, float *out, int tokens, int k);
 
+/* The routed and shared experts of one MoE FFN layer for a batch of decode tokens: MoE::forward after
+ * its norm and before its residual add (MoE.cpp:29-52 with SharedExperts.cpp:25-55), from the router
+ * logits.  out [tokens, hidden_size] gets (out + the routed sum) + the shared experts' down projection
+ * of SiLU(shared gate x) * (shared up x), each token's result exactly that of
+ * qlin_moe_routed_decode_grouped_logits followed by qlin_launch_quant_swiglu_rows and
+ * qlin_launch_quant_matmul_add on the shared weights, which is what the call runs when the shared
+ * down projection cannot take the m > 1 matrix-core kernel; when it can (tokens > 1), that launch
+ * also adds the routed sum, so the separate combine launch is not needed.  Shared weights:
+ * gate and up [shared_ffn, in_dim] of shared_type with rows of shared_gate_up_row_bytes, down
+ * [hidden_size, shared_ffn] with rows of shared_down_row_bytes; shared_ffn = 0 runs the routed part
+ * alone.  workspace: at least qlin_moe_ffn_workspace_bytes(...) bytes, 256-byte aligned (the routed
+ * part's workspace, then the shared activations).  Other arguments and limits as
+ * qlin_moe_routed_decode_grouped_logits's; k = 0 runs the shared experts alone. */
+size_t qlin_moe_ffn_workspace_bytes(int tokens, int k, int n_experts, int ffn_dim, int hidden_size, int shared_ffn);
+int qlin_moe_ffn_decode_grouped_logits(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                       size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                       size_t down_bytes, int n_experts, int ffn_dim, int in_dim, int hidden_size,
+                                       int shared_type, const uint8_t *shared_gate, const uint8_t *shared_up,
+                                       size_t shared_gate_up_row_bytes, const uint8_t *shared_down,
+                                       size_t shared_down_row_bytes, int shared_ffn, const float *x,
+                                       const float *router_logits, float routed_scaling, int *expert_ids,
+                                       float *route_weights, void *workspace, size_t workspace_bytes, float *out,
+                                       int tokens, int k);
+
 /* No counterpart in the reference: qlin_moe_routed_decode_grouped for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops that forbid it).  The same arguments
  * without the workspace: the call runs on a scratch array the library keeps on each GPU for the

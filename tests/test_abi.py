@@ -210,6 +210,39 @@ def test_moe_from_logits_validation():
     assert token(k=0) == OK
 
 
+def test_moe_ffn_validation():
+    """The MoE FFN call: the batched routing call's rules, the shared weights' checks and the larger workspace
+    (the shared activations after the routed part), all before any launch."""
+    need = qlin.lib().qlin_moe_ffn_workspace_bytes(16, 6, 64, 1408, 2048, 2816)
+    assert need == qlin.lib().qlin_moe_grouped_workspace_bytes(16, 6, 64, 1408, 2048) + 16 * 2816 * 4
+    assert qlin.lib().qlin_moe_ffn_workspace_bytes(16, 6, 64, 1408, 2048, -1) == 0
+    g = dict(gate=FAKE, up=FAKE, gub=64 * 1408 * 1152, down=FAKE, db=64 * 2048 * 968, ne=64, ffn=1408, ind=2048,
+             hid=2048, st=12, sg=FAKE, su=FAKE, srb=1152, sd=FAKE, sdrb=1584, sffn=2816, x=FAKE, lg=FAKE, ids=FAKE,
+             rw=FAKE, ws=FAKE, wsb=need, out=FAKE, tokens=16, k=6)
+
+    def ffn(gu=12, dt=6, **kw):
+        v = {**g, **kw}
+        return qlin.status("qlin_moe_ffn_decode_grouped_logits", gu, v["gate"], v["up"], v["gub"], dt, v["down"],
+                           v["db"], v["ne"], v["ffn"], v["ind"], v["hid"], v["st"], v["sg"], v["su"], v["srb"],
+                           v["sd"], v["sdrb"], v["sffn"], v["x"], v["lg"], 1.0, v["ids"], v["rw"], v["ws"], v["wsb"],
+                           v["out"], v["tokens"], v["k"])
+    assert ffn(dt=2) == UNSUP
+    assert ffn(st=99) == UNSUP
+    assert ffn(sffn=-1) == SHAPE
+    assert ffn(sffn=2800) == SHAPE          # the shared down's inner dimension: not whole Q4_K super-blocks
+    assert ffn(lg=0) == NULL
+    assert ffn(ids=0) == NULL
+    assert ffn(sg=0) == NULL
+    assert ffn(sd=0) == NULL
+    assert ffn(srb=1151) == ROWB
+    assert ffn(sg=FAKE + 1) == ALIGN
+    assert ffn(ne=257, gub=257 * 1408 * 1152, db=257 * 2048 * 968,
+               wsb=qlin.lib().qlin_moe_ffn_workspace_bytes(16, 6, 257, 1408, 2048, 2816)) == LIMIT
+    assert ffn(wsb=need - 1) == LIMIT       # room for the routed part, not for the shared activations
+    assert ffn(ws=FAKE + 16) == ALIGN
+    assert ffn(tokens=0, wsb=0) == OK
+
+
 def test_fused_decoder_launch_validation():
     """The norm fused into the decode GEMV and SwiGLU, and the rotary embedding fused into attention."""
     x, w, nw = FAKE, FAKE, FAKE

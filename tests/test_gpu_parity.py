@@ -766,6 +766,64 @@ def test_moe_grouped_unaligned_output():
     assert normwise_rel_err(host(out_d).reshape(tokens, hid) - out0, ref - out0) <= 1e-4
 
 
+@pytest.mark.parametrize("gu,E,tokens,k,ffn,hid,sffn,stype", [
+    (Q4_K, 64, 16, 6, 1408, 2048, 2816, Q4_K),  # C5: the shared down-add applies the routed sum
+    (Q4_K, 8, 5, 2, 256, 512, 512, Q4_K),       # a short batch, same form
+    (Q4_K, 8, 6, 2, 256, 512, 160, Q8_0),       # shared Q8_0 (f32-element matrix-core kernel), same form
+    (Q4_K, 8, 1, 2, 256, 512, 512, Q4_K),       # one token: the shared down-add is the decode GEMV, own combine
+    (Q6_K, 8, 4, 2, 256, 512, 512, Q4_K),       # Q6_K gate/up: the per-token routed path, then the shared calls
+    (Q4_K, 16, 4, 0, 256, 512, 512, Q4_K),      # no routes: the shared experts alone
+    (Q4_K, 16, 4, 3, 256, 512, 0, Q4_K),        # no shared experts: the routed call alone
+])
+def test_moe_ffn_matches_three_calls(gu, E, tokens, k, ffn, hid, sffn, stype):
+    """The MoE FFN call (routed from the logits, then the shared experts) gives, bit for bit, what the
+    routed call from logits followed by qlin_launch_quant_swiglu_rows and qlin_launch_quant_matmul_add
+    give on the same inputs, and the per-token reference's routed sum plus the shared experts to 1e-4."""
+    wg, wu, grb, geb, wdn, drb, deb, x, _, _ = _moe_batch(gu, Q5_0, E, ffn, hid, tokens, k, 401 + E + tokens)
+    rng = np.random.default_rng(411 + tokens)
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    if sffn:
+        sg, srb, _ = qgen.random_matrix(stype, sffn, hid, seed=421 + sffn)
+        su, _, _ = qgen.random_matrix(stype, sffn, hid, seed=422 + sffn)
+        sd, sdrb, _ = qgen.random_matrix(stype, hid, sffn, seed=423 + sffn)
+    else:
+        sg = su = sd = np.zeros(16, np.uint8)
+        srb, sdrb = qlin.row_bytes(stype, hid), 0
+    out0 = rng.standard_normal((tokens, hid)).astype(np.float32)
+    d = {n: dev(v) for n, v in dict(wg=wg, wu=wu, wdn=wdn, x=x, lg=logits, sg=sg, su=su, sd=sd).items()}
+    nbytes = qlin.lib().qlin_moe_ffn_workspace_bytes(tokens, k, E, ffn, hid, sffn)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
+    wsp = (ws.data_ptr() + 255) // 256 * 256
+    kk = max(k, 1)
+    out_f, ids_f, rw_f = dev(out0), torch.full((tokens, kk), -7, dtype=torch.int32, device="cuda"), empty_f32(tokens, kk)
+    banner(f"moe ffn fused gu={gu} E={E} tokens={tokens} k={k} shared={sffn} type {stype}")
+    qlin.call("qlin_moe_ffn_decode_grouped_logits", gu, d["wg"], d["wu"], wg.size, Q5_0, d["wdn"], wdn.size, E, ffn,
+              hid, hid, stype, d["sg"], d["su"], srb, d["sd"], sdrb, sffn, d["x"], d["lg"], 1.0, ids_f, rw_f, wsp,
+              nbytes, out_f, tokens, k)
+    out_3, ids_3, rw_3 = dev(out0), torch.full((tokens, kk), -7, dtype=torch.int32, device="cuda"), empty_f32(tokens, kk)
+    sact = empty_f32(tokens, max(sffn, 1))
+    if k:
+        qlin.call("qlin_moe_routed_decode_grouped_logits", gu, d["wg"], d["wu"], wg.size, Q5_0, d["wdn"], wdn.size, E,
+                  ffn, hid, hid, d["x"], d["lg"], 1.0, ids_3, rw_3, wsp, nbytes, out_3, tokens, k)
+    if sffn:
+        qlin.quant_swiglu_rows(stype, d["sg"], d["su"], srb, srb, d["x"], sact, sffn, hid, tokens)
+        qlin.quant_matmul_add(stype, d["sd"], sdrb, sact, out_3, hid, sffn, tokens)
+    torch.cuda.synchronize()
+    assert torch.equal(out_f, out_3)
+    if k:
+        assert torch.equal(ids_f, ids_3) and torch.equal(rw_f, rw_3)
+    ref = out0.copy()
+    if k:
+        ids_r, _ = orc.router_topk(logits, k, 1.0)
+        assert np.array_equal(host(ids_f), ids_r)
+        ref = _moe_batch_ref(gu, Q5_0, wg, wu, grb, geb, wdn, drb, deb, x, ids_r, host(rw_f), out0, ffn, hid)
+    if sffn:
+        for t in range(tokens):
+            act = orc.swiglu(stype, sg, su, srb, srb, x[t], sffn, hid).astype(np.float32)
+            ref[t] = orc.gemv_add(stype, sd, sdrb, act, ref[t], hid, sffn)
+    assert normwise_rel_err(host(out_f) - out0, ref - out0) <= 1e-4
+
+
 def test_moe_grouped_wide_input_two_routes_per_pass():
     """in_dim 10240: four routes' staged activations would not fit in LDS, so gate/up runs two routes
     per pass; every expert has more than two routes (4 experts, 8 tokens x 2 routes)."""

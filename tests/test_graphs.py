@@ -2,7 +2,8 @@
 synchronises or reads back), so a captured call is replayed several times, with the program's own eager work
 and synchronisations between the replays, and every replay must give the eager result bit for bit (the
 kernels sum in fixed orders).  Covers the decode GEMV forms, the fused norm launches, the batched and
-per-token MoE calls (workspace, allocation-free and from router logits) and a whole decoder step."""
+per-token MoE calls (workspace, allocation-free and from router logits), the MoE FFN call (routed and shared
+experts) and a whole decoder step."""
 import numpy as np
 import pytest
 
@@ -138,6 +139,39 @@ def test_graph_moe_grouped(form):
         else:
             qlin.call("qlin_moe_routed_decode_grouped_logits", Q4_K, wgd, wud, wg.size, Q5_0, wdd, wd.size, E, ffn,
                       hid, hid, x, logits, 1.0, ids_o, rw_o, wsp, nbytes, out, tokens, k)
+
+    def reset():
+        out.copy_(out0)
+        ids_o.fill_(-3)
+        rw_o.zero_()
+
+    _replays_match(torch, qlin, run, lambda: [out, ids_o, rw_o], reset)
+
+
+def test_graph_moe_ffn():
+    """The MoE FFN call (routed from the logits, shared experts, the routed sum added in the shared down-add)."""
+    torch, qlin = _env()
+    from gpu_util import dev, empty_f32
+    E, ffn, hid, tokens, k, sffn = 16, 256, 512, 8, 4, 512
+    wg, wu, wd = _moe_mats(E, ffn, hid, 650)
+    sg, srb, _ = qgen.random_matrix(Q4_K, sffn, hid, seed=654)
+    su, _, _ = qgen.random_matrix(Q4_K, sffn, hid, seed=655)
+    sd, sdrb, _ = qgen.random_matrix(Q4_K, hid, sffn, seed=656)
+    wgd, wud, wdd, sgd, sud, sdd = (dev(a) for a in (wg, wu, wd, sg, su, sd))
+    rng = np.random.default_rng(657)
+    x = dev(rng.standard_normal((tokens, hid)).astype(np.float32))
+    logits = dev(rng.standard_normal((tokens, E)).astype(np.float32))
+    out0 = dev(rng.standard_normal((tokens, hid)).astype(np.float32))
+    out = empty_f32(tokens, hid)
+    ids_o = torch.zeros((tokens, k), dtype=torch.int32, device="cuda")
+    rw_o = empty_f32(tokens, k)
+    nbytes = qlin.lib().qlin_moe_ffn_workspace_bytes(tokens, k, E, ffn, hid, sffn)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
+    wsp = (ws.data_ptr() + 255) // 256 * 256
+
+    def run():
+        qlin.call("qlin_moe_ffn_decode_grouped_logits", Q4_K, wgd, wud, wg.size, Q5_0, wdd, wd.size, E, ffn, hid, hid,
+                  Q4_K, sgd, sud, srb, sdd, sdrb, sffn, x, logits, 1.0, ids_o, rw_o, wsp, nbytes, out, tokens, k)
 
     def reset():
         out.copy_(out0)
