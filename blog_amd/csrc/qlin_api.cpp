@@ -199,6 +199,28 @@ int qlin_launch_rms_norm_quant_gemv_multi(int type, int n_mats, const uint8_t *c
     return launched(qlin::mfma_gemv(type, weights, ys, out_dims, n_mats, rb, x, in_dim, false, stream(), &norm));
 }
 
+int qlin_launch_quant_gemv_argmax(int type, const uint8_t *w, size_t rb, const float *x, const uint16_t *norm_weight,
+                                  int norm_type, float eps, int one_plus, float *logits, int out_dim, int in_dim,
+                                  void *scratch, int *out_idx) {
+    if (norm_weight && norm_type != 0 && norm_type != 1) return QLIN_ERR_SHAPE;
+    int rc = check_weight(type, w, rb, out_dim, in_dim);
+    if (rc) return rc;
+    if (out_dim <= 0) return QLIN_ERR_SHAPE;
+    if ((rc = check_f32(x, true)) || (rc = check_f32(logits, true))) return rc;
+    if (!scratch || !out_idx) return QLIN_ERR_NULL;
+    if (!aligned(scratch, 4) || !aligned(out_idx, 4) || !aligned(norm_weight, 2)) return QLIN_ERR_ALIGN;
+    const uint8_t *ws[1] = {w};
+    if (!qlin::mfma_ok(type, ws, 1, rb, x, out_dim, in_dim, false)) return QLIN_ERR_LIMIT;
+    constexpr int kPairs = QLIN_GEMV_ARGMAX_SCRATCH_BYTES / 8;  // (float, int) per workgroup
+    const int grid = qlin::mfma_gemv_pairs(type, w, rb, x, out_dim, in_dim);
+    if (grid <= 0 || grid > kPairs) return QLIN_ERR_LIMIT;
+    float *pv = static_cast<float *>(scratch);
+    int *pi = reinterpret_cast<int *>(pv + kPairs);
+    const qlin::RmsNorm norm{norm_weight, norm_type, eps, one_plus};
+    return launched(qlin::mfma_gemv_argmax(type, w, rb, x, logits, out_dim, in_dim, norm_weight ? &norm : nullptr, pv,
+                                           pi, out_idx, stream()));
+}
+
 int qlin_launch_rms_norm_quant_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x,
                                       const uint16_t *norm_weight, int norm_type, float eps, int one_plus,
                                       float *act, int ffn_dim, int in_dim) {

@@ -61,6 +61,14 @@ struct RmsNorm {
 // with norm, x is first normalized (in the staging, not in memory).
 bool mfma_ok(int type, const uint8_t *const *w, int nmat, size_t row_bytes, const float *x, int total, int in_dim,
              bool swiglu);
+// One matrix's decode GEMV (optionally normalizing x) and the argmax of its outputs, as qlin_launch_argmax
+// gives it: every workgroup writes its pick to pairs_v / pairs_i (mfma_gemv_pairs(...) entries: the
+// launch's workgroup count, 0 when the matrix-core kernel does not take the shape), and one more launch
+// reduces them into *out_idx.
+int mfma_gemv_pairs(int type, const uint8_t *w, size_t row_bytes, const float *x, int out_dim, int in_dim);
+hipError_t mfma_gemv_argmax(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y, int out_dim,
+                            int in_dim, const RmsNorm *norm, float *pairs_v, int *pairs_i, int *out_idx,
+                            hipStream_t s);
 hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const int *rows, int nmat,
                      size_t row_bytes, const float *x, int in_dim, bool add, hipStream_t s,
                      const RmsNorm *norm = nullptr);

@@ -178,7 +178,21 @@ struct MfmaArgs {
     float scaling;
     int *ids_out;
     float *rw_out;
+    // The greedy pick of the outputs (plain launches of one matrix, no add): workgroup b writes the
+    // largest of its rows' outputs and its row, the lowest row among equals (NaN never wins, (-inf, 0)
+    // when nothing beats -inf), to amax_v[b] and amax_i[b]; a later launch reduces the pairs by the
+    // same rule, which gives the argmax of the whole output whatever the order.
+    float *amax_v;
+    int *amax_i;
 };
+
+// (v, i) becomes (v2, i2) when that is larger, or equal at a lower index: the argmax's rule
+__device__ __forceinline__ void pick_better(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
 
 constexpr int kMaxRoutes = 16;  // routes of one routed launch (top-k of one token)
 
@@ -426,7 +440,13 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         }
     };
 
-    if (nsteps == 0) return;  // uniform per workgroup
+    if (nsteps == 0) {  // uniform per workgroup
+        if (!ROUTED && !SWIGLU && a.amax_v && tid == 0) {
+            a.amax_v[bid] = -INFINITY;
+            a.amax_i[bid] = 0;
+        }
+        return;
+    }
 
     // x first: requested before any weight load of the workgroup.  Every load is branch-free, which
     // lets the compiler wait for exactly the loads a step consumes and keep the younger ones in
@@ -961,6 +981,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         }
         return;
     }
+    float best_v = -INFINITY;  // the greedy pick over the rows this thread writes (amax_v set)
+    int best_i = 0;
     auto write_row = [&](int r, const float (&tot)[NW]) {
         const int gr = grow(r);
         if constexpr (ROUTED) {
@@ -975,6 +997,27 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             int local;
             mats.locate(gr, wp, yp, local);
             yp[local] = a.add ? yp[local] + tot[0] : tot[0];
+            pick_better(best_v, best_i, tot[0], gr);
+        }
+    };
+    // the workgroup's pick: the threads', then the waves' (the rule does not depend on the order)
+    auto write_pick = [&]() {
+        if constexpr (!ROUTED && !SWIGLU) {
+            if (!a.amax_v) return;  // uniform
+            __shared__ float s_pv[kWaves];
+            __shared__ int s_pi[kWaves];
+#pragma unroll
+            for (int m = 32; m > 0; m >>= 1) pick_better(best_v, best_i, __shfl_xor(best_v, m, 64), __shfl_xor(best_i, m, 64));
+            if (lane == 0) {
+                s_pv[wave] = best_v;
+                s_pi[wave] = best_i;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                for (int w = 1; w < kWaves; ++w) pick_better(best_v, best_i, s_pv[w], s_pi[w]);
+                a.amax_v[bid] = best_v;
+                a.amax_i[bid] = best_i;
+            }
         }
     };
     // Each row's step partials added in a fixed order.  With many chunks, L consecutive lanes share
@@ -997,6 +1040,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             }
             if (live && j == 0) write_row(r, tot);
         }
+        write_pick();
         return;
     }
     for (int r = tid; r < nrows; r += kThreads) {
@@ -1011,6 +1055,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         }
         write_row(r, tot);
     }
+    write_pick();
 }
 
 using Plan = plan::Gemv;
@@ -1103,9 +1148,10 @@ Launch prepare(int type, const MfmaArgs &a, int k, bool swiglu, bool routed) {
     return l;
 }
 
-hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStream_t s) {
+hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStream_t s, int *grid = nullptr) {
     const Launch l = prepare(type, a, k, swiglu, routed);
     if (!l.ok) return hipErrorInvalidValue;  // the *_ok checks reject these shapes first
+    if (grid) *grid = l.p.grid;
     const int units = QLIN_MFMA_INTERLEAVE ? (a.total + 15) / 16 : a.total;  // tiles or rows per workgroup
     a.rows_q = units / l.p.grid;
     a.rows_r = units % l.p.grid;
@@ -1113,6 +1159,31 @@ hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStr
     void *args[] = {&a};
     const hipError_t e = hipLaunchKernel(l.k.fn, dim3(l.p.grid), dim3(l.k.threads), args, l.p.lds, s);
     return e != hipSuccess ? e : hipGetLastError();
+}
+
+// The workgroups' greedy picks (amax_v, amax_i of a launch of n workgroups) reduced by one workgroup
+// with the same rule: the argmax of the launch's whole output.
+constexpr int kPickThreads = 256;
+__global__ __launch_bounds__(kPickThreads) void pick_pairs_kernel(const float *__restrict__ pv,
+                                                                  const int *__restrict__ pi, int n,
+                                                                  int *__restrict__ out_idx) {
+    __shared__ float s_v[kPickThreads / 64];
+    __shared__ int s_i[kPickThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float v = -INFINITY;
+    int idx = 0;
+    for (int j = tid; j < n; j += kPickThreads) pick_better(v, idx, pv[j], pi[j]);
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) pick_better(v, idx, __shfl_xor(v, m, 64), __shfl_xor(idx, m, 64));
+    if (lane == 0) {
+        s_v[wave] = v;
+        s_i[wave] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kPickThreads / 64; ++w) pick_better(v, idx, s_v[w], s_i[w]);
+        *out_idx = idx;
+    }
 }
 
 MfmaArgs base_args(int type, size_t rb, const float *x, int k) {
@@ -1199,6 +1270,34 @@ hipError_t mfma_gemv(int type, const uint8_t *const *w, float *const *y, const i
     a.total = total;
     a.add = add ? 1 : 0;
     return launch(type, a, k, false, false, s);
+}
+
+int mfma_gemv_pairs(int type, const uint8_t *w, size_t rb, const float *x, int n, int k) {
+    MfmaArgs a = base_args(type, rb, x, k);
+    a.w[0] = w;
+    a.row_end[0] = n;
+    a.nmat = 1;
+    a.total = n;
+    const Launch l = prepare(type, a, k, false, false);
+    return l.ok ? l.p.grid : 0;
+}
+
+hipError_t mfma_gemv_argmax(int type, const uint8_t *w, size_t rb, const float *x, float *y, int n, int k,
+                            const RmsNorm *norm, float *pairs_v, int *pairs_i, int *out_idx, hipStream_t s) {
+    MfmaArgs a = base_args(type, rb, x, k);
+    set_norm(a, norm);
+    a.w[0] = w;
+    a.y[0] = y;
+    a.row_end[0] = n;
+    a.nmat = 1;
+    a.total = n;
+    a.amax_v = pairs_v;
+    a.amax_i = pairs_i;
+    int grid = 0;
+    const hipError_t e = launch(type, a, k, false, false, s, &grid);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(pick_pairs_kernel, dim3(1), dim3(kPickThreads), 0, s, pairs_v, pairs_i, grid, out_idx);
+    return hipGetLastError();
 }
 
 hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t rb, const float *x, float *act, int ffn,

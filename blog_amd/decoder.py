@@ -110,6 +110,7 @@ class Qwen2Decoder:
         self.attn = torch.zeros(P, cfg.q_dim, dtype=f32, device=dev)
         self.act = torch.zeros(P, F, dtype=f32, device=dev)
         self.logits = torch.zeros(cfg.vocab, dtype=f32, device=dev)
+        self.pick_scratch = torch.zeros(8192, dtype=torch.uint8, device=dev)  # the head's per-workgroup picks
         self.kc = [torch.zeros(max_seq, cfg.kv_dim, dtype=f32, device=dev) for _ in range(cfg.layers)]
         self.vc = [torch.zeros(max_seq, cfg.kv_dim, dtype=f32, device=dev) for _ in range(cfg.layers)]
         self.prompt_ids = torch.zeros(P, dtype=i32, device=dev)
@@ -175,12 +176,15 @@ class Qwen2Decoder:
         c, L, t = self.cfg, self.L, c_ptr
         hr = t(self.h) + 4 * row * c.hidden
         if self.fuse and hr % 16 == 0:
-            qlin.rms_norm_quant_gemv_multi(c.wtype, [self.w["table"]], self.rb_h, hr, self.w["final_norm"], 0, c.eps, 0,
-                                           [self.logits], [c.vocab], c.hidden)
-        else:
-            self._norm(hr, t(self.xn), self.w["final_norm"], 1)
-            self._ok("lm_head", L.qlin_launch_quant_gemv(c.wtype, t(self.w["table"]), self.rb_h, t(self.xn),
-                                                         t(self.logits), c.vocab, c.hidden, 1))
+            # the norm inside the head GEMV, and each of its workgroups' greedy pick in its epilogue (one
+            # small launch reduces the picks): two launches instead of norm, GEMV and a scan of every logit
+            self._ok("lm_head_argmax", L.qlin_launch_quant_gemv_argmax(
+                c.wtype, t(self.w["table"]), self.rb_h, hr, t(self.w["final_norm"]), 0, c.eps, 0, t(self.logits),
+                c.vocab, c.hidden, t(self.pick_scratch), t(self.token)))
+            return
+        self._norm(hr, t(self.xn), self.w["final_norm"], 1)
+        self._ok("lm_head", L.qlin_launch_quant_gemv(c.wtype, t(self.w["table"]), self.rb_h, t(self.xn),
+                                                     t(self.logits), c.vocab, c.hidden, 1))
         self._ok("argmax", L.qlin_launch_argmax(t(self.logits), c.vocab, t(self.token)))
 
     def prefill(self, prompt) -> None:

@@ -40,6 +40,15 @@
  *                              value are stored in the caches at the row's position as before, but q is
  *                              left as it is (the rotated q lives only in the launch).  Alignment as
  *                              qlin_launch_attend's for q, the caches and attn; k and v 4-byte aligned.
+ *   qlin_launch_quant_gemv_argmax  the output head and the greedy pick: logits = W x, or W rms_norm(x) when
+ *                              norm_weight is non-null, as qlin_launch_quant_gemv / ..._rms_norm_quant_gemv_multi
+ *                              give them, then *out_idx as qlin_launch_argmax gives it for those logits (the
+ *                              largest, the lowest index among equals, NaN never; 0 when nothing beats -inf).
+ *                              Each workgroup of the GEMV reduces its own rows to one (value, index) pair in
+ *                              scratch (QLIN_GEMV_ARGMAX_SCRATCH_BYTES of device memory, 4-byte aligned, used
+ *                              by nothing else while the launches run), and one small launch reduces the pairs:
+ *                              two launches instead of a GEMV and a one-workgroup scan of every logit.  Shapes
+ *                              as the fused RMSNorm launches' (else QLIN_ERR_LIMIT); out_dim >= 1.
  */
 #ifndef QLIN_DECODER_H
 #define QLIN_DECODER_H
@@ -67,6 +76,10 @@ int qlin_launch_rms_norm_quant_gemv_multi(int type, int n_mats, const uint8_t *c
 int qlin_launch_rms_norm_quant_swiglu(int type, const uint8_t *w_gate, const uint8_t *w_up, size_t row_bytes,
                                       const float *x, const uint16_t *norm_weight, int norm_type, float eps,
                                       int one_plus, float *act, int ffn_dim, int in_dim);
+#define QLIN_GEMV_ARGMAX_SCRATCH_BYTES 8192
+int qlin_launch_quant_gemv_argmax(int type, const uint8_t *weights, size_t row_bytes, const float *x,
+                                  const uint16_t *norm_weight, int norm_type, float eps, int one_plus, float *logits,
+                                  int out_dim, int in_dim, void *scratch, int *out_idx);
 
 #ifdef __cplusplus
 }

@@ -273,6 +273,28 @@ def test_fused_decoder_launch_validation():
     assert ra(q=FAKE + 4) == ALIGN
 
 
+def test_gemv_argmax_validation():
+    """The head GEMV with the greedy pick: the GEMV's checks, the scratch and the index required, at least one
+    output, and the matrix-core shapes only (LIMIT otherwise), all before any launch."""
+    # qlin_launch_quant_gemv_argmax(type, w, rb, x, norm_w, norm_type, eps, one_plus, logits, out_dim, in_dim,
+    #                               scratch, out_idx)
+    run = lambda t=8, w=FAKE, rb=102, x=FAKE, nw=FAKE, nt=0, lg=FAKE, n=16, k=96, sc=FAKE, oi=FAKE: qlin.status(
+        "qlin_launch_quant_gemv_argmax", t, w, rb, x, nw, nt, 1e-6, 0, lg, n, k, sc, oi)
+    assert run(t=3) == UNSUP
+    assert run(n=0) == SHAPE
+    assert run(nt=2) == SHAPE
+    assert run(rb=101) == ROWB
+    assert run(x=0) == NULL
+    assert run(lg=0) == NULL
+    assert run(sc=0) == NULL
+    assert run(oi=0) == NULL
+    assert run(sc=FAKE + 2) == ALIGN
+    assert run(oi=FAKE + 1) == ALIGN
+    assert run(nw=FAKE + 1) == ALIGN
+    assert run() == LIMIT              # in_dim 96: not whole 128-weight chunks for the matrix-core kernels
+    assert run(nw=0, nt=7) == LIMIT    # without a norm its type is not read
+
+
 def test_swiglu_and_down_validation():
     assert qlin.status("qlin_launch_quant_swiglu_indexed", 12, FAKE, FAKE, 100, 100, 144, 144, FAKE, FAKE, FAKE,
                        2, 1, 256) == ROWB

@@ -239,6 +239,71 @@ def test_rms_norm_fused_gemv(qtype, hidden, outs, wtype, one_plus):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("qtype,hidden,vocab,norm,case", [
+    (qgen.Q8_0, 896, 151936, True, "random"),   # C3's tied head with the final norm
+    (qgen.Q8_0, 896, 151936, True, "tie"),      # the largest logit twice: the lower row wins
+    (qgen.Q4_K, 1024, 3000, False, "random"),
+    (qgen.Q6_K, 1024, 4100, False, "tie"),
+    (qgen.Q5_0, 1152, 777, True, "random"),
+    (qgen.Q8_0, 896, 5000, False, "nan"),       # every third row's logit NaN (a NaN block scale): never picked
+    (qgen.Q8_0, 896, 300, False, "allnan"),     # every logit NaN: nothing beats -inf, index 0
+])
+def test_gemv_argmax(qtype, hidden, vocab, norm, case):
+    """The head GEMV with the greedy pick in its epilogue: the logits are the plain launches' bit for bit,
+    and the index is qlin_launch_argmax's over them (and numpy's first maximum when nothing is NaN)."""
+    torch = _gpu()
+    from gpu_util import banner, dev, empty_f32, host
+    from blog_amd import qlin
+    rng = np.random.default_rng(vocab + hidden)
+    x = (rng.standard_normal(hidden) * 3).astype(np.float32)
+    bits, _ = _norm_weights(rng, hidden, 0)
+    w, rb, _ = qgen.random_matrix(qtype, vocab, hidden, seed=530 + vocab)
+    if case in ("nan", "allnan"):
+        # Q8_0 block 0 of the chosen rows gets the f16 NaN 0x7e00 as its scale
+        w = w.copy()
+        rows = w.reshape(vocab, rb)
+        chosen = rows if case == "allnan" else rows[1::3]
+        chosen[:, 0:2] = [0x00, 0x7e]
+    if case == "tie":
+        # copy the row of the largest logit into a row below it: two equal logits
+        lg = empty_f32(vocab)
+        if norm:
+            qlin.rms_norm_quant_gemv_multi(qtype, [dev(w)], rb, dev(x), dev(bits), 0, 1e-6, 0, [lg], [vocab], hidden)
+        else:
+            qlin.call("qlin_launch_quant_gemv", qtype, dev(w), rb, dev(x), lg, vocab, hidden, 1)
+        top = int(np.argmax(host(lg)))
+        low = top // 2 if top > 0 else 1
+        w = w.copy()
+        w.reshape(vocab, rb)[min(low, top)] = w.reshape(vocab, rb)[max(low, top)]
+    wd, xd, nd = dev(w), dev(x), dev(bits) if norm else None
+    logits, idx = empty_f32(vocab), torch.full((1,), -5, dtype=torch.int32, device="cuda")
+    scratch = torch.empty(8192, dtype=torch.uint8, device="cuda")
+    banner(f"gemv argmax type={qtype} hidden={hidden} vocab={vocab} norm={norm} case={case}")
+    qlin.call("qlin_launch_quant_gemv_argmax", qtype, wd, rb, xd, nd if norm else 0, 0, 1e-6, 0, logits, vocab, hidden,
+              scratch, idx)
+    ref_lg, ref_idx = empty_f32(vocab), torch.full((1,), -5, dtype=torch.int32, device="cuda")
+    if norm:
+        qlin.rms_norm_quant_gemv_multi(qtype, [wd], rb, xd, nd, 0, 1e-6, 0, [ref_lg], [vocab], hidden)
+    else:
+        qlin.call("qlin_launch_quant_gemv", qtype, wd, rb, xd, ref_lg, vocab, hidden, 1)
+    qlin.call("qlin_launch_argmax", ref_lg, vocab, ref_idx)
+    torch.cuda.synchronize()
+    assert torch.equal(logits.view(torch.int32), ref_lg.view(torch.int32))  # bit for bit, NaNs included
+    got = int(host(idx)[0])
+    assert got == int(host(ref_idx)[0])
+    h = host(logits)
+    if case == "allnan":
+        assert np.isnan(h).all() and got == 0
+    elif case == "nan":
+        assert np.isnan(h[1::3]).all() and not np.isnan(h[0::3]).any()
+        assert got == int(np.nanargmax(h))
+    else:
+        assert got == int(np.argmax(h))
+    if case == "tie":
+        assert (h == h[got]).sum() >= 2 and got == int(np.flatnonzero(h == h.max())[0])
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("qtype,hidden,ffn", [(qgen.Q8_0, 896, 4864), (qgen.Q4_K, 3584, 18944), (qgen.Q4_0, 512, 100)])
 def test_rms_norm_fused_swiglu(qtype, hidden, ffn):
     torch = _gpu()
