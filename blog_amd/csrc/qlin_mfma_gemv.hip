@@ -3,7 +3,9 @@
 // Computes y[o] = sum_k w(o, k) x[k] (reference quant_gemv_kernel / quant_gemv_add_kernel,
 // AI/codes/local-llm/src/backend/cuda/ops/kernel.cu:1192-1244) for up to four matrices sharing x
 // (their rows form one concatenated index space), or the fused SwiGLU act[o] = g/(1+exp(-g))*u of a
-// gate/up pair (quant_swiglu_kernel, kernel.cu:1289-1328).
+// gate/up pair (quant_swiglu_kernel, kernel.cu:1289-1328).  For one matrix it can also leave each
+// workgroup's greedy pick of its outputs (the argmax rule of kernel.cu:3531-3592) for
+// pick_pairs_kernel, which reduces them: an output head and its argmax without a scan of the logits.
 //
 // Why matrix cores for a GEMV.  Without packed FP32 a CU retires about one wave64 VALU instruction
 // per clock, and decoding a Q4_K weight plus an f32 multiply-add costs about three of them per
