@@ -740,8 +740,7 @@ def wl_c5(args, torch, qlin, gen):
     nws = qlin.lib().qlin_moe_ffn_workspace_bytes(tokens, k, E, ffn, hid, sffn)
     ws = torch.empty(nws + 256, dtype=torch.uint8, device="cuda")
     wsp = (ws.data_ptr() + 255) // 256 * 256
-    act = torch.empty(k, ffn, device="cuda")
-    sact = torch.empty(sffn, device="cuda")
+    act = torch.empty(k * ffn + sffn, device="cuda")
     sacts = torch.empty(tokens, sffn, device="cuda")
     gub, db = mats[0][0].numel(), mats[0][2].numel()
     s_rb, sd_rb = qlin.row_bytes(Q4_K, hid), qlin.row_bytes(Q4_K, sffn)
@@ -761,13 +760,12 @@ def wl_c5(args, torch, qlin, gen):
             qlin.call("qlin_launch_quant_matmul_add", Q4_K, sd, sd_rb, sacts, out, hid, sffn, tokens)
 
     def step_per_token():
+        # each token's whole FFN in the per-token call: routing, routed and shared SwiGLU in one launch,
+        # routed down, shared down-add
         for wg, wu, wd, sg, su, sd in mats:
-            qlin.call("qlin_launch_moe_router_topk", logits, ids, rw, tokens, E, k, 1.0)
             for t in range(tokens):
-                qlin.call("qlin_moe_routed_decode_indexed", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid,
-                          x[t], ids[t], rw[t], act, out[t], k)
-                qlin.call("qlin_launch_quant_swiglu", Q4_K, sg, su, s_rb, s_rb, x[t], sact, sffn, hid)
-                qlin.call("qlin_launch_quant_gemv_add", Q4_K, sd, sd_rb, sact, out[t], hid, sffn)
+                qlin.call("qlin_moe_ffn_decode_indexed_logits", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid,
+                          Q4_K, sg, su, s_rb, sd, sd_rb, sffn, x[t], logits[t], 1.0, ids[t], rw[t], act, out[t], k)
 
     reps = max(5, args.steps // 4)
     us, us_three = (v / copies for v in graphs_us_interleaved(torch, qlin, [step_grouped, step_three_calls], reps))
@@ -871,8 +869,29 @@ def wl_moe_token(args, torch, qlin, gen):
             qlin.call("qlin_launch_quant_down_f32_indexed_accum_ordered", Q5_0, wd, db // E, d_rb, act, ids[c], rw[c],
                       out, k, hid, ffn)
 
+    # the whole MoE FFN of a token: the routed experts plus the 2 shared experts (Q4_K gate/up
+    # [2816, 2048], Q4_K down [2048, 2816]), in one call or as the separate calls
+    sffn = 2816
+    shared = [(synth_blocks(torch, Q4_K, sffn, hid, gen), synth_blocks(torch, Q4_K, sffn, hid, gen),
+               synth_blocks(torch, Q4_K, hid, sffn, gen)) for _ in range(copies)]
+    s_rb, sd_rb = qlin.row_bytes(Q4_K, hid), qlin.row_bytes(Q4_K, sffn)
+    act_f = torch.empty(k * ffn + sffn, device="cuda")
+
+    def ffn_call():
+        for c, ((wg, wu, wd), (sg, su, sd)) in enumerate(zip(mats, shared)):
+            qlin.call("qlin_moe_ffn_decode_indexed_logits", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, Q4_K,
+                      sg, su, s_rb, sd, sd_rb, sffn, x, logits[c], 1.0, ids[c], rw[c], act_f, out, k)
+
+    def ffn_separate():
+        for c, ((wg, wu, wd), (sg, su, sd)) in enumerate(zip(mats, shared)):
+            qlin.call("qlin_moe_routed_decode_indexed_logits", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, x,
+                      logits[c], 1.0, ids[c], rw[c], act, out, k)
+            qlin.quant_swiglu(Q4_K, sg, su, s_rb, s_rb, x, act_f[k * ffn:], sffn, hid)
+            qlin.quant_gemv_add(Q4_K, sd, sd_rb, act_f[k * ffn:], out, hid, sffn)
+
     reps = max(1, args.steps // 4)
     us = graph_us(torch, qlin, step, reps) / copies
+    us_ffn, us_ffn3 = (t / copies for t in graphs_us_interleaved(torch, qlin, [ffn_call, ffn_separate], reps))
     route()
     torch.cuda.synchronize()
     us_sw = graph_us(torch, qlin, swiglu_only, reps) / copies
@@ -881,8 +900,11 @@ def wl_moe_token(args, torch, qlin, gen):
     sw_bytes = k * 2 * ffn * g_rb + 4 * hid + 4 * k * ffn
     dn_bytes = k * hid * d_rb + 4 * k * ffn + 8 * hid
     nbytes = sw_bytes + dn_bytes + 4 * E
+    ffn_bytes = nbytes + 2 * sffn * s_rb + hid * sd_rb + 8 * sffn
     log(f"moe token: {us:.2f} us/token (router + routed decode), SwiGLU {us_sw:.2f} us, down {us_dn:.2f} us, "
         f"{distinct} distinct experts per token at least")
+    log(f"moe ffn token (routed + shared): {us_ffn:.2f} us in one call ({ffn_bytes / us_ffn / 1e3:.0f} GB/s), "
+        f"{us_ffn3:.2f} us as the separate calls")
     result = {
         "metric": "per-token routed MoE decode HBM GB/s (DeepSeek-V2-Lite shape, top-6 of 64, 1 token)",
         "value": round(nbytes / us / 1e3, 1), "unit": "GB/s", "pct_of_peak": round(100 * nbytes / us / 1e3 / PEAK_HBM_GBS, 2),
@@ -893,7 +915,11 @@ def wl_moe_token(args, torch, qlin, gen):
                    "gate_up": "Q4_K", "down": "Q5_0", "algorithmic_bytes_per_step": nbytes,
                    "launches_per_step": "moe_routed_decode_indexed_logits (routed SwiGLU with the routing, "
                                         "routed down)",
-                   "swiglu_us": round(us_sw, 3), "down_us": round(us_dn, 3), "execution": "hip graph replay"},
+                   "swiglu_us": round(us_sw, 3), "down_us": round(us_dn, 3), "execution": "hip graph replay",
+                   "ffn_token_us": round(us_ffn, 3), "ffn_token_separate_calls_us": round(us_ffn3, 3),
+                   "ffn_token_bytes": ffn_bytes,
+                   "ffn_token": "qlin_moe_ffn_decode_indexed_logits with the 2 shared experts (Q4_K [2816, 2048] "
+                                "gate/up, [2048, 2816] down): 3 launches; separate calls: 4"},
         "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": "mfma_gemv_kernel<12, true, 1, false, true> (routed gate/up SwiGLU, 6 x 2 x [1408, 2048])",

@@ -524,12 +524,12 @@ int qlin_moe_routed_decode_indexed(int gu_type, const uint8_t *gate, const uint8
                                                             hidden, ffn_dim);
 }
 
-int qlin_moe_routed_decode_indexed_logits(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
-                                          int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
-                                          int ffn_dim, int in_dim, int hidden, const float *x,
-                                          const float *router_logits, float routed_scaling, int *ids, float *rw,
-                                          float *act, float *out, int k) {
-    // qlin_moe_routed_decode_indexed's checks (ids and rw are written here), all before anything runs
+// The per-token call from logits: qlin_moe_routed_decode_indexed's checks (ids and rw are written here),
+// all before anything runs.
+static int indexed_logits_check(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                int down_type, const uint8_t *down, size_t down_bytes, int n_experts, int ffn_dim,
+                                int in_dim, int hidden, const float *x, const float *router_logits, int *ids,
+                                float *rw, float *act, float *out, int k) {
     if (!ids || !rw || !router_logits) return QLIN_ERR_NULL;
     if (down_type != QLIN_TYPE_Q4_K && down_type != QLIN_TYPE_Q6_K && down_type != QLIN_TYPE_Q5_0 &&
         down_type != QLIN_TYPE_Q8_0)
@@ -550,7 +550,21 @@ int qlin_moe_routed_decode_indexed_logits(int gu_type, const uint8_t *gate, cons
         (rc = check_f32(act, true)) || (rc = check_f32(router_logits, true)))
         return rc;
     if (!aligned(ids, 4)) return QLIN_ERR_ALIGN;
-    if (k == 0) return QLIN_OK;
+    return QLIN_OK;
+}
+
+int qlin_moe_routed_decode_indexed_logits(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                          int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
+                                          int ffn_dim, int in_dim, int hidden, const float *x,
+                                          const float *router_logits, float routed_scaling, int *ids, float *rw,
+                                          float *act, float *out, int k) {
+    int rc = indexed_logits_check(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts, ffn_dim,
+                                  in_dim, hidden, x, router_logits, ids, rw, act, out, k);
+    if (rc || k == 0) return rc;
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const size_t d_rb = d_eb / static_cast<size_t>(hidden);
     if (n_experts <= 64 && qlin::mfma_routed_ok(gu_type, true, gate, up, g_eb, g_rb, x, k, ffn_dim, in_dim)) {
         // the routing in the gate/up launch (its workgroup 0 writes ids and rw), then the down launch
         const qlin::MoeRouter router{router_logits, routed_scaling, ids, rw};
@@ -563,6 +577,61 @@ int qlin_moe_routed_decode_indexed_logits(int gu_type, const uint8_t *gate, cons
     if ((rc = qlin_launch_moe_router_topk(router_logits, ids, rw, 1, n_experts, k, routed_scaling))) return rc;
     return qlin_moe_routed_decode_indexed(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts,
                                           ffn_dim, in_dim, hidden, x, ids, rw, act, out, k);
+}
+
+// MoE::forward for one token (MoE.cpp:29-52 after the norm, before the residual add): the routed experts
+// from the logits, then the shared experts.  Where the routed SwiGLU takes the shared gate and up rows as
+// extra routes (same format and row stride, shared_ffn a multiple of ffn_dim, at most 16 routes in all,
+// up to 64 experts) that is 3 launches instead of 4: routing + routed and shared SwiGLU, routed down,
+// shared down-add.  Either way out gets (out + routed) + shared, bit for bit as the separate calls.
+int qlin_moe_ffn_decode_indexed_logits(int gu_type, const uint8_t *gate, const uint8_t *up, size_t gate_up_bytes,
+                                       int down_type, const uint8_t *down, size_t down_bytes, int n_experts,
+                                       int ffn_dim, int in_dim, int hidden, int shared_type, const uint8_t *shared_gate,
+                                       const uint8_t *shared_up, size_t shared_gate_up_rb, const uint8_t *shared_down,
+                                       size_t shared_down_rb, int shared_ffn, const float *x,
+                                       const float *router_logits, float routed_scaling, int *ids, float *rw,
+                                       float *act, float *out, int k) {
+    if (shared_ffn < 0) return QLIN_ERR_SHAPE;
+    int rc = indexed_logits_check(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes, n_experts, ffn_dim,
+                                  in_dim, hidden, x, router_logits, ids, rw, act, out, k);
+    if (rc) return rc;
+    const bool shared = shared_ffn > 0;
+    if (shared) {
+        if ((rc = check_weight(shared_type, shared_gate, shared_gate_up_rb, shared_ffn, in_dim)) ||
+            (rc = check_weight(shared_type, shared_up, shared_gate_up_rb, shared_ffn, in_dim)) ||
+            (rc = check_weight(shared_type, shared_down, shared_down_rb, hidden, shared_ffn)))
+            return rc;
+    }
+    float *sact = act + static_cast<size_t>(k) * ffn_dim;  // the shared activations follow the routes'
+    const size_t g_eb = gate_up_bytes / static_cast<size_t>(n_experts);
+    const size_t g_rb = g_eb / static_cast<size_t>(ffn_dim);
+    const int n_sh = shared && shared_ffn % ffn_dim == 0 ? shared_ffn / ffn_dim : 0;
+    const bool fuse = k > 0 && n_sh > 0 && n_experts <= 64 && shared_type == gu_type && shared_gate_up_rb == g_rb &&
+                      qlin::mfma_routed_ok(gu_type, true, gate, up, g_eb, g_rb, x, k + n_sh, ffn_dim, in_dim) &&
+                      qlin::mfma_routed_ok(gu_type, true, shared_gate, shared_up, g_eb, g_rb, x, k + n_sh, ffn_dim,
+                                           in_dim);
+    if (fuse) {
+        const size_t d_eb = down_bytes / static_cast<size_t>(n_experts);
+        const size_t d_rb = d_eb / static_cast<size_t>(hidden);
+        const qlin::MoeRouter router{router_logits, routed_scaling, ids, rw};
+        const hipError_t e = qlin::mfma_swiglu_routed(gu_type, gate, up, g_eb, g_rb, x, nullptr, act, k, ffn_dim,
+                                                      in_dim, stream(), &router, n_experts, shared_gate, shared_up,
+                                                      n_sh);
+        if (e != hipSuccess) return QLIN_ERR_LAUNCH;
+        if ((rc = qlin_launch_quant_down_f32_indexed_accum_ordered(down_type, down, d_eb, d_rb, act, ids, rw, out, k,
+                                                                    hidden, ffn_dim)))
+            return rc;
+        return qlin_launch_quant_gemv_add(shared_type, shared_down, shared_down_rb, sact, out, hidden, shared_ffn);
+    }
+    if ((rc = qlin_moe_routed_decode_indexed_logits(gu_type, gate, up, gate_up_bytes, down_type, down, down_bytes,
+                                                    n_experts, ffn_dim, in_dim, hidden, x, router_logits,
+                                                    routed_scaling, ids, rw, act, out, k)))
+        return rc;
+    if (!shared) return QLIN_OK;
+    if ((rc = qlin_launch_quant_swiglu(shared_type, shared_gate, shared_up, shared_gate_up_rb, shared_gate_up_rb, x,
+                                       sact, shared_ffn, in_dim)))
+        return rc;
+    return qlin_launch_quant_gemv_add(shared_type, shared_down, shared_down_rb, sact, out, hidden, shared_ffn);
 }
 
 static bool embed_mla_type(int t) {

@@ -81,10 +81,13 @@ hipError_t mfma_swiglu(int type, const uint8_t *wg, const uint8_t *wu, size_t ro
 bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1, size_t expert_bytes,
                     size_t row_bytes, const float *x, int routes, int rows, int k);
 // router: the routes are router_topk's picks of the token's logits (n_experts <= 64), made in the
-// launch and written to router->ids / router->w; ids is then not read.
+// launch and written to router->ids / router->w; ids is then not read.  sh_routes > 0: sh_routes more
+// routes after them, the consecutive ffn_dim-row blocks of the shared gate and up matrices sh_wg / sh_wu
+// (same format and row stride), written after the routes' rows in act.
 hipError_t mfma_swiglu_routed(int type, const uint8_t *wg, const uint8_t *wu, size_t expert_bytes, size_t row_bytes,
                               const float *x, const int *ids, float *act, int routes, int ffn_dim, int in_dim,
-                              hipStream_t s, const MoeRouter *router = nullptr, int n_experts = 0);
+                              hipStream_t s, const MoeRouter *router = nullptr, int n_experts = 0,
+                              const uint8_t *sh_wg = nullptr, const uint8_t *sh_wu = nullptr, int sh_routes = 0);
 hipError_t mfma_down_routed(int type, const uint8_t *wd, size_t expert_bytes, size_t row_bytes, const float *act,
                             const int *ids, const float *rw, float *out, int routes, int hidden, int ffn_dim,
                             hipStream_t s);

@@ -186,6 +186,11 @@ struct MfmaArgs {
     // same rule, which gives the argmax of the whole output whatever the order.
     float *amax_v;
     int *amax_i;
+    // Routed SwiGLU: the last sh_routes routes are not experts but consecutive route_rows-row blocks of
+    // the shared gate and up matrices sh_w0 and sh_w1 (same format and row stride): the shared experts
+    // in the same launch.  They are not routed and never empty.
+    const uint8_t *sh_w0, *sh_w1;
+    int sh_routes;
 };
 
 // (v, i) becomes (v2, i2) when that is larger, or equal at a lower index: the argmax's rule
@@ -368,8 +373,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             // route of this lane's concatenated row (the 16 rows of a tile may span two routes)
             const int r = route_of(gr, a.route_rows, a.route_magic);
             const int row = gr - r * a.route_rows;
-            p.rp = expert(which ? mats.w[1] : mats.w[0], r) + static_cast<size_t>(row) * a.row_bytes +
-                   static_cast<size_t>(p.sb) * CB;
+            const int rs = r - (a.routes - a.sh_routes);  // >= 0: a block of the shared matrices
+            const uint8_t *base =
+                rs >= 0 ? (which ? a.sh_w1 : a.sh_w0) + static_cast<size_t>(rs) * a.route_rows * a.row_bytes
+                        : expert(which ? mats.w[1] : mats.w[0], r);
+            p.rp = base + static_cast<size_t>(row) * a.row_bytes + static_cast<size_t>(p.sb) * CB;
         } else if constexpr (ROUTED) {
             // chunk sb of the concatenated activations is chunk cl of route r (wave-uniform)
             const int r = route_of(p.sb, a.cpr, a.cpr_magic);
@@ -500,7 +508,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             if (a.logits) {  // uniform: wave 0 routes the token (the only live wave: its LDS alone)
                 __shared__ __attribute__((aligned(16))) float s_rv[64], s_rex[64];
                 __shared__ float s_rdn;
-                route_token_rank(wave == 0, a.logits, a.ne, a.routes, a.scaling, s_rv, s_rex, &s_rdn,
+                route_token_rank(wave == 0, a.logits, a.ne, a.routes - a.sh_routes, a.scaling, s_rv, s_rex, &s_rdn,
                                  [&](int r, int e, float w) {
                                      s_ids[r] = e;
                                      if (blockIdx.x == 0) {
@@ -511,10 +519,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
                 routed_here = true;
             }
         }
-        if (!routed_here && tid < a.routes) {
+        if (!routed_here && tid < a.routes - a.sh_routes) {
             s_ids[tid] = a.ids[tid];
             if constexpr (!SWIGLU) s_rw[tid] = a.rw[tid];
         }
+        if (tid >= a.routes - a.sh_routes && tid < a.routes) s_ids[tid] = 0;  // the shared blocks
         __syncthreads();
     }
 
@@ -1339,8 +1348,12 @@ bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1,
 
 hipError_t mfma_swiglu_routed(int type, const uint8_t *wg, const uint8_t *wu, size_t eb, size_t rb, const float *x,
                               const int *ids, float *act, int routes, int ffn, int k, hipStream_t s,
-                              const MoeRouter *router, int n_experts) {
-    MfmaArgs a = swiglu_routed_args(type, wg, wu, eb, rb, x, ids, act, routes, ffn, k);
+                              const MoeRouter *router, int n_experts, const uint8_t *sh_wg, const uint8_t *sh_wu,
+                              int sh_routes) {
+    MfmaArgs a = swiglu_routed_args(type, wg, wu, eb, rb, x, ids, act, routes + sh_routes, ffn, k);
+    a.sh_w0 = sh_wg;
+    a.sh_w1 = sh_wu;
+    a.sh_routes = sh_routes;
     if (router) {
         a.logits = router->logits;
         a.ne = n_experts;

@@ -70,6 +70,8 @@ SIGNATURES = {
     "qlin_gemm": (I, [I, P, SZ, P, P, I, I, I]),
     "qlin_moe_routed_decode_indexed": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, P, I]),
     "qlin_moe_routed_decode_indexed_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, F, P, P, P, P, I]),
+    "qlin_moe_ffn_decode_indexed_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, I, P, P, SZ, P, SZ, I, P, P, F, P, P,
+                                               P, P, I]),
     "qlin_moe_grouped_workspace_bytes": (SZ, [I, I, I, I, I]),
     "qlin_moe_routed_decode_grouped": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, P, P, SZ, P, I, I]),
     "qlin_moe_routed_decode_grouped_logits": (I, [I, P, P, SZ, I, P, SZ, I, I, I, I, P, P, F, P, P, P, SZ, P, I, I]),

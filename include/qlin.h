@@ -255,6 +255,25 @@ int qlin_moe_routed_decode_indexed_logits(int gate_up_type, const uint8_t *gate_
                                           int *expert_ids, float *route_weights, float *act_scratch, float *out,
                                           int k);
 
+/* MoE::forward for one decode token after its norm and before its residual add (MoE.cpp:29-52 with
+ * SharedExperts.cpp:25-55), from the router logits: out [hidden_size] gets (out + the routed sum) + the
+ * shared experts' down projection of SiLU(shared gate x) * (shared up x), exactly the result of
+ * qlin_moe_routed_decode_indexed_logits followed by qlin_launch_quant_swiglu and
+ * qlin_launch_quant_gemv_add on the shared weights.  When the shared gate and up have gate_up_type and
+ * the routed row stride, shared_ffn is a multiple of ffn_dim with k + shared_ffn / ffn_dim <= 16, and
+ * n_experts <= 64, the routed SwiGLU launch also computes the shared SwiGLU (3 launches instead of 4).
+ * Shared weights as qlin_moe_ffn_decode_grouped_logits's; shared_ffn = 0 runs the routed part alone.
+ * act_scratch: at least k * ffn_dim + shared_ffn floats (the routes' activations, then the shared
+ * ones).  Other arguments and checks as qlin_moe_routed_decode_indexed_logits's. */
+int qlin_moe_ffn_decode_indexed_logits(int gate_up_type, const uint8_t *gate_exps, const uint8_t *up_exps,
+                                       size_t gate_up_bytes, int down_type, const uint8_t *down_exps,
+                                       size_t down_bytes, int n_experts, int ffn_dim, int in_dim, int hidden_size,
+                                       int shared_type, const uint8_t *shared_gate, const uint8_t *shared_up,
+                                       size_t shared_gate_up_row_bytes, const uint8_t *shared_down,
+                                       size_t shared_down_row_bytes, int shared_ffn, const float *x,
+                                       const float *router_logits, float routed_scaling, int *expert_ids,
+                                       float *route_weights, float *act_scratch, float *out, int k);
+
 /* No reference counterpart (the reference decodes one token at a time): moe_routed_decode_indexed
  * for a batch of tokens, each selected expert's weights read once for all the routes that chose it.
  * x [tokens, in_dim], expert_ids / route_weights [tokens, k], out [tokens, hidden_size] (+=); per

@@ -242,6 +242,26 @@ def test_moe_ffn_validation():
     assert ffn(ws=FAKE + 16) == ALIGN
     assert ffn(tokens=0, wsb=0) == OK
 
+    def token(gu=12, dt=6, **kw):
+        v = {**g, "act": FAKE, **kw}
+        return qlin.status("qlin_moe_ffn_decode_indexed_logits", gu, v["gate"], v["up"], v["gub"], dt, v["down"],
+                           v["db"], v["ne"], v["ffn"], v["ind"], v["hid"], v["st"], v["sg"], v["su"], v["srb"],
+                           v["sd"], v["sdrb"], v["sffn"], v["x"], v["lg"], 1.0, v["ids"], v["rw"], v["act"],
+                           v["out"], v["k"])
+    assert token(dt=2) == UNSUP
+    assert token(gu=8) == UNSUP
+    assert token(st=99) == UNSUP
+    assert token(sffn=-1) == SHAPE
+    assert token(sffn=2800) == SHAPE
+    assert token(lg=0) == NULL
+    assert token(act=0) == NULL
+    assert token(su=0) == NULL
+    assert token(srb=1151) == ROWB
+    assert token(sd=FAKE + 1) == ALIGN
+    assert token(ids=FAKE + 2) == ALIGN
+    assert token(ne=257, gub=257 * 1408 * 1152, db=257 * 2048 * 968) == LIMIT
+    assert token(k=0, sffn=0) == OK
+
 
 def test_fused_decoder_launch_validation():
     """The norm fused into the decode GEMV and SwiGLU, and the rotary embedding fused into attention."""

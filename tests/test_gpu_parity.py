@@ -824,6 +824,69 @@ def test_moe_ffn_matches_three_calls(gu, E, tokens, k, ffn, hid, sffn, stype):
     assert normwise_rel_err(host(out_f) - out0, ref - out0) <= 1e-4
 
 
+@pytest.mark.parametrize("gu,E,k,ffn,hid,sffn,stype", [
+    (Q4_K, 64, 6, 1408, 2048, 2816, Q4_K),  # DeepSeek-V2-Lite: the shared experts ride in the routed SwiGLU
+    (Q4_K, 8, 2, 256, 512, 512, Q4_K),      # same form, two shared blocks
+    (Q6_K, 8, 2, 256, 512, 256, Q6_K),      # Q6_K gate/up, one shared block
+    (Q4_K, 8, 2, 256, 512, 160, Q8_0),      # shared type differs: the separate calls
+    (Q4_K, 8, 2, 512, 512, 768, Q4_K),      # shared_ffn not a multiple of ffn_dim: the separate calls
+    (Q4_K, 32, 15, 256, 512, 512, Q4_K),    # 17 routes in all: the separate calls
+    (Q4_K, 100, 6, 256, 512, 512, Q4_K),    # over 64 experts: the router launch, then the separate calls
+    (Q4_K, 8, 0, 256, 512, 512, Q4_K),      # no routes: the shared experts alone
+    (Q4_K, 16, 3, 256, 512, 0, Q4_K),       # no shared experts: the routed call alone
+])
+def test_moe_ffn_token_matches_separate_calls(gu, E, k, ffn, hid, sffn, stype):
+    """The per-token MoE FFN call gives, bit for bit, what the routed call from logits followed by
+    qlin_launch_quant_swiglu and qlin_launch_quant_gemv_add on the shared weights give, and the
+    oracle's routed sum plus shared experts to 1e-4."""
+    wg, grb, geb = _experts(gu, E, ffn, hid, 501 + E)
+    wu, _, _ = _experts(gu, E, ffn, hid, 502 + E)
+    wdn, drb, deb = _experts(Q5_0, E, hid, ffn, 503 + E)
+    rng = np.random.default_rng(504 + k)
+    x = rng.standard_normal(hid).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    if sffn:
+        sg, srb, _ = qgen.random_matrix(stype, sffn, hid, seed=511 + sffn)
+        su, _, _ = qgen.random_matrix(stype, sffn, hid, seed=512 + sffn)
+        sd, sdrb, _ = qgen.random_matrix(stype, hid, sffn, seed=513 + sffn)
+    else:
+        sg = su = sd = np.zeros(16, np.uint8)
+        srb, sdrb = qlin.row_bytes(stype, hid), 0
+    out0 = rng.standard_normal(hid).astype(np.float32)
+    d = {n: dev(v) for n, v in dict(wg=wg, wu=wu, wdn=wdn, x=x, lg=logits, sg=sg, su=su, sd=sd).items()}
+    kk = max(k, 1)
+    out_f, ids_f, rw_f = dev(out0), torch.full((kk,), -7, dtype=torch.int32, device="cuda"), empty_f32(kk)
+    act_f = empty_f32(k * ffn + sffn + 1)
+    banner(f"moe ffn token gu={gu} E={E} k={k} shared={sffn} type {stype}")
+    qlin.call("qlin_moe_ffn_decode_indexed_logits", gu, d["wg"], d["wu"], wg.size, Q5_0, d["wdn"], wdn.size, E, ffn,
+              hid, hid, stype, d["sg"], d["su"], srb, d["sd"], sdrb, sffn, d["x"], d["lg"], 0.75, ids_f, rw_f, act_f,
+              out_f, k)
+    out_s, ids_s, rw_s = dev(out0), torch.full((kk,), -7, dtype=torch.int32, device="cuda"), empty_f32(kk)
+    act_s, sact = empty_f32(kk * ffn), empty_f32(max(sffn, 1))
+    qlin.call("qlin_moe_routed_decode_indexed_logits", gu, d["wg"], d["wu"], wg.size, Q5_0, d["wdn"], wdn.size, E,
+              ffn, hid, hid, d["x"], d["lg"], 0.75, ids_s, rw_s, act_s, out_s, k)
+    if sffn:
+        qlin.quant_swiglu(stype, d["sg"], d["su"], srb, srb, d["x"], sact, sffn, hid)
+        qlin.quant_gemv_add(stype, d["sd"], sdrb, sact, out_s, hid, sffn)
+    torch.cuda.synchronize()
+    assert torch.equal(out_f, out_s)
+    if sffn:
+        assert torch.equal(act_f[k * ffn:k * ffn + sffn], sact)
+    if k:
+        assert torch.equal(ids_f, ids_s) and torch.equal(rw_f, rw_s)
+        assert torch.equal(act_f[:k * ffn], act_s[:k * ffn])
+    ref = out0.copy()
+    if k:
+        ids_r, _ = orc.router_topk(logits, k, 0.75)
+        assert np.array_equal(host(ids_f), ids_r[0])
+        act = orc.swiglu_indexed(gu, wg, wu, geb, geb, grb, grb, x, ids_r[0], ffn, hid)
+        ref = orc.down_indexed_ordered(Q5_0, wdn, deb, drb, act, ids_r[0], host(rw_f), out0, hid, ffn)
+    if sffn:
+        act = orc.swiglu(stype, sg, su, srb, srb, x, sffn, hid).astype(np.float32)
+        ref = orc.gemv_add(stype, sd, sdrb, act, ref, hid, sffn)
+    assert normwise_rel_err(host(out_f) - out0, ref - out0) <= 1e-4
+
+
 def test_moe_grouped_wide_input_two_routes_per_pass():
     """in_dim 10240: four routes' staged activations would not fit in LDS, so gate/up runs two routes
     per pass; every expert has more than two routes (4 experts, 8 tokens x 2 routes)."""

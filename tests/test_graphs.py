@@ -207,6 +207,36 @@ def test_graph_moe_token_from_logits():
     _replays_match(torch, qlin, run, lambda: [out, ids, rw, act], reset)
 
 
+def test_graph_moe_ffn_token():
+    """The per-token MoE FFN call with the shared experts in the routed SwiGLU launch."""
+    torch, qlin = _env()
+    from gpu_util import dev, empty_f32
+    E, ffn, hid, k, sffn = 32, 256, 512, 6, 512
+    wg, wu, wd = _moe_mats(E, ffn, hid, 660)
+    sg, srb, _ = qgen.random_matrix(Q4_K, sffn, hid, seed=664)
+    su, _, _ = qgen.random_matrix(Q4_K, sffn, hid, seed=665)
+    sd, sdrb, _ = qgen.random_matrix(Q4_K, hid, sffn, seed=666)
+    wgd, wud, wdd, sgd, sud, sdd = (dev(a) for a in (wg, wu, wd, sg, su, sd))
+    rng = np.random.default_rng(667)
+    x = dev(rng.standard_normal(hid).astype(np.float32))
+    logits = dev(rng.standard_normal(E).astype(np.float32))
+    out0 = dev(rng.standard_normal(hid).astype(np.float32))
+    out, act, rw = empty_f32(hid), empty_f32(k * ffn + sffn), empty_f32(k)
+    ids = torch.zeros(k, dtype=torch.int32, device="cuda")
+
+    def run():
+        qlin.call("qlin_moe_ffn_decode_indexed_logits", Q4_K, wgd, wud, wg.size, Q5_0, wdd, wd.size, E, ffn, hid, hid,
+                  Q4_K, sgd, sud, srb, sdd, sdrb, sffn, x, logits, 1.0, ids, rw, act, out, k)
+
+    def reset():
+        out.copy_(out0)
+        ids.fill_(-3)
+        rw.zero_()
+        act.zero_()
+
+    _replays_match(torch, qlin, run, lambda: [out, ids, rw, act], reset)
+
+
 def test_graph_decoder_steps_match_eager():
     """A small Qwen2-architecture decoder (fused norms and rotary): the step captured once and replayed
     gives, step after step, the eager decoder's logits and tokens (the step reads its token and position
