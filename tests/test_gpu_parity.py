@@ -824,7 +824,7 @@ def test_moe_ffn_matches_three_calls(gu, E, tokens, k, ffn, hid, sffn, stype):
     assert normwise_rel_err(host(out_f) - out0, ref - out0) <= 1e-4
 
 
-@pytest.mark.parametrize("gu,E,k,ffn,hid,sffn,stype", [
+@pytest.mark.parametrize("gu,E,k,ffn,hid,sffn,stype,special", [(*c, None)[:8] for c in [
     (Q4_K, 64, 6, 1408, 2048, 2816, Q4_K),  # DeepSeek-V2-Lite: the shared experts ride in the routed SwiGLU
     (Q4_K, 8, 2, 256, 512, 512, Q4_K),      # same form, two shared blocks
     (Q6_K, 8, 2, 256, 512, 256, Q6_K),      # Q6_K gate/up, one shared block
@@ -834,8 +834,9 @@ def test_moe_ffn_matches_three_calls(gu, E, tokens, k, ffn, hid, sffn, stype):
     (Q4_K, 100, 6, 256, 512, 512, Q4_K),    # over 64 experts: the router launch, then the separate calls
     (Q4_K, 8, 0, 256, 512, 512, Q4_K),      # no routes: the shared experts alone
     (Q4_K, 16, 3, 256, 512, 0, Q4_K),       # no shared experts: the routed call alone
-])
-def test_moe_ffn_token_matches_separate_calls(gu, E, k, ffn, hid, sffn, stype):
+    (Q4_K, 8, 6, 256, 512, 512, Q4_K, "two_finite"),  # 4 empty routes next to the shared blocks
+]])
+def test_moe_ffn_token_matches_separate_calls(gu, E, k, ffn, hid, sffn, stype, special):
     """The per-token MoE FFN call gives, bit for bit, what the routed call from logits followed by
     qlin_launch_quant_swiglu and qlin_launch_quant_gemv_add on the shared weights give, and the
     oracle's routed sum plus shared experts to 1e-4."""
@@ -845,6 +846,9 @@ def test_moe_ffn_token_matches_separate_calls(gu, E, k, ffn, hid, sffn, stype):
     rng = np.random.default_rng(504 + k)
     x = rng.standard_normal(hid).astype(np.float32)
     logits = rng.standard_normal((1, E)).astype(np.float32)
+    if special == "two_finite":
+        logits[0, :] = -np.inf
+        logits[0, [E - 1, 2]] = [0.5, 0.25]
     if sffn:
         sg, srb, _ = qgen.random_matrix(stype, sffn, hid, seed=511 + sffn)
         su, _, _ = qgen.random_matrix(stype, sffn, hid, seed=512 + sffn)
