@@ -71,6 +71,8 @@
 // A wave loads the step it will compute next while it computes the current one, and parks each
 // step's 16 row sums in LDS; they are added in super-block order at the end (deterministic) and
 // only then is y written.
+#include <cstddef>
+
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
@@ -141,6 +143,16 @@ template <> struct Chunk<T_Q6_K> { static constexpr int elems = 256, bytes = 210
 template <int FMT> constexpr int kSumElems = FMT == T_Q6_K ? 16 : 32;
 
 
+// The kernel argument block.  Each 64-byte line of it that a launch reads is a scalar-cache miss at the
+// start of every wave: the fields every launch reads come first, then one union of the fields only the
+// plain launches read and those only the routed launches read, so a plain launch reads 3 lines and a
+// routed one 4 (the workgroup count is passed here rather than read from the implicit arguments that
+// follow the block).  Adding 24 bytes to the earlier, flat block moved the implicit arguments into a
+// fifth line and cost the plain launches 0.2-0.3 us each; this layout took the decode step from
+// 1.1008 ms (the flat block before those bytes) to 1.0974 ms: q/k/v and o gained 0.25 and 0.08 us, while
+// the down projection, whose instructions are the same but for the argument offsets, lost 0.2 us for a
+// reason not found (the common fields keep their earlier order; padding the block back to its earlier
+// size did not change it).
 struct MfmaArgs {
     const uint8_t *w[kMaxStreamMats];
     float *y[kMaxStreamMats];
@@ -158,40 +170,52 @@ struct MfmaArgs {
     // wave, and the 16 waves of a CU share that unit).
     int rows_q, rows_r;
     uint32_t nsb_magic;
-    // Routed launches: route r's weights start at w[.] + ids[r] * eb (a negative id: no expert, its
-    // loads read expert 0 and its results are dropped).  SwiGLU: route r owns concatenated rows
-    // [r * route_rows, (r + 1) * route_rows); otherwise chunks [r * cpr, (r + 1) * cpr) of every row,
-    // weighted by rw[r].  The magics are ceil(2^32 / divisor), exact as nsb_magic (0: divisor 1).
-    const int *ids;
-    const float *rw;
-    size_t eb;
-    int routes, route_rows, cpr;
-    uint32_t route_magic, cpr_magic;
-    // RMSNorm of x fused into the staging (norm_w non-null; the plain launches only): x is used as
-    // x[j] * rsqrt(mean x^2 + eps) * w[j], w bf16 (norm_type 0) or f16 (1), plus one if one_plus
-    const uint16_t *norm_w;
-    int norm_type, norm_one_plus;
-    float norm_eps;
-    // Routed SwiGLU from router logits (logits non-null, ne <= 64): wave 0 picks the token's routes
-    // (route_token_rank) instead of reading ids, and workgroup 0 writes the picks and their weights
-    // (times scaling) to ids_out and rw_out for the down launch.
-    const float *logits;
-    int ne;
-    float scaling;
-    int *ids_out;
-    float *rw_out;
-    // The greedy pick of the outputs (plain launches of one matrix, no add): workgroup b writes the
-    // largest of its rows' outputs and its row, the lowest row among equals (NaN never wins, (-inf, 0)
-    // when nothing beats -inf), to amax_v[b] and amax_i[b]; a later launch reduces the pairs by the
-    // same rule, which gives the argmax of the whole output whatever the order.
-    float *amax_v;
-    int *amax_i;
-    // Routed SwiGLU: the last sh_routes routes are not experts but consecutive route_rows-row blocks of
-    // the shared gate and up matrices sh_w0 and sh_w1 (same format and row stride): the shared experts
-    // in the same launch.  They are not routed and never empty.
-    const uint8_t *sh_w0, *sh_w1;
-    int sh_routes;
+    int grid;  // workgroups in the launch
+    union {
+        // routed launches (first: value-initialisation zeroes the whole union)
+        struct {
+            // Route r's weights start at w[.] + ids[r] * eb (a negative id: no expert, its loads read
+            // expert 0 and its results are dropped).  SwiGLU: route r owns concatenated rows
+            // [r * route_rows, (r + 1) * route_rows); otherwise chunks [r * cpr, (r + 1) * cpr) of every
+            // row, weighted by rw[r].  The magics are ceil(2^32 / divisor), exact as nsb_magic (0:
+            // divisor 1).
+            const int *ids;
+            const float *rw;
+            size_t eb;
+            int routes, route_rows, cpr;
+            uint32_t route_magic, cpr_magic;
+            // SwiGLU from router logits (logits non-null, ne <= 64): wave 0 picks the token's routes
+            // (route_token_rank) instead of reading ids, and workgroup 0 writes the picks and their
+            // weights (times scaling) to ids_out and rw_out for the down launch.
+            int ne;
+            const float *logits;
+            float scaling;
+            int *ids_out;
+            float *rw_out;
+            // SwiGLU: the last sh_routes routes are not experts but consecutive route_rows-row blocks
+            // of the shared gate and up matrices sh_w0 and sh_w1 (same format and row stride): the
+            // shared experts in the same launch.  They are not routed and never empty.
+            const uint8_t *sh_w0, *sh_w1;
+            int sh_routes;
+        };
+        // plain launches
+        struct {
+            // RMSNorm of x fused into the staging (norm_w non-null): x is used as
+            // x[j] * rsqrt(mean x^2 + eps) * w[j], w bf16 (norm_type 0) or f16 (1), plus one if one_plus
+            const uint16_t *norm_w;
+            int norm_type, norm_one_plus;
+            float norm_eps;
+            // The greedy pick of the outputs (one matrix, no add): workgroup b writes the largest of its
+            // rows' outputs and its row, the lowest row among equals (NaN never wins, (-inf, 0) when
+            // nothing beats -inf), to amax_v[b] and amax_i[b]; a later launch reduces the pairs by the
+            // same rule, which gives the argmax of the whole output whatever the order.
+            float *amax_v;
+            int *amax_i;
+        };
+    };
 };
+static_assert(offsetof(MfmaArgs, amax_i) + sizeof(int *) <= 192, "the plain launches' fields fill 3 lines");
+static_assert(sizeof(MfmaArgs) <= 256, "the routed launches' fields fill 4 lines");
 
 // (v, i) becomes (v2, i2) when that is larger, or equal at a lower index: the argmax's rule
 __device__ __forceinline__ void pick_better(float &v, int &i, float v2, int i2) {
@@ -276,7 +300,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 #if QLIN_MFMA_INTERLEAVE
     // 16-row tiles bid, bid + G, bid + 2G, ... (G workgroups): all workgroups sweep one region
     // (rows_q, rows_r here count tiles: tiles / G and tiles % G, from the host)
-    const int G = gridDim.x;
+    const int G = a.grid;
     const int ntl = a.rows_q + (bid < a.rows_r ? 1 : 0);
     const int nrows = ntl ? (ntl - 1) * 16 + min(16, a.total - 16 * (bid + (ntl - 1) * G)) : 0;
     auto grow = [&](int lr) { return 16 * (bid + (lr >> 4) * G) + (lr & 15); };  // global row of local row lr
@@ -1167,6 +1191,7 @@ hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStr
     a.rows_q = units / l.p.grid;
     a.rows_r = units % l.p.grid;
     a.nsb_magic = magic_of(a.nsb);
+    a.grid = l.p.grid;
     void *args[] = {&a};
     const hipError_t e = hipLaunchKernel(l.k.fn, dim3(l.p.grid), dim3(l.k.threads), args, l.p.lds, s);
     return e != hipSuccess ? e : hipGetLastError();
