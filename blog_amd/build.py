@@ -16,7 +16,7 @@ OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libqlin.so")
 ARCH = os.environ.get("QLIN_ARCH", "gfx950")
 
-SOURCES = ["qlin_gemv.hip", "qlin_q4k_stream.hip", "qlin_mfma_gemv.hip", "qlin_q4k_gemm.hip", "qlin_qblk_gemm.hip", "qlin_dequant.hip", "qlin_q8_1.hip", "qlin_moe.hip", "qlin_moe_grouped.hip", "qlin_embed_mla.hip", "qlin_dense.hip", "qlin_mla_latent.hip", "qlin_q8_1_moe.hip", "qlin_decoder.hip", "qlin_probe.hip", "qlin_api.cpp", "qlin_gguf.cpp"]
+SOURCES = ["qlin_gemv.hip", "qlin_q4k_stream.hip", "qlin_mfma_gemv.hip", "qlin_q4k_gemm.hip", "qlin_f32_gemm.hip", "qlin_qblk_gemm.hip", "qlin_dequant.hip", "qlin_q8_1.hip", "qlin_moe.hip", "qlin_moe_grouped.hip", "qlin_embed_mla.hip", "qlin_dense.hip", "qlin_mla_latent.hip", "qlin_q8_1_moe.hip", "qlin_decoder.hip", "qlin_api.cpp", "qlin_gguf.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

@@ -87,7 +87,6 @@ SIGNATURES = {
     "qlin_launch_rms_norm_quant_gemv_multi": (I, [I, I, P, SZ, P, P, I, F, I, P, P, I]),
     "qlin_launch_rms_norm_quant_swiglu": (I, [I, P, P, SZ, P, P, I, F, I, P, I, I]),
     "qlin_launch_quant_gemv_argmax": (I, [I, P, SZ, P, P, I, F, I, P, I, I, P, P]),
-    "qlin_probe_stream_read": (I, [P, SZ, I, P]),
     "qlin_launch_quant_embedding": (I, [I, P, P, P, SZ, I, I]),
     "qlin_launch_mla_absorb_q_nope": (I, [I, P, P, SZ, P, I, I, I, I, I]),
     "qlin_launch_mla_absorb_q4_xsum_delta": (I, [P, P, SZ, P, I, I, I, I, I]),

@@ -11,7 +11,7 @@ import pytest
 from blog_amd import qlin
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("qlin.h", "qlin_gguf.h", "qlin_decoder.h", "qlin_probe.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("qlin.h", "qlin_gguf.h", "qlin_decoder.h")]
 
 OK, UNSUP, SHAPE, NULL, ROWB, LIMIT, LAUNCH, ALIGN = range(8)
 
