@@ -1,5 +1,5 @@
-// qlin_f32_gemm.hip -- Q4_K weights x f32 activations, the prefill GEMM behind quant_matmul (m > 1), on
-// the fp16 matrix cores of gfx950.
+// qlin_f32_gemm.hip -- Q4_K and Q6_K weights x f32 activations, the prefill GEMM behind quant_matmul
+// (m > 1), on the fp16 matrix cores of gfx950 (Q6_K: see compute_q6 below).
 //
 // Computes y[r, o] (=|+=) sum_k w(o, k) x[r, k] with w(o, k) = d*sc_j*q - dmin*m_j (kernel.cu:913-930)
 // and f32 activations x, the reference's quant_matmul_kernel (AI/codes/local-llm/src/backend/cuda/
@@ -27,6 +27,8 @@
 // register set reloaded part by part with the next super-block as in the Q8_1 GEMM.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
+
+#include <type_traits>
 
 namespace qlin {
 namespace {
@@ -96,7 +98,31 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
 
 template <int V> using ic = std::integral_constant<int, V>;
 
-__global__ __launch_bounds__(kThreads) void q4k_f32_gemm_kernel(const F32GemmArgs a) {
+// Q6_K (210-byte super-blocks: ql[128], qh[64], int8 scales[16], d f16; kernel.cu:1122-1156): element l
+// of 32-block j = 4 h + g6 is q = (nibble g6 / 2 of ql[64 h + 32 (g6 % 2) + l]) | (bits 2 g6 .. 2 g6 + 1
+// of qh[32 h + l]) << 4, value d * sc[8 h + 2 g6 + l / 16] * (q - 32).  Lane group g holds elements
+// 8g .. 8g+7 of a block, all under scale 2 g6 + g / 2, so B = sc (q - 32) carries the block's two
+// scales; |sc (q - 32)| <= 4096 is not exact in fp16, so it is split as B1 = fp16(sc (q - 32)) and
+// B2 = fma(q - 32, sc, -B1), both exact integers (|B2| <= 1).  A block takes hi B1, hi B2 and lo B1
+// into the accumulator; lo B2 is at most 2^-22 of hi B1 and is left out.  d applies per super-block.
+// Rows: 4-byte aligned with an even number of super-blocks (super-block s starts 2 past a multiple of
+// 4 when s is odd); each 8-byte piece a lane needs is read as 3 aligned dwords and realigned.
+struct K6Raw {
+    uint32_t ql[4][3], qh[2][3], sd[5];
+};
+__device__ __forceinline__ void load3(uint32_t (&w)[3], const uint8_t *p) {
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+    w[0] = q[0];
+    w[1] = q[1];
+    w[2] = q[2];
+}
+__device__ __forceinline__ uint2 piece(const uint32_t (&w)[3], int off) {
+    return make_uint2(__builtin_amdgcn_alignbyte(w[1], w[0], off), __builtin_amdgcn_alignbyte(w[2], w[1], off));
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void f32_gemm_kernel(const F32GemmArgs a) {
+    constexpr bool Q6 = FMT == T_Q6_K;
     extern __shared__ uint4 lds[];
     auto hi_plane = [&](int buf) { return lds + buf * kBuf; };
     auto lo_plane = [&](int buf) { return lds + buf * kBuf + kPlane; };
@@ -131,20 +157,47 @@ __global__ __launch_bounds__(kThreads) void q4k_f32_gemm_kernel(const F32GemmArg
 #pragma unroll
         for (int t = 0; t < kNT; ++t) acc[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    struct WRaw {
+    struct WRawQ4 {
         uint4 hdr[kNT];
         uint2 qs[kNT][4];
+    };
+    struct WRawQ6 {
+        K6Raw k[kNT];
+    };
+    using WRaw = std::conditional_t<Q6, WRawQ6, WRawQ4>;
+    // Q6_K: super-block s of the rows (past the end the last one of the same parity), from the aligned
+    // address at or 2 before it
+    auto sbase = [&](int t, int sb) {
+        sb = min(sb, a.nsb - 2 + (sb & 1));
+        return wrow[t] + static_cast<size_t>(sb) * 210 - 2 * (sb & 1);
+    };
+    auto fetch_half = [&](WRawQ6 &w, int sb, int h) {
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+            const uint8_t *b = sbase(t, sb);
+            load3(w.k[t].ql[2 * h], b + 64 * h + 8 * g);
+            load3(w.k[t].ql[2 * h + 1], b + 64 * h + 32 + 8 * g);
+            load3(w.k[t].qh[h], b + 128 + 32 * h + 8 * g);
+        }
+    };
+    auto fetch_sd = [&](WRawQ6 &w, int sb) {
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+            const uint32_t *q = reinterpret_cast<const uint32_t *>(sbase(t, sb) + 192);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) w.k[t].sd[i] = q[i];
+        }
     };
     struct XRaw {
         float4 v[8];
     };
     // past the end a fetch reloads the last super-block (valid addresses, never used)
-    auto fetch_hdr = [&](WRaw &w, int sb) {
+    auto fetch_hdr = [&](WRawQ4 &w, int sb) {
         sb = min(sb, a.nsb - 1);
 #pragma unroll
         for (int t = 0; t < kNT; ++t) w.hdr[t] = *reinterpret_cast<const uint4 *>(wrow[t] + static_cast<size_t>(sb) * 144);
     };
-    auto fetch_qs = [&](WRaw &w, int sb, int pr) {
+    auto fetch_qs = [&](WRawQ4 &w, int sb, int pr) {
         sb = min(sb, a.nsb - 1);
 #pragma unroll
         for (int t = 0; t < kNT; ++t)
@@ -190,20 +243,118 @@ __global__ __launch_bounds__(kThreads) void q4k_f32_gemm_kernel(const F32GemmArg
             ph[16 * gg] = make_uint4(h[0], h[1], h[2], h[3]);
             pl[16 * gg] = make_uint4(l[0], l[1], l[2], l[3]);
         }
-        float sum = 0.0f;
+        if constexpr (!Q6) {
+            float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) sum += xs[i];
-        sum *= 0.03125f;
-        const _Float16 sh = static_cast<_Float16>(sum);
-        const _Float16 sl = static_cast<_Float16>(sum - static_cast<float>(sh));
-        reinterpret_cast<_Float16 *>(hi_rows(buf) + smt * 64 + sn)[sj] = sh;
-        reinterpret_cast<_Float16 *>(lo_rows(buf) + smt * 64 + sn)[sj] = sl;
+            for (int i = 0; i < 32; ++i) sum += xs[i];
+            sum *= 0.03125f;
+            const _Float16 sh = static_cast<_Float16>(sum);
+            const _Float16 sl = static_cast<_Float16>(sum - static_cast<float>(sh));
+            reinterpret_cast<_Float16 *>(hi_rows(buf) + smt * 64 + sn)[sj] = sh;
+            reinterpret_cast<_Float16 *>(lo_rows(buf) + smt * 64 + sn)[sj] = sl;
+        }
         if (sj == 0) exps(buf)[st] = s;
     };
 
     // One super-block: B operands of the 8 sub-blocks against both x parts into one accumulator per
     // tile, the min term, then the scaled, exponent-corrected sum into acc.
-    auto compute = [&](WRaw &w, int buf, int next) {
+    struct Frag {
+        uint4 h[kMT], l[kMT];
+    };
+    auto load_frag_of = [&](Frag &f, int buf, int J) {
+        const uint4 *hp = hi_plane(buf), *lp = lo_plane(buf);
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) {
+            f.h[i] = hp[(i * 8 + J) * 64 + lane];
+            f.l[i] = lp[(i * 8 + J) * 64 + lane];
+        }
+    };
+    // Q6_K: one super-block's blocks (three MFMAs each), then d and the exponent into acc
+    auto compute_q6 = [&](WRawQ6 &w, int buf, int next) {
+        const int off = 2 * (next - 1 & 1);
+        uint32_t s4[kNT][4];
+        float dw[kNT];
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s4[t][i] = __builtin_amdgcn_alignbyte(w.k[t].sd[i + 1], w.k[t].sd[i], off);
+            dw[t] = f16_bits_to_f32((w.k[t].sd[4] >> (8 * off)) & 0xffffu);
+        }
+        fetch_sd(w, next);
+        f32x4 D[kMT][kNT];
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+#pragma unroll
+            for (int t = 0; t < kNT; ++t) D[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const int gb = g >> 1;
+        auto block = [&](auto jc, const Frag &f) {
+            constexpr int J = decltype(jc)::value, H = J >> 2, G6 = J & 3;
+            uint4 B1[kNT], B2[kNT];
+#pragma unroll
+            for (int t = 0; t < kNT; ++t) {
+                // scale 8 H + 2 G6 + g / 2 = byte 2 J + g / 2 of the 16, as the fp16 pair (sc, sc)
+                const uint32_t scb = (s4[t][J >> 1] >> (8 * (2 * (J & 1) + gb))) ^ 0x80u;
+                const f16x2 sc2 = u2h(__builtin_amdgcn_perm(0x64646464u, scb, 0x04000400u)) + splat(-1152.0f);
+                const uint2 l2 = piece(w.k[t].ql[2 * H + (G6 & 1)], off), h2 = piece(w.k[t].qh[H], off);
+                const uint32_t u0 = ((l2.x >> (4 * (G6 >> 1))) & 0x0f0f0f0fu) | (((h2.x >> (2 * G6)) & 0x03030303u) << 4);
+                const uint32_t u1 = ((l2.y >> (4 * (G6 >> 1))) & 0x0f0f0f0fu) | (((h2.y >> (2 * G6)) & 0x03030303u) << 4);
+                const f16x2 c32 = splat(-1056.0f);  // (q, 0x64) = 1024 + q
+                f16x2 q[4];
+                q[0] = u2h(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) + c32;
+                q[1] = u2h(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) + c32;
+                q[2] = u2h(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) + c32;
+                q[3] = u2h(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) + c32;
+                uint32_t b1[4], b2[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f16x2 p1 = q[e] * sc2;
+                    b1[e] = h2u(p1);
+                    b2[e] = h2u(__builtin_elementwise_fma(q[e], sc2, -p1));
+                }
+                B1[t] = make_uint4(b1[0], b1[1], b1[2], b1[3]);
+                B2[t] = make_uint4(b2[0], b2[1], b2[2], b2[3]);
+            }
+#pragma unroll
+            for (int i = 0; i < kMT; ++i)
+#pragma unroll
+                for (int t = 0; t < kNT; ++t) {
+                    D[i][t] = mfma(f.h[i], B1[t], D[i][t]);
+                    D[i][t] = mfma(f.h[i], B2[t], D[i][t]);
+                    D[i][t] = mfma(f.l[i], B1[t], D[i][t]);
+                }
+            if constexpr (J == 3) fetch_half(w, next, 0);
+            if constexpr (J == 7) fetch_half(w, next, 1);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        Frag f0, f1;
+        load_frag_of(f0, buf, 0);
+        load_frag_of(f1, buf, 1);
+        block(ic<0>{}, f0);
+        load_frag_of(f0, buf, 2);
+        block(ic<1>{}, f1);
+        load_frag_of(f1, buf, 3);
+        block(ic<2>{}, f0);
+        load_frag_of(f0, buf, 4);
+        block(ic<3>{}, f1);
+        load_frag_of(f1, buf, 5);
+        block(ic<4>{}, f0);
+        load_frag_of(f0, buf, 6);
+        block(ic<5>{}, f1);
+        load_frag_of(f1, buf, 7);
+        block(ic<6>{}, f0);
+        block(ic<7>{}, f1);
+        const int *ex = exps(buf);
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) {
+            const int4 e4 = *reinterpret_cast<const int4 *>(ex + i * 16 + 4 * g);
+            const int er[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+            for (int t = 0; t < kNT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][t][r] += ldexpf(D[i][t][r] * dw[t], -er[r]);
+        }
+    };
+    auto compute = [&](WRawQ4 &w, int buf, int next) {
         const uint4 *hp = hi_plane(buf), *lp = lo_plane(buf);
         float dd[kNT], dmin[kNT];
         uint32_t mlo[kNT], mhi[kNT];
@@ -314,16 +465,23 @@ __global__ __launch_bounds__(kThreads) void q4k_f32_gemm_kernel(const F32GemmArg
 
     WRaw w;
     XRaw x;
-    fetch_hdr(w, 0);
+    if constexpr (Q6) {
+        fetch_sd(w, 0);
+        fetch_half(w, 0, 0);
+        fetch_half(w, 0, 1);
+    } else {
+        fetch_hdr(w, 0);
 #pragma unroll
-    for (int pr = 0; pr < 4; ++pr) fetch_qs(w, 0, pr);
+        for (int pr = 0; pr < 4; ++pr) fetch_qs(w, 0, pr);
+    }
     fetch_x(x, 0);
     stage(x, 0);
     fetch_x(x, 1);
     __syncthreads();
     for (int sb = 0; sb < a.nsb; ++sb) {
         const int buf = sb & 1;
-        compute(w, buf, sb + 1);
+        if constexpr (Q6) compute_q6(w, buf, sb + 1);
+        else compute(w, buf, sb + 1);
         stage(x, buf ^ 1);  // past the end: a copy of the last super-block, never read
         fetch_x(x, sb + 2);
         __syncthreads();
@@ -349,13 +507,15 @@ __global__ __launch_bounds__(kThreads) void q4k_f32_gemm_kernel(const F32GemmArg
 
 }  // namespace
 
-bool q4k_f32_gemm_ok(const uint8_t *w, size_t rb, const float *x, int in_dim) {
-    return in_dim % 256 == 0 && rb % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
-           (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+bool f32_gemm_ok(int type, const uint8_t *w, size_t rb, const float *x, int in_dim) {
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return false;
+    if (type == T_Q4_K) return in_dim % 256 == 0 && rb % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+    if (type == T_Q6_K) return in_dim % 512 == 0 && rb % 4 == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0;
+    return false;
 }
 
-hipError_t q4k_f32_gemm(const uint8_t *w, size_t rb, const float *x, float *y, int out_dim, int in_dim, int m,
-                        bool add, hipStream_t s) {
+hipError_t f32_gemm(int type, const uint8_t *w, size_t rb, const float *x, float *y, int out_dim, int in_dim, int m,
+                    bool add, hipStream_t s) {
     if (out_dim == 0 || m == 0) return hipSuccess;
     F32GemmArgs a;
     a.w = w;
@@ -368,7 +528,8 @@ hipError_t q4k_f32_gemm(const uint8_t *w, size_t rb, const float *x, float *y, i
     a.nsb = in_dim / 256;
     a.add = add ? 1 : 0;
     const dim3 grid = gemm_grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    hipLaunchKernelGGL(q4k_f32_gemm_kernel, grid, dim3(kThreads), kLdsBytes, s, a);
+    if (type == T_Q6_K) hipLaunchKernelGGL(f32_gemm_kernel<T_Q6_K>, grid, dim3(kThreads), kLdsBytes, s, a);
+    else hipLaunchKernelGGL(f32_gemm_kernel<T_Q4_K>, grid, dim3(kThreads), kLdsBytes, s, a);
     return hipGetLastError();
 }
 

@@ -86,8 +86,7 @@ hipError_t gemv(int type, const uint8_t *w, size_t rb, const float *x, float *y,
         return mfma_gemv(type, &w, &y, &n, 1, rb, x, k, add, s);
     if (type == T_Q4_K && m == 1 && q4k_stream_ok(&w, 1, rb, x, n, k, false))
         return q4k_stream_gemv(&w, &y, &n, 1, rb, x, k, add, s);
-    if (type == T_Q4_K && m >= kF32GemmMinRows && q4k_f32_gemm_ok(w, rb, x, k))
-        return q4k_f32_gemm(w, rb, x, y, n, k, m, add, s);
+    if (m >= kF32GemmMinRows && f32_gemm_ok(type, w, rb, x, k)) return f32_gemm(type, w, rb, x, y, n, k, m, add, s);
     if (m > 1 && dense_ok(type, w, nullptr, rb, x, k)) return dense_matmul(type, w, nullptr, rb, x, y, n, k, m, add, s);
     return gemv_generic(type, w, rb, x, y, n, k, m, add, s);
 }

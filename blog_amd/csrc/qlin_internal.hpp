@@ -134,15 +134,15 @@ hipError_t quantize_q8_1(const float *x, uint8_t *xq, int in_dim, int m, bool ra
 bool qblk_gemm_ok(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, int in_dim);
 hipError_t qblk_gemm_q8_1(int type, const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y, int out_dim,
                           int in_dim, int m, hipStream_t s);
-// Q4_K x f32 activations, the prefill GEMM of quant_matmul for m >= kF32GemmMinRows rows, on the fp16
-// matrix cores (qlin_f32_gemm.hip); fewer rows take dense_matmul.  add: y += the product.
+// Q4_K / Q6_K x f32 activations, the prefill GEMM of quant_matmul for m >= kF32GemmMinRows rows, on the
+// fp16 matrix cores (qlin_f32_gemm.hip); fewer rows take dense_matmul.  add: y += the product.
 #ifndef QLIN_F32_GEMM_MIN_ROWS
 #define QLIN_F32_GEMM_MIN_ROWS 64
 #endif
 constexpr int kF32GemmMinRows = QLIN_F32_GEMM_MIN_ROWS;
-bool q4k_f32_gemm_ok(const uint8_t *w, size_t row_bytes, const float *x, int in_dim);
-hipError_t q4k_f32_gemm(const uint8_t *w, size_t row_bytes, const float *x, float *y, int out_dim, int in_dim, int m,
-                        bool add, hipStream_t s);
+bool f32_gemm_ok(int type, const uint8_t *w, size_t row_bytes, const float *x, int in_dim);
+hipError_t f32_gemm(int type, const uint8_t *w, size_t row_bytes, const float *x, float *y, int out_dim, int in_dim,
+                    int m, bool add, hipStream_t s);
 // Q4_K x Q8_1 prefill GEMM on the fp16 matrix cores (qlin_q4k_gemm.hip).
 bool q4k_gemm_ok(const uint8_t *w, size_t row_bytes, const uint8_t *xq, int in_dim);
 hipError_t q4k_gemm_q8_1(const uint8_t *w, size_t row_bytes, const uint8_t *xq, float *y, int out_dim, int in_dim,

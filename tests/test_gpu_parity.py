@@ -176,7 +176,8 @@ def test_gemv_several_rows(qtype, m):
     (Q4_K, 200, 1024, 2), (Q4_K, 1000, 3584, 16), (Q4_K, 2816, 2048, 17), (Q4_K, 96, 256, 64), (Q4_K, 40, 4608, 65),
     (Q4_K, 33, 512, 130),
     (Q8_0, 4864, 896, 32), (Q8_0, 896, 4864, 32), (Q8_0, 50, 96, 5),     # C3's prompt: K 896 = 3.5 chunks
-    (Q4_0, 300, 3584, 16), (Q5_0, 2048, 1408, 6), (Q6_K, 77, 2048, 20)])
+    (Q4_0, 300, 3584, 16), (Q5_0, 2048, 1408, 6), (Q6_K, 77, 2048, 20), (Q6_K, 77, 2048, 70),
+    (Q6_K, 300, 512, 129)])
 def test_matmul_rows_f32_matrix_cores(qtype, out_dim, in_dim, m):
     """m > 1 rows (launch_quant_matmul, kernel.cu:1254-1279) on the f32 matrix cores: row tails
     (out_dim % 16), fewer and more chunks than waves, a partial last chunk (K / 32 not a multiple of
@@ -399,37 +400,44 @@ def test_q4k_gemm_c4_shape_every_row():
     assert row_err.max() <= 1e-5, (int(row_err.argmax()), float(row_err.max()))
 
 
-def test_f32_gemm_prefill_shape_every_row():
+@pytest.mark.parametrize("qtype,N,K", [(Q4_K, 14336, 4096), (Q6_K, 8192, 2048)])
+def test_f32_gemm_prefill_shape_every_row(qtype, N, K):
     """The engine's prefill entry (TensorTool::quant_direct_gemm -> launch_quant_matmul with f32
-    activations, TensorTool.cpp:163-168, kernel.cu:1254-1279) at Llama/Qwen-7B MLP shape: Q4_K
-    [14336, 4096] x [512, 4096] N(0,1) f32 activations on the fp16 matrix cores, every weight row
-    checked against the f64 oracle on 64 tokens that include both ends of every 64-token tile."""
-    N, K, M = 14336, 4096, 512
-    rng = np.random.default_rng(91)
-    rb = K // 256 * 144
-    w = rng.integers(0, 256, size=(N, K // 256, 144), dtype=np.uint8)
-    w[:, :, 0:4] = f16_bits(np.abs(rng.standard_normal((N, K // 256, 2))) * 0.01).view(np.uint8).reshape(N, K // 256, 4)
+    activations, TensorTool.cpp:163-168, kernel.cu:1254-1279) on the fp16 matrix cores: Q4_K at
+    Llama/Qwen-7B MLP shape [14336, 4096] and Q6_K at the DeepSeek-V2-Lite lm_head's K (2048, 8192 of
+    its 102400 rows) x [512, K] N(0,1) f32 activations, every weight row checked against the f64
+    oracle on 64 tokens that include both ends of every 64-token tile."""
+    M = 512
+    rng = np.random.default_rng(91 + qtype)
+    bb = 144 if qtype == Q4_K else 210
+    rb = K // 256 * bb
+    w = rng.integers(0, 256, size=(N, K // 256, bb), dtype=np.uint8)
+    if qtype == Q4_K:
+        w[:, :, 0:4] = f16_bits(np.abs(rng.standard_normal((N, K // 256, 2))) * 0.01).view(np.uint8).reshape(N, K // 256, 4)
+    else:
+        w[:, :, 208:210] = f16_bits(np.abs(rng.standard_normal((N, K // 256, 1))) * 0.01).view(np.uint8).reshape(N, K // 256, 2)
     x = rng.standard_normal((M, K)).astype(np.float32)
-    banner("f32 prefill gemm 512x4096x14336")
+    banner(f"f32 prefill gemm type={qtype} {M}x{K}x{N}")
     yd = empty_f32(M, N)
-    qlin.quant_matmul(Q4_K, dev(w.reshape(-1)), rb, dev(x), yd, N, K, M)
+    qlin.quant_matmul(qtype, dev(w.reshape(-1)), rb, dev(x), yd, N, K, M)
     ends = np.array([[64 * t, 64 * t + 63] for t in range(M // 64)]).reshape(-1)
     rest = rng.choice(np.setdiff1d(np.arange(M), ends), 64 - ends.size, replace=False)
     toks = np.sort(np.concatenate([ends, rest]))
-    ref = orc.matmul_f64(Q4_K, w.reshape(-1), rb, x[toks], N, K)
+    ref = orc.matmul_f64(qtype, w.reshape(-1), rb, x[toks], N, K)
     got = host(yd)[toks]
     assert normwise_rel_err(got, ref) <= FP32
     row_err = np.linalg.norm(got - ref, axis=0) / np.maximum(np.linalg.norm(ref, axis=0), 1e-30)
     assert row_err.max() <= 1e-5, (int(row_err.argmax()), float(row_err.max()))
 
 
-def test_f32_gemm_token_scales():
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_f32_gemm_token_scales(qtype):
     """The prefill GEMM scales each token's 256 values of a super-block by a power of two into the
     fp16 range: tokens whose values span 1e-30 .. 1e30, an all-zero token, a token with one huge
     value among tiny ones and a super-block of zeros inside a token, each within 1e-5 of the f64
     oracle relative to that token's own largest output (a shared scale would lose the small ones)."""
     N, K, M = 300, 1024, 70
-    w, rb, vals = qgen.random_matrix(Q4_K, N, K, seed=95)
+    w, rb, vals = qgen.random_matrix(qtype, N, K, seed=95)
     rng = np.random.default_rng(96)
     x = rng.standard_normal((M, K)).astype(np.float32)
     mags = [1e-30, 1e-12, 1e-3, 1.0, 1e3, 1e12, 1e30]
@@ -439,11 +447,11 @@ def test_f32_gemm_token_scales():
     x[11] = np.float32(1e-6) * rng.standard_normal(K).astype(np.float32)
     x[11, 77] = 1e6
     x[12, 256:512] = 0.0
-    banner("f32 prefill gemm token scales")
+    banner(f"f32 prefill gemm token scales type={qtype}")
     yd = empty_f32(M, N)
-    qlin.quant_matmul(Q4_K, dev(w), rb, dev(x), yd, N, K, M)
+    qlin.quant_matmul(qtype, dev(w), rb, dev(x), yd, N, K, M)
     got = host(yd)
-    ref = orc.matmul_f64(Q4_K, w, rb, x, N, K)
+    ref = orc.matmul_f64(qtype, w, rb, x, N, K)
     assert np.all(got[10] == 0.0)
     for i in range(M):
         if i == 10:
@@ -453,17 +461,17 @@ def test_f32_gemm_token_scales():
         assert err <= COND, (i, float(err))
 
 
-@pytest.mark.parametrize("m", [64, 96])
-def test_f32_gemm_add(m):
+@pytest.mark.parametrize("qtype,m", [(Q4_K, 64), (Q4_K, 96), (Q6_K, 96)])
+def test_f32_gemm_add(qtype, m):
     """y += W x over m >= 64 tokens (launch_quant_matmul's add form) on the prefill GEMM."""
     N, K = 520, 2048
-    w, rb, _ = qgen.random_matrix(Q4_K, N, K, seed=97 + m)
+    w, rb, _ = qgen.random_matrix(qtype, N, K, seed=97 + m)
     x = qgen.random_x(m, K, seed=98 + m)
     y0 = np.random.default_rng(99).standard_normal((m, N)).astype(np.float32)
     banner(f"f32 prefill gemm add m={m}")
     yd = dev(y0)
-    qlin.quant_matmul_add(Q4_K, dev(w), rb, dev(x), yd, N, K, m)
-    ref = y0.astype(np.float64) + orc.matmul_f64(Q4_K, w, rb, x, N, K)
+    qlin.quant_matmul_add(qtype, dev(w), rb, dev(x), yd, N, K, m)
+    ref = y0.astype(np.float64) + orc.matmul_f64(qtype, w, rb, x, N, K)
     assert normwise_rel_err(host(yd), ref) <= FP32
 
 
