@@ -350,9 +350,10 @@ def cpu_gemv_gbs(torch, qtype, w_dev, rb, n, k, seconds):
             "one_thread_gbs": round(gbs1, 3), "one_thread_sample": f"{p1} passes, {t1:.1f} s", **host_cpu()}
 
 
-def gemv_config(args, torch, qlin, gen, workload, metric, qtype, shapes, copies):
-    """shapes: [(name, rows, cols)] launched in order per step; `copies` distinct sets rotate."""
-    sets = [[synth_blocks(torch, qtype, n, k, gen) for _, n, k in shapes] for _ in range(copies)]
+def gemv_config(args, torch, qlin, gen, workload, metric, qtype, shapes, copies, scale=0.01):
+    """shapes: [(name, rows, cols)] launched in order per step; `copies` distinct sets rotate; block
+    scales f16(|N(0,1)| * scale)."""
+    sets = [[synth_blocks(torch, qtype, n, k, gen, scale) for _, n, k in shapes] for _ in range(copies)]
     xs = {k: torch.randn(k, device="cuda", generator=gen) for _, _, k in shapes}
     ys = {n: torch.empty(n, device="cuda") for _, n, _ in shapes}
     rbs = [qlin.row_bytes(qtype, k) for _, _, k in shapes]
@@ -397,7 +398,7 @@ def wl_c1(args, torch, qlin, gen):
 def wl_c2(args, torch, qlin, gen):
     return gemv_config(args, torch, qlin, gen, "c2-q4_0-ffn-triple",
                        "Q4_0 GEMV triple HBM GB/s (Qwen2-7B FFN gate, up, down; batch 1)", Q4_0,
-                       [("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)], 10)
+                       [("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)], 10, scale=0.02)
 
 
 def wl_q6k(args, torch, qlin, gen):
@@ -584,16 +585,16 @@ def wl_c4(args, torch, qlin, gen):
         w = ws[0].view(N, -1)[:rows].contiguous().view(-1).cpu().numpy()
         xh = x.cpu().numpy()
         xqh = orc.quantize_q8_1(xh, K)
-        passes, t = 0, 0.0
-        while t < args.cpu_seconds:
-            t0 = time.perf_counter()
-            orc.matmul_q8_1(Q4_K, w, rb, xqh, rows, K, M)
-            t += time.perf_counter() - t0
-            passes += 1
+        threads = cpu_threads()
+        ps, p, t, ps1, p1, t1 = cpu_timed(lambda nt: orc.matmul_q8_1(Q4_K, w, rb, xqh, rows, K, M, threads=nt),
+                                          threads, args.cpu_seconds)
+        f = 2.0 * M * rows * K
         result["cpu_baseline"] = {
-            "value": round(2.0 * M * rows * K * passes / t / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
-            "kind": "port", "sample": f"{rows} of the {N} weight rows x {M} tokens x {K}, {passes} passes, "
-                                      f"{t:.1f} s; oracle orc_matmul_q8_1 (reference block-dot order, f64)"}
+            "value": round(f * ps / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of the {N} weight rows x {M} tokens x {K}, {p} passes, {t:.1f} s; oracle "
+                      f"orc_matmul_q8_1 (reference block-dot order, f64; OpenMP over rows)",
+            "one_thread_tflops": round(f * ps1 / 1e12, 5), "one_thread_sample": f"{p1} passes, {t1:.1f} s",
+            **host_cpu()}
     return result
 
 
@@ -651,71 +652,86 @@ def wl_prefill(args, torch, qlin, gen):
         rows = 64
         wh = w.view(N, -1)[:rows].contiguous().view(-1).cpu().numpy()
         xqh = orc.quantize_q8_1(x.cpu().numpy(), K)
-        passes, t = 0, 0.0
-        while t < args.cpu_seconds:
-            t0 = time.perf_counter()
-            orc.matmul_q8_1(Q6_K, wh, rb, xqh, rows, K, M)
-            t += time.perf_counter() - t0
-            passes += 1
+        threads = cpu_threads()
+        ps, p, t, ps1, p1, t1 = cpu_timed(lambda nt: orc.matmul_q8_1(Q6_K, wh, rb, xqh, rows, K, M, threads=nt),
+                                          threads, args.cpu_seconds)
+        f = 2.0 * M * rows * K
         result["cpu_baseline"] = {
-            "value": round(2.0 * M * rows * K * passes / t / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
-            "kind": "port", "sample": f"{rows} of the {N} weight rows x {M} tokens x {K}, {passes} passes, "
-                                      f"{t:.1f} s; oracle orc_matmul_q8_1 (reference block-dot order, f64)"}
+            "value": round(f * ps / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of the {N} weight rows x {M} tokens x {K}, {p} passes, {t:.1f} s; oracle "
+                      f"orc_matmul_q8_1 (reference block-dot order, f64; OpenMP over rows)",
+            "one_thread_tflops": round(f * ps1 / 1e12, 5), "one_thread_sample": f"{p1} passes, {t1:.1f} s",
+            **host_cpu()}
     return result
 
 
-def wl_floor(args, torch, qlin, gen):
-    """The decode step's launch structure with the kernels replaced by plain streaming reads
-    (qlin_probe_stream_read): per token M's 113 launches (per layer q/k/v, o, gate/up, down; then the
-    lm_head) each reading a distinct region of one buffer of the same size as its weights; the same 113
-    launches with nothing to read; and one launch reading all of a token's bytes.  The floor that any
-    113-launch kernel sequence over these bytes meets on this GPU."""
-    L = qlin.lib()
-    rbh, rbf = qlin.row_bytes(Q4_K, HIDDEN), qlin.row_bytes(Q4_K, FFN)
-    sizes = []
-    for _ in range(LAYERS):
-        sizes += [(HIDDEN + 2 * KV) * rbh, HIDDEN * rbh, 2 * FFN * rbh, HIDDEN * rbf]
-    sizes.append(VOCAB * rbh)
-    sizes = [(n + 255) // 256 * 256 for n in sizes]
-    total = sum(sizes)
-    buf = torch.empty(total, dtype=torch.uint8, device="cuda")
-    buf.fill_(1)
-    sink = torch.zeros(1, device="cuda")
-    base, sp = buf.data_ptr(), sink.data_ptr()
+def cpu_timed(fn, threads, seconds):
+    """Calls fn(nthreads) for about `seconds` on the process's thread share and for half as long on one
+    thread; returns (passes/s on the share, passes, s, passes/s on one thread, passes, s)."""
+    def timed(nthreads, budget):
+        passes, t = 0, 0.0
+        while t < budget or passes == 0:
+            t0 = time.perf_counter()
+            fn(nthreads)
+            t += time.perf_counter() - t0
+            passes += 1
+        return passes / t, passes, t
+    return (*timed(threads, seconds), *timed(1, seconds / 2))
 
-    def launches(nbytes_of, wgs):
-        off = 0
-        for n in sizes:
-            rc = L.qlin_probe_stream_read(base + off, nbytes_of(n), wgs, sp)
-            if rc != 0:
-                raise qlin.QlinError("qlin_probe_stream_read", rc)
-            off += n
 
-    reps = max(5, args.steps // 4)
-    res = {}
-    for wgs in (1024, 2048, 4096):
-        res[f"reads_{wgs}_wg_us"] = round(graph_us(torch, qlin, lambda w=wgs: launches(lambda n: n, w), reps), 1)
-    res["empty_113_us"] = round(graph_us(torch, qlin, lambda: launches(lambda n: 0, 256), reps), 1)
-
-    def one():
-        rc = L.qlin_probe_stream_read(base, total, 4096, sp)
-        if rc != 0:
-            raise qlin.QlinError("qlin_probe_stream_read", rc)
-
-    res["one_launch_us"] = round(graph_us(torch, qlin, one, reps), 1)
-    best = min(v for k, v in res.items() if k.startswith("reads_"))
-    log(f"floor: 113 streaming launches {best:.1f} us/token, 113 empty launches {res['empty_113_us']:.1f} us, "
-        f"one launch of all {total / 1e9:.2f} GB {res['one_launch_us']:.1f} us")
-    return {
-        "metric": "decode-step streaming floor: 113 plain-read launches of M's bytes (tokens/s)",
-        "value": round(1e6 / best, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": 3,
-        "ms_per_step": round(best / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8 (bytes read)", "data": "synthetic (a buffer of M's per-token bytes, contents irrelevant)",
-        "config": {"workload": "decode-stream-floor", "launches_per_step": len(sizes), "bytes_per_step": total,
-                   "gbs_at_floor": round(total / best / 1e3, 1),
-                   "pct_of_peak_at_floor": round(100 * total / best / 1e3 / PEAK_HBM_GBS, 2),
-                   "one_launch_gbs": round(total / res["one_launch_us"] / 1e3, 1), **res},
+def wl_prefill_f32(args, torch, qlin, gen):
+    """The prefill entry the engine calls (TensorTool::quant_direct_gemm -> launch_quant_matmul, f32
+    activations, TensorTool.cpp:163-168, kernel.cu:1254-1279): Q4_K [14336, 4096] x [512, 4096] (the
+    headline) and DeepSeek-V2-Lite's Q6_K lm_head [102400, 2048] x [512, 2048], N(0,1) f32 activations.
+    A step is one qlin_launch_quant_matmul; two weight copies are rotated."""
+    M = 512
+    shapes = [("q4k_mlp", Q4_K, 14336, 4096), ("q6k_lm_head", Q6_K, 102400, 2048)]
+    res, head = {}, None
+    for name, qt, N, K in shapes:
+        rb = qlin.row_bytes(qt, K)
+        ws = [synth_blocks(torch, qt, N, K, gen) for _ in range(2)]
+        x = torch.randn(M, K, device="cuda", generator=gen)
+        y = torch.empty(M, N, device="cuda")
+        reps = max(10, args.steps // 4)
+        us = graph_us(torch, qlin, lambda qt=qt, ws=ws, rb=rb, x=x, y=y, N=N, K=K:
+                      [qlin.quant_matmul(qt, w, rb, x, y, N, K, M) for w in ws], reps) / len(ws)
+        flops = 2.0 * M * N * K
+        res[name] = {"type": qt, "n": N, "k": K, "us": round(us, 2), "tflops": round(flops / us / 1e6, 1)}
+        log(f"prefill f32 {name}: {us:.2f} us ({flops / us / 1e6:.1f} TFLOP/s)")
+        if head is None:
+            head = (qt, ws[0], rb, x, N, K, us, flops, reps)
+    qt, w, rb, x, N, K, us, flops, reps = head
+    result = {
+        "metric": "Q4_K x f32 prefill GEMM TFLOP/s (launch_quant_matmul, M=512, K=4096, N=14336)",
+        "value": round(flops / us / 1e6, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps * 2, "warmup": 3,
+        "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 (x 2^s as hi + lo parts) x f16 (integers sc*q), f32 accumulation",
+        "data": "synthetic (random Q4_K / Q6_K blocks; f32 N(0,1) activations)",
+        "config": {"workload": "prefill-f32-gemm", "m": M, "k": K, "n": N, "weight_format": "Q4_K",
+                   "activation_format": "f32", "algorithmic_flops_per_step": flops,
+                   "launches_per_step": ["quant_matmul"], "execution": "hip graph replay", "shapes": res},
+        "roofline": {"bound": "mfma", "achieved": round(flops / us / 1e6, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(flops / us / 1e6 / 2500.0, 4), "traffic": None,
+                     "kernel": "f32_gemm_kernel<12> (fp16 MFMA 16x16x32, two per block; peak = dense fp16)",
+                     "avg_launch_us": round(us, 3), "algorithmic_flops_per_launch": flops},
     }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        rows, toks = 64, 64
+        wh = w.view(N, -1)[:rows].contiguous().view(-1).cpu().numpy()
+        xh = np.ascontiguousarray(x[:toks].cpu().numpy())
+        threads = cpu_threads()
+        ps, p, t, ps1, p1, t1 = cpu_timed(lambda nt: orc.matmul_f32(qt, wh, rb, xh, rows, K, nt), threads,
+                                          args.cpu_seconds)
+        f = 2.0 * rows * toks * K
+        result["cpu_baseline"] = {
+            "value": round(f * ps / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of the {N} weight rows x {toks} of the {M} tokens x {K}, {p} passes, {t:.1f} s; "
+                      f"oracle orc_matmul_f32 (the reference's f32 dot per (token, row), OpenMP over rows)",
+            "one_thread_tflops": round(f * ps1 / 1e12, 5), "one_thread_sample": f"{p1} passes, {t1:.1f} s",
+            **host_cpu()}
+    return result
 
 
 def wl_c5(args, torch, qlin, gen):
@@ -803,9 +819,11 @@ def wl_c5(args, torch, qlin, gen):
 
 
 def cpu_moe_gbs(torch, mats, x, ids, rw, E, ffn, hid, k, seconds):
-    """The oracle's per-token routed MoE (orc_swiglu_indexed, then orc_down_indexed_ordered; one thread,
-    double-precision sums) over the batch's tokens for about `seconds`: GB/s of the expert bytes that
-    each token's routes read."""
+    """The oracle's per-token routed MoE (orc_swiglu_indexed, then orc_down_indexed_ordered, double-
+    precision sums) over the batch's tokens for about `seconds`: on the process's thread share (one
+    token per thread at a time; the oracle's calls release the interpreter) and on one thread.  GB/s of
+    the expert bytes that each token's routes read."""
+    import concurrent.futures as cf
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     wg, wu, wd = (t.cpu().numpy() for t in mats[:3])
@@ -813,19 +831,32 @@ def cpu_moe_gbs(torch, mats, x, ids, rw, E, ffn, hid, k, seconds):
     grb, drb = geb // ffn, deb // hid
     xs, idh, rwh = x.cpu().numpy(), ids.cpu().numpy(), rw.cpu().numpy()
     per_token = k * (2 * geb + deb)
-    tokens, t = 0, 0.0
-    out = np.zeros(hid, np.float32)
-    while t < seconds or tokens == 0:
-        i = tokens % xs.shape[0]
-        t0 = time.perf_counter()
+
+    def token(i):
+        out = np.zeros(hid, np.float32)
         act = orc.swiglu_indexed(Q4_K, wg, wu, geb, geb, grb, grb, xs[i], idh[i], ffn, hid)
         orc.down_indexed_ordered(6, wd, deb, drb, act, idh[i], rwh[i], out, hid, ffn)
-        t += time.perf_counter() - t0
-        tokens += 1
-    return {"value": round(per_token * tokens / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+
+    def timed(nthreads, budget):
+        tokens, t = 0, 0.0
+        with cf.ThreadPoolExecutor(max_workers=nthreads) as ex:
+            while t < budget or tokens == 0:
+                batch = [(tokens + j) % xs.shape[0] for j in range(nthreads)]
+                t0 = time.perf_counter()
+                list(ex.map(token, batch))
+                t += time.perf_counter() - t0
+                tokens += nthreads
+        return tokens, t
+
+    threads = cpu_threads()
+    tokens, t = timed(threads, seconds)
+    tokens1, t1 = timed(1, seconds / 2)
+    return {"value": round(per_token * tokens / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "tokens_per_s": round(tokens / t, 2),
-            "sample": f"{tokens} tokens' routed experts ({per_token / 1e6:.1f} MB each), {t:.1f} s; oracle "
-                      f"orc_swiglu_indexed + orc_down_indexed_ordered (one thread)", **host_cpu()}
+            "sample": f"{tokens} tokens' routed experts ({per_token / 1e6:.1f} MB each), {t:.1f} s, {threads} "
+                      f"tokens at a time; oracle orc_swiglu_indexed + orc_down_indexed_ordered",
+            "one_thread_gbs": round(per_token * tokens1 / t1 / 1e9, 3),
+            "one_thread_sample": f"{tokens1} tokens, {t1:.1f} s", **host_cpu()}
 
 
 def wl_moe_token(args, torch, qlin, gen):
@@ -934,7 +965,7 @@ def wl_moe_token(args, torch, qlin, gen):
 WORKLOADS = {"qwen2-7b-q4k-decode-token": None, "c5-moe-grouped": wl_c5, "c1-q8_0-gemv-4096": wl_c1, "c2-q4_0-ffn-triple": wl_c2,
              "c3-q8_0-decode-token": wl_c3, "c4-q4k-prefill-gemm": wl_c4, "deepseek-q6_k-lm-head": wl_q6k,
              "deepseek-moe-token": wl_moe_token, "deepseek-prefill-gemm": wl_prefill,
-             "decode-stream-floor": wl_floor}
+             "prefill-f32-gemm": wl_prefill_f32}
 
 
 def host_cpu() -> dict:

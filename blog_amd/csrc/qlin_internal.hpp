@@ -92,8 +92,11 @@ hipError_t mfma_down_routed(int type, const uint8_t *wd, size_t expert_bytes, si
                             const int *ids, const float *rw, float *out, int routes, int hidden, int ffn_dim,
                             hipStream_t s);
 
-// Q4_K over m > 1 rows of f32 activations on the f32 matrix cores (qlin_dense.hip): mode 0 stores
-// y[r, o], 1 adds into it, 2 writes act[r, o] = silu(gate . x_r) * (up . x_r) with w1 the up matrix.
+// m > 1 rows of f32 activations (qlin_dense.hip), for fewer than kF32GemmMinRows rows or the other
+// formats: Q4_K on the bf16 matrix cores with x as bf16 hi + lo (x to about 2^-17 of itself, products
+// exact, f32 accumulation), the other formats on the f32 matrix cores with the reference's f32 operands.
+// Mode 0 stores y[r, o], 1 adds into it, 2 writes act[r, o] = silu(gate . x_r) * (up . x_r) with w1 the up
+// matrix.
 bool dense_ok(int type, const uint8_t *w0, const uint8_t *w1, size_t row_bytes, const float *x, int in_dim);
 // mode 1 (y +=) with combine: y = (y + the routed total) + the product, as the combine launch and then
 // the plain mode 1 give it

@@ -526,7 +526,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         }
     }
     if constexpr (ROUTED) {
-        // the routes' experts (and down weights): every weight address depends on them
+        // the routes' experts (and down weights): every weight address depends on them.  A route that
+        // nothing below sets stays -1 (no expert: its loads read expert 0 and its results are dropped);
+        // these writes and every later one are wave 0's, so they land in program order.
+        if (tid < kMaxRoutes) s_ids[tid] = -1;
         bool routed_here = false;
         if constexpr (SWIGLU) {
             if (a.logits) {  // uniform: wave 0 routes the token (the only live wave: its LDS alone)

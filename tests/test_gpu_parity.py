@@ -113,7 +113,9 @@ GEMV_CASES = [
 
 @pytest.mark.parametrize("qtype,out_dim,in_dim", GEMV_CASES)
 def test_gemv_parity(qtype, out_dim, in_dim):
-    w, rb, vals = qgen.random_matrix(qtype, out_dim, in_dim, seed=out_dim * 7 + in_dim + qtype)
+    # block scales f16(|N(0,1)| * 0.01), and * 0.02 for Q4_0 as the Qwen2-7B Q4_0 FFN configuration draws them
+    w, rb, vals = qgen.random_matrix(qtype, out_dim, in_dim, seed=out_dim * 7 + in_dim + qtype,
+                                     scale=0.02 if qtype == Q4_0 else 0.01)
     x = qgen.random_x(1, in_dim, seed=in_dim + 1)
     banner(f"gemv type={qtype} N={out_dim} K={in_dim}")
     y = gpu_gemv(qtype, w, rb, x, out_dim, in_dim)
@@ -179,9 +181,11 @@ def test_gemv_several_rows(qtype, m):
     (Q4_0, 300, 3584, 16), (Q5_0, 2048, 1408, 6), (Q6_K, 77, 2048, 20), (Q6_K, 77, 2048, 70),
     (Q6_K, 300, 512, 129)])
 def test_matmul_rows_f32_matrix_cores(qtype, out_dim, in_dim, m):
-    """m > 1 rows (launch_quant_matmul, kernel.cu:1254-1279) on the f32 matrix cores: row tails
-    (out_dim % 16), fewer and more chunks than waves, a partial last chunk (K / 32 not a multiple of
-    8), token tails within and across 64-token grid rows, and every format."""
+    """m > 1 rows (launch_quant_matmul, kernel.cu:1254-1279) on the matrix cores: below 64 rows, Q4_K on
+    the bf16 ones (x as bf16 hi + lo) and the other formats on the f32 ones; from 64 rows, Q4_K and Q6_K
+    on the prefill GEMM (fp16, x as scaled hi + lo).  Row tails (out_dim % 16, and of the GEMM's 256-row
+    tiles), fewer and more chunks than waves, a partial last chunk (K / 32 not a multiple of 8), token
+    tails within and across 64-token tiles, and every format."""
     w, rb, vals = qgen.random_matrix(qtype, out_dim, in_dim, seed=out_dim + m + qtype)
     x = qgen.random_x(m, in_dim, seed=m + 7)
     banner(f"dense matmul type={qtype} n={out_dim} k={in_dim} m={m}")
@@ -1011,8 +1015,9 @@ def test_swiglu_stream(ffn, hid):
 def test_swiglu_matrix_core_formats(qtype, ffn, hid):
     """Fused gate/up SiLU on the 32-weight formats (C2's gate/up pair in one launch) and on Q6_K
     (rows of whole 16-byte units at hid = 2048, of dwords at 768)."""
-    wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=410 + hid)
-    wu, _, _ = qgen.random_matrix(qtype, ffn, hid, seed=411 + hid)
+    sc = 0.02 if qtype == Q4_0 else 0.01  # the Qwen2-7B Q4_0 FFN configuration's block scales
+    wg, rb, _ = qgen.random_matrix(qtype, ffn, hid, seed=410 + hid, scale=sc)
+    wu, _, _ = qgen.random_matrix(qtype, ffn, hid, seed=411 + hid, scale=sc)
     x = qgen.random_x(1, hid, seed=412)[0]
     act_d = empty_f32(ffn)
     banner(f"swiglu type={qtype} ffn={ffn} hid={hid}")

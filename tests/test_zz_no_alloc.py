@@ -11,7 +11,7 @@ import oracle as orc
 import qgen
 from blog_amd import qlin
 from gpu_util import banner, bind_stream, dev, host
-from qgen import Q4_K, Q5_0
+from qgen import Q4_K, Q5_0, Q6_K
 
 pytestmark = pytest.mark.gpu
 
@@ -27,39 +27,56 @@ def _stream():
 E, FFN, HID, K = 16, 512, 1024, 4
 
 
-@pytest.fixture(scope="module")
-def experts():
-    wg, grb, _ = qgen.random_matrix(Q4_K, E * FFN, HID, seed=1201)
-    wu, _, _ = qgen.random_matrix(Q4_K, E * FFN, HID, seed=1202)
-    wd, drb, _ = qgen.random_matrix(Q5_0, E * HID, FFN, seed=1203)
+def _experts(gu_type, e, ffn, hid, seed):
+    wg, _, _ = qgen.random_matrix(gu_type, e * ffn, hid, seed=seed)
+    wu, _, _ = qgen.random_matrix(gu_type, e * ffn, hid, seed=seed + 1)
+    wd, _, _ = qgen.random_matrix(Q5_0, e * hid, ffn, seed=seed + 2)
     return dev(wg), dev(wu), dev(wd), wg.size, wd.size
 
 
-def _inputs(tokens, seed):
+@pytest.fixture(scope="module")
+def experts():
+    return _experts(Q4_K, E, FFN, HID, 1201)
+
+
+def _inputs(tokens, e, hid, seed):
     rng = np.random.default_rng(seed)
-    x = rng.standard_normal((tokens, HID)).astype(np.float32)
-    ids, rw = orc.router_topk(rng.standard_normal((tokens, E)).astype(np.float32), K, 1.0)
+    x = rng.standard_normal((tokens, hid)).astype(np.float32)
+    ids, rw = orc.router_topk(rng.standard_normal((tokens, e)).astype(np.float32), K, 1.0)
     ids = np.ascontiguousarray(ids)
     ids[0, 1] = -1  # a route without an expert
-    out0 = rng.standard_normal((tokens, HID)).astype(np.float32)
+    out0 = rng.standard_normal((tokens, hid)).astype(np.float32)
     return x, ids, np.ascontiguousarray(rw), out0
 
 
-def test_noalloc_equals_workspace_entry_on_two_calls(experts):
-    wg, wu, wd, gub, db = experts
-    for call, tokens in enumerate((12, 3)):
-        x, ids, rw, out0 = _inputs(tokens, 1210 + call)
+# Every path that runs on the shared scratch, each on two calls in a row with fewer tokens the second
+# time (the second call reads the array the first one left): the gate/up launch grouping the routes
+# itself (16 experts, 48 and 12 routes); group_kernel first, for more than 256 experts and for more
+# than 1024 routes; and the per-token kernels with act in the scratch (Q6_K gate/up, which the grouped
+# kernels do not take).
+CASES = [("in-kernel grouping", Q4_K, E, FFN, HID, (12, 3)),
+         ("group_kernel: 300 experts", Q4_K, 300, 64, 256, (12, 3)),
+         ("group_kernel: 1200 routes", Q4_K, 16, 64, 256, (300, 260)),
+         ("per-token Q6_K gate/up", Q6_K, 16, 128, 512, (6, 2))]
+
+
+@pytest.mark.parametrize("name,gu_type,e,ffn,hid,calls", CASES, ids=[c[0] for c in CASES])
+def test_noalloc_equals_workspace_entry_on_two_calls(name, gu_type, e, ffn, hid, calls):
+    wg, wu, wd, gub, db = _experts(gu_type, e, ffn, hid, 1201 + e + ffn)
+    for call, tokens in enumerate(calls):
+        x, ids, rw, out0 = _inputs(tokens, e, hid, 1210 + call + e)
         xd, idd, rwd = dev(x), dev(ids), dev(rw)
-        banner(f"moe noalloc call {call} tokens={tokens}")
-        nbytes = qlin.lib().qlin_moe_grouped_workspace_bytes(tokens, K, E, FFN, HID)
+        banner(f"moe noalloc {name} call {call} tokens={tokens}")
+        nbytes = qlin.lib().qlin_moe_grouped_workspace_bytes(tokens, K, e, ffn, hid)
+        assert nbytes <= (8 << 20)
         ws = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
         wsp = (ws.data_ptr() + 255) // 256 * 256
         out_ws = dev(out0)
-        qlin.call("qlin_moe_routed_decode_grouped", Q4_K, wg, wu, gub, Q5_0, wd, db, E, FFN, HID, HID, xd, idd, rwd,
-                  wsp, nbytes, out_ws, tokens, K)
+        qlin.call("qlin_moe_routed_decode_grouped", gu_type, wg, wu, gub, Q5_0, wd, db, e, ffn, hid, hid, xd, idd,
+                  rwd, wsp, nbytes, out_ws, tokens, K)
         out_na = dev(out0)
-        qlin.call("qlin_moe_routed_decode_grouped_noalloc", Q4_K, wg, wu, gub, Q5_0, wd, db, E, FFN, HID, HID, xd, idd,
-                  rwd, out_na, tokens, K)
+        qlin.call("qlin_moe_routed_decode_grouped_noalloc", gu_type, wg, wu, gub, Q5_0, wd, db, e, ffn, hid, hid, xd,
+                  idd, rwd, out_na, tokens, K)
         a, b = host(out_na), host(out_ws)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
         assert not np.array_equal(a, out0)
