@@ -25,6 +25,9 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # keep every IEEE operation as written (bit-exact dequant); explicit fmaf() calls still fuse
     "-ffp-contract=off",
+    # leading scalar kernel arguments preloaded into SGPRs at wave launch (gfx950), so a wave's first
+    # requests need no scalar load of the argument segment
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

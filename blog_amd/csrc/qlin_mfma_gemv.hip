@@ -227,6 +227,20 @@ __device__ __forceinline__ void pick_better(float &v, int &i, float v2, int i2) 
 
 constexpr int kMaxRoutes = 16;  // routes of one routed launch (top-k of one token)
 
+// What every wave needs before its first requests (x, the first matrix, the row stride and the
+// step decomposition), passed as leading scalar kernel arguments: gfx950 preloads those into SGPRs
+// when it launches the wave, so the first x and weight requests wait for no scalar load of the
+// argument block, which follows them (its fields: MfmaArgs).
+// (13 dwords: at most 14 are preloaded, beside the argument segment's own pointer, in the 16 user SGPRs.)
+struct Lead {
+    const float *x;
+    const uint8_t *w0;
+    size_t rb;
+    int nsb, total, rows_q, rows_r;
+    uint32_t magic;
+    int grid, nmat;
+};
+
 // The argument arrays, copied into registers once: indexing the kernel-argument struct with a
 // per-lane value would compile to vector loads of the argument segment, whose completion shares the
 // vmcnt counter with the weight stream and forces a full drain of the prefetched loads.
@@ -235,10 +249,10 @@ struct Mats {
     float *y[kMaxStreamMats];
     int end[kMaxStreamMats];
     int nmat;
-    __device__ explicit Mats(const MfmaArgs &a) : nmat(a.nmat) {
+    __device__ Mats(const MfmaArgs &a, const Lead &ld) : nmat(ld.nmat) {
 #pragma unroll
         for (int i = 0; i < kMaxStreamMats; ++i) {
-            w[i] = a.w[i];
+            w[i] = i ? a.w[i] : ld.w0;
             y[i] = a.y[i];
             end[i] = a.row_end[i];
         }
@@ -272,13 +286,17 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_
 // whole 16-byte units of its row (16-aligned rows of 8k super-blocks), so its ql and qh are read as
 // three aligned 16-byte pieces each.  ROUTED: the routed-expert forms (a.ids).
 template <int FMT, bool SWIGLU, int XR, bool WIDE = false, bool ROUTED = false>
-__global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const MfmaArgs a) {
+__global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const float *lx, const uint8_t *lw0, size_t lrb,
+                                                                       int lnsb, int ltotal, int lrows_q, int lrows_r,
+                                                                       uint32_t lmagic, int lgrid, int lnmat,
+                                                                       const MfmaArgs a) {
+    const Lead ld{lx, lw0, lrb, lnsb, ltotal, lrows_q, lrows_r, lmagic, lgrid, lnmat};
     constexpr int kWaves = waves_for(SWIGLU), kThreads = threads_for(SWIGLU);
     constexpr int NW = SWIGLU ? 2 : 1;  // matrices per output row (gate, up)
     constexpr int CE = Chunk<FMT>::elems, CB = Chunk<FMT>::bytes;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int XS = kSumElems<FMT>;
-    const int nsb = a.nsb, K = nsb * CE;
+    const int nsb = ld.nsb, K = nsb * CE;
     // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
     // per 32 elements, in no more LDS than the bf16 layout takes (3 KP + K/4 against 4 KX + K/8 bytes).
     // Q5_0 has only this form.
@@ -300,13 +318,13 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
 #if QLIN_MFMA_INTERLEAVE
     // 16-row tiles bid, bid + G, bid + 2G, ... (G workgroups): all workgroups sweep one region
     // (rows_q, rows_r here count tiles: tiles / G and tiles % G, from the host)
-    const int G = a.grid;
-    const int ntl = a.rows_q + (bid < a.rows_r ? 1 : 0);
-    const int nrows = ntl ? (ntl - 1) * 16 + min(16, a.total - 16 * (bid + (ntl - 1) * G)) : 0;
+    const int G = ld.grid;
+    const int ntl = ld.rows_q + (bid < ld.rows_r ? 1 : 0);
+    const int nrows = ntl ? (ntl - 1) * 16 + min(16, ld.total - 16 * (bid + (ntl - 1) * G)) : 0;
     auto grow = [&](int lr) { return 16 * (bid + (lr >> 4) * G) + (lr & 15); };  // global row of local row lr
 #else
-    const int rb = bid * a.rows_q + min(bid, a.rows_r);
-    const int nrows = a.rows_q + (bid < a.rows_r ? 1 : 0);
+    const int rb = bid * ld.rows_q + min(bid, ld.rows_r);
+    const int nrows = ld.rows_q + (bid < ld.rows_r ? 1 : 0);
     auto grow = [&](int lr) { return rb + lr; };
 #endif
     // The workgroup's work is the flat sequence of steps (16-row tile, matrix, super-block), which
@@ -315,7 +333,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     const int nsteps = (nrows + 15) / 16 * NW * nsb;
     const int n = lane & 15, g = lane >> 4;
     const ScaleDecoder dec(g);
-    const Mats mats(a);
+    const Mats mats(a, ld);
 
     // A-operand role of this lane: row i = n holds part (i & 1) of sub-block i >> 1, which is
     // carried by the slots of lane-group g only when (i >> 2) == g.
@@ -388,7 +406,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
         Pos p;
         p.s = s;
         const int c = min(s, nsteps - 1);
-        p.tw = nsb == 1 ? c : static_cast<int>(__umulhi(static_cast<uint32_t>(c), a.nsb_magic));
+        p.tw = nsb == 1 ? c : static_cast<int>(__umulhi(static_cast<uint32_t>(c), ld.magic));
         p.sb = c - p.tw * nsb;
         int tile, which;
         split_tw(p.tw, tile, which);
@@ -399,23 +417,23 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
             const int row = gr - r * a.route_rows;
             const int rs = r - (a.routes - a.sh_routes);  // >= 0: a block of the shared matrices
             const uint8_t *base =
-                rs >= 0 ? (which ? a.sh_w1 : a.sh_w0) + static_cast<size_t>(rs) * a.route_rows * a.row_bytes
+                rs >= 0 ? (which ? a.sh_w1 : a.sh_w0) + static_cast<size_t>(rs) * a.route_rows * ld.rb
                         : expert(which ? mats.w[1] : mats.w[0], r);
-            p.rp = base + static_cast<size_t>(row) * a.row_bytes + static_cast<size_t>(p.sb) * CB;
+            p.rp = base + static_cast<size_t>(row) * ld.rb + static_cast<size_t>(p.sb) * CB;
         } else if constexpr (ROUTED) {
             // chunk sb of the concatenated activations is chunk cl of route r (wave-uniform)
             const int r = route_of(p.sb, a.cpr, a.cpr_magic);
             const int cl = p.sb - r * a.cpr;
-            p.rp = expert(mats.w[0], r) + static_cast<size_t>(gr) * a.row_bytes + static_cast<size_t>(cl) * CB;
+            p.rp = expert(mats.w[0], r) + static_cast<size_t>(gr) * ld.rb + static_cast<size_t>(cl) * CB;
         } else if constexpr (SWIGLU) {
-            p.rp = (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * a.row_bytes +
+            p.rp = (which ? mats.w[1] : mats.w[0]) + static_cast<size_t>(gr) * ld.rb +
                    static_cast<size_t>(p.sb) * CB;
         } else {
             const uint8_t *wp;
             float *yp;
             int local;
             mats.locate(gr, wp, yp, local);
-            p.rp = wp + static_cast<size_t>(local) * a.row_bytes + static_cast<size_t>(p.sb) * CB;
+            p.rp = wp + static_cast<size_t>(local) * ld.rb + static_cast<size_t>(p.sb) * CB;
         }
         return p;
     };
@@ -487,7 +505,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const Mf
     // flight.
     float4 xv[XR];
 #pragma unroll
-    for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(a.x)[min(tid + r * kThreads, K / 4 - 1)];
+    for (int r = 0; r < XR; ++r) xv[r] = reinterpret_cast<const float4 *>(ld.x)[min(tid + r * kThreads, K / 4 - 1)];
     if (!ROUTED && a.norm_w) {  // uniform
         // the norm weights are requested with x; the sum of squares over the workgroup (each thread
         // its float4s in order, then the wave, then the waves in order)
@@ -1195,7 +1213,12 @@ hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStr
     a.rows_r = units % l.p.grid;
     a.nsb_magic = magic_of(a.nsb);
     a.grid = l.p.grid;
-    void *args[] = {&a};
+    const float *lx = a.x;
+    const uint8_t *lw0 = a.w[0];
+    size_t lrb = a.row_bytes;
+    int lnsb = a.nsb, ltotal = a.total, lrows_q = a.rows_q, lrows_r = a.rows_r, lgrid = a.grid, lnmat = a.nmat;
+    uint32_t lmagic = a.nsb_magic;
+    void *args[] = {&lx, &lw0, &lrb, &lnsb, &ltotal, &lrows_q, &lrows_r, &lmagic, &lgrid, &lnmat, &a};
     const hipError_t e = hipLaunchKernel(l.k.fn, dim3(l.p.grid), dim3(l.k.threads), args, l.p.lds, s);
     return e != hipSuccess ? e : hipGetLastError();
 }
