@@ -167,60 +167,78 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Wave maximum in register moves (every lane active, wave-uniform control flow): DPP within each
+// row of 16 lanes (quads, then the other quad of each 8, then the other 8), then the gfx950 lane
+// swaps between rows 2r and 2r + 1 and between the two halves of the wave.  Every lane gets the
+// maximum; fmaxf is exact, so the result is the same as any other order's.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_move<0xb1>(v));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_move<0x4e>(v));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);
+    // (the two results hold rows 0, 0, 2, 2 and 1, 1, 3, 3: their maximum is the row pair's)
+    v = fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(s16[0])),
+              __builtin_bit_cast(float, static_cast<uint32_t>(s16[1])));
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);
+    return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(s32[0])),
+                 __builtin_bit_cast(float, static_cast<uint32_t>(s32[1])));
+}
+
 // ---- router top-k of one token by one wave (at most 64 experts) --------------------------------
 // Lane e holds expert e's logit (non-finite as -inf).  Pick r is the expert with exactly r experts
 // ahead of it -- a larger logit, or an equal one at a lower index -- which is the order of k
-// successive argmaxes that prefer the lower index, the reference's strict-'>' first maximum.  Picks
-// past the finite logits fall back to expert r (0 past ne) with weight 0; a pick's weight is
+// successive argmaxes that prefer the lower index, the reference's strict-'>' first maximum; they are
+// taken here as k wave maxima, each pick the lowest lane holding the maximum, which then drops out.
+// Picks past the finite logits fall back to expert r (0 past ne) with weight 0; a pick's weight is
 // exp(l - max) / (the exponentials summed in expert order) times scaling.
-// Every wave of the workgroup calls this in step (it holds two workgroup barriers); only waves with
-// live set read logits (row of ne floats), use the LDS and put their picks, through
-// put(r, expert, weight).  sv, ex: 64 floats each, 16-byte aligned, and dn: one float, of LDS that no
-// other live wave uses (waves without live set touch none of it).
+// Wave-local: no workgroup barrier.  live is uniform per wave; only live waves read logits (row of ne
+// floats), use ex (64 floats, 16-byte aligned, of LDS that no other wave uses) and put their picks,
+// through put(r, expert, weight), called by one lane per pick.
 template <class Put>
-__device__ __forceinline__ void route_token_rank(bool live, const float *row, int ne, int k, float scaling, float *sv,
-                                                 float *ex, float *dn, Put put) {
+__device__ __forceinline__ void route_token_rank(bool live, const float *row, int ne, int k, float scaling, float *ex,
+                                                 Put put) {
+    if (!live) return;
     const int lane = threadIdx.x & 63;
-    const float l = live && lane < ne ? row[lane] : -INFINITY;
+    const float l = lane < ne ? row[lane] : -INFINITY;
     const float v = isfinite(l) ? l : -INFINITY;
-    const float maxv = wave_max(v);
-    if (live) {
-        sv[lane] = v;
-        ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;  // 0 for -inf and past ne
-    }
-    __syncthreads();
-    if (live && lane == 0) {
-        // in expert order; past ne the exponentials are 0 and leave the sum as it is
-        float denom = 0.0f;
-        if (isfinite(maxv)) {
-            float4 q[16];
+    const float maxv = wave_max_dpp(v);
+    ex[lane] = isfinite(maxv) ? expf(v - maxv) : 0.0f;  // 0 for -inf and past ne
+    // The wave's LDS accesses run in program order, so every lane reads all 64 values just written.
+    __builtin_amdgcn_wave_barrier();
+    // in expert order (every lane alike); past ne the exponentials are 0 and leave the sum as it is
+    float denom = 0.0f;
+    if (isfinite(maxv)) {
+        float4 q[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) q[i] = reinterpret_cast<const float4 *>(ex)[i];
+        for (int i = 0; i < 16; ++i) q[i] = reinterpret_cast<const float4 *>(ex)[i];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                denom += q[i].x;
-                denom += q[i].y;
-                denom += q[i].z;
-                denom += q[i].w;
-            }
-        }
-        *dn = denom;
-    }
-    int ahead = 0;  // past ne the logits are -inf, never ahead of a finite one
-    if (live) {
-#pragma unroll 4
-        for (int j = 0; j < 16; ++j) {
-            const float4 q = reinterpret_cast<const float4 *>(sv)[j];
-            ahead += (q.x > v || (q.x == v && 4 * j < lane)) + (q.y > v || (q.y == v && 4 * j + 1 < lane)) +
-                     (q.z > v || (q.z == v && 4 * j + 2 < lane)) + (q.w > v || (q.w == v && 4 * j + 3 < lane));
+        for (int i = 0; i < 16; ++i) {
+            denom += q[i].x;
+            denom += q[i].y;
+            denom += q[i].z;
+            denom += q[i].w;
         }
     }
-    __syncthreads();
-    const float denom = live ? *dn : 0.0f;
     const bool fin = v != -INFINITY;
     const int nf = static_cast<int>(__popcll(__ballot(fin)));
-    if (live && fin && ahead < k) put(ahead, lane, (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * scaling);
-    for (int r = nf + lane; live && r < k; r += 64) put(r, r < ne ? r : 0, 0.0f);
+    float cur = v;  // the finite logits not yet picked
+    const int kf = min(k, nf);
+    for (int r = 0; r < kf; ++r) {
+        const float m = wave_max_dpp(cur);  // finite: nf - r finite logits remain
+        const int p = static_cast<int>(__ffsll(static_cast<long long>(__ballot(cur == m)))) - 1;
+        if (lane == p) {
+            put(r, lane, (denom > 0.0f ? expf(v - maxv) / denom : 0.0f) * scaling);
+            cur = -INFINITY;
+        }
+    }
+    for (int r = nf + lane; r < k; r += 64) put(r, r < ne ? r : 0, 0.0f);
 }
 
 }  // namespace qlin

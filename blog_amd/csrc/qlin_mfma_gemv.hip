@@ -551,9 +551,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
         bool routed_here = false;
         if constexpr (SWIGLU) {
             if (a.logits) {  // uniform: wave 0 routes the token (the only live wave: its LDS alone)
-                __shared__ __attribute__((aligned(16))) float s_rv[64], s_rex[64];
-                __shared__ float s_rdn;
-                route_token_rank(wave == 0, a.logits, a.ne, a.routes - a.sh_routes, a.scaling, s_rv, s_rex, &s_rdn,
+                __shared__ __attribute__((aligned(16))) float s_rex[64];
+                route_token_rank(wave == 0, a.logits, a.ne, a.routes - a.sh_routes, a.scaling, s_rex,
                                  [&](int r, int e, float w) {
                                      s_ids[r] = e;
                                      if (blockIdx.x == 0) {

@@ -107,16 +107,14 @@ __global__ __launch_bounds__(64) void router_kernel(const float *__restrict__ lo
     }
 }
 
-// At most 64 experts, one wave per token (route_token_rank): the order of router_kernel's k successive
-// wave argmaxes, found in one pass of compares against the logits in LDS instead of k rounds of
-// cross-lane reductions; the weights and the fallback for picks past the finite logits are
-// router_kernel's.
+// At most 64 experts, one wave per token (route_token_rank): router_kernel's k successive wave
+// argmaxes on the logits held one per lane, with router_kernel's weights and fallback for picks past
+// the finite logits.
 __global__ __launch_bounds__(64) void router_rank_kernel(const float *__restrict__ logits, int *__restrict__ idx,
                                                          float *__restrict__ wout, int ne, int k, float scaling) {
-    __shared__ __attribute__((aligned(16))) float sv[64], ex[64];
-    __shared__ float dn;
+    __shared__ __attribute__((aligned(16))) float ex[64];
     const size_t t = blockIdx.x;
-    route_token_rank(true, logits + t * ne, ne, k, scaling, sv, ex, &dn, [&](int r, int e, float w) {
+    route_token_rank(true, logits + t * ne, ne, k, scaling, ex, [&](int r, int e, float w) {
         idx[t * k + r] = e;
         wout[t * k + r] = w;
     });

@@ -137,17 +137,21 @@ using plan::kXPad;
 //   Per block: sum x*w = d * (D - corr * X), X = sum of x (hi + lo) over the block, because the
 //   operand is bf16(128 + u) with u = q + 16 (Q5_0), or l / h (Q8_0: 128*17 + 128).
 template <int FMT> struct StepFmt;
-// w0, w1: relative cost of a 16-row tile per pass and per route (fitted to measured launch times
-// at 1 .. 4 routes per expert); the workgroups split the selected experts' tiles by this cost.
+// The workgroups split the selected experts' work by a cost: w0 per 16-row tile and pass, w1 per tile
+// and route, and ws per expert and pass (the workgroup that takes part of an expert stages its routes'
+// x and starts a new stream of steps).  Fitted to per-workgroup times within one launch of the C5
+// shape (16 tokens, top-6 of 64): a gate/up tile 1.27 us, a route on it 0.04 us, an expert 4.4 us; a
+// down tile 0.57 us, a route on it 0.07 us, an expert 3.8 us.  (Weights fitted earlier to whole-launch
+// times, (4, 1, 0) for gate/up, left the workgroups with one-route experts 40% longer than the rest.)
 template <> struct StepFmt<T_Q4_K> {
-    static constexpr int ce = 256, bb = 144, cb = 144, tpb = 0, w0 = 4, w1 = 1;
+    static constexpr int ce = 256, bb = 144, cb = 144, tpb = 0, w0 = 32, w1 = 1, ws = 112;
 };
 template <> struct StepFmt<T_Q5_0> {
-    static constexpr int ce = 128, bb = 22, cb = 88, nd = 5, tpb = 4, w0 = 8, w1 = 1;
+    static constexpr int ce = 128, bb = 22, cb = 88, nd = 5, tpb = 4, w0 = 8, w1 = 1, ws = 54;
     static constexpr float corr = 144.0f;
 };
 template <> struct StepFmt<T_Q8_0> {
-    static constexpr int ce = 128, bb = 34, cb = 136, nd = 8, tpb = 8, w0 = 8, w1 = 1;
+    static constexpr int ce = 128, bb = 34, cb = 136, nd = 8, tpb = 8, w0 = 8, w1 = 1, ws = 54;
     static constexpr float corr = 2304.0f;
 };
 
@@ -174,9 +178,8 @@ struct StreamArgs {
     int *ids_out;
     float *w_out;
 };
-// LDS of the in-kernel router, after the staged ids: per wave the 64 logits, their exponentials and
-// the denominator (132 floats, a multiple of 16 bytes)
-constexpr int kRouteWaveFloats = 132;
+// LDS of the in-kernel router, after the staged ids: per wave the 64 exponentials
+constexpr int kRouteWaveFloats = 64;
 
 // 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
 // shared by the 16 waves of a CU: both helpers take 32-bit arithmetic when the operands allow
@@ -202,10 +205,15 @@ __device__ __forceinline__ int64_t uni(int64_t v) {
                                 static_cast<uint32_t>(uni(static_cast<int>(u))));
 }
 
-// Cost of one 16-row tile of an expert with cnt routes: its passes and its routes.
+// Cost of one 16-row tile of an expert with cnt routes (its passes and its routes), and of the
+// expert's set-up per pass, which comes first in the expert's cost range.
 template <int FMT, int NQ>
 __device__ __forceinline__ int64_t tile_cost(int cnt) {
     return static_cast<int64_t>((cnt + NQ - 1) / NQ) * StepFmt<FMT>::w0 + static_cast<int64_t>(cnt) * StepFmt<FMT>::w1;
+}
+template <int FMT, int NQ>
+__device__ __forceinline__ int64_t setup_cost(int cnt) {
+    return static_cast<int64_t>((cnt + NQ - 1) / NQ) * StepFmt<FMT>::ws;
 }
 
 // SW: gate and up matrices with SiLU(gate) * up out (Q4_K); otherwise one matrix, its dot out.
@@ -258,11 +266,11 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
         if (a.logits) {  // uniform
             // router_rank_kernel's picks, one token per wave at a time (E <= 64: lane e holds expert e)
             const int k = a.x_div, T = R / k;
-            float *sv = reinterpret_cast<float *>(smem) + R16 + wave * kRouteWaveFloats, *ex = sv + 64, *dn = ex + 64;
+            float *ex = reinterpret_cast<float *>(smem) + R16 + wave * kRouteWaveFloats;
             for (int i = R + tid; i < R16; i += kSThreads) sids[i] = -1;
-            for (int t0 = 0; t0 < T; t0 += kSWaves) {  // the same trip count in every wave: barriers inside
+            for (int t0 = 0; t0 < T; t0 += kSWaves) {
                 const int t = t0 + wave;
-                route_token_rank(t < T, a.logits + static_cast<size_t>(t) * E, E, k, a.scaling, sv, ex, dn,
+                route_token_rank(t < T, a.logits + static_cast<size_t>(t) * E, E, k, a.scaling, ex,
                                  [&](int r, int e, float w) {
                                      const size_t o = static_cast<size_t>(t) * k + r;
                                      sids[o] = e;
@@ -271,8 +279,8 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                                          a.w_out[o] = w;
                                      }
                                  });
-                __syncthreads();  // this round's scratch is read; the next round rewrites it
             }
+            __syncthreads();  // the picks are in LDS
         } else {
             for (int i = tid; i < R16; i += kSThreads) sids[i] = i < R ? a.ids[i] : -1;
             __syncthreads();
@@ -353,10 +361,12 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     if (nsel == 0) return;  // uniform
 
     // Each workgroup takes an equal share of the total cost, in tiles: tile t of selected expert s
-    // starts at cost s_pref[s] + t * tile_cost and belongs to the workgroup whose range holds that.
+    // starts at cost s_pref[s] + setup_cost + t * tile_cost and belongs to the workgroup whose range
+    // holds that.
     {
+        const int cs = GRP ? (tid < nsel ? segs[tid].z : 0) : seg_cnt;
         const int64_t v =
-            tid < nsel ? static_cast<int64_t>(a.tpe) * tile_cost<FMT, NQ>(GRP ? segs[tid].z : seg_cnt) : 0;
+            tid < nsel ? setup_cost<FMT, NQ>(cs) + static_cast<int64_t>(a.tpe) * tile_cost<FMT, NQ>(cs) : 0;
         int64_t inc = v;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
@@ -421,10 +431,10 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     };
 
     for (int s = uni(s_first); s < nsel; ++s) {
-        const int64_t ps = uni(s_pref[s]);
-        if (ps >= c1) break;
+        if (uni(s_pref[s]) >= c1) break;
         const int4 sg = segs[s];
         const int e = uni(sg.x), beg = uni(sg.y), cnt = uni(sg.z);
+        const int64_t ps = uni(s_pref[s]) + setup_cost<FMT, NQ>(cnt);  // where the expert's tiles start
         const int64_t ct = tile_cost<FMT, NQ>(cnt);
         const int lt0 = static_cast<int>(max(ceil_div(c0 - ps, ct), int64_t{0}));
         const int lt1 = static_cast<int>(min(ceil_div(c1 - ps, ct), static_cast<int64_t>(a.tpe)));
