@@ -104,6 +104,11 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 #ifndef QLIN_MFMA_LONG_DEPTH
 #define QLIN_MFMA_LONG_DEPTH 1
 #endif
+// Equal rows per workgroup where whole tiles would leave some with one tile more (1), or whole
+// tiles only (0)
+#ifndef QLIN_MFMA_EVEN
+#define QLIN_MFMA_EVEN 1
+#endif
 // Workgroup b of G takes 16-row tiles b, b + G, b + 2G, ... (1), so that all workgroups sweep one
 // region of the weights together, rather than a contiguous slice each (0): 1.6% faster over the
 // decode step (gate/up and lm_head, the launches with several tiles per workgroup).
@@ -317,11 +322,20 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     const int bid = blockIdx.x;
 #if QLIN_MFMA_INTERLEAVE
     // 16-row tiles bid, bid + G, bid + 2G, ... (G workgroups): all workgroups sweep one region
-    // (rows_q, rows_r here count tiles: tiles / G and tiles % G, from the host)
+    // (rows_q, rows_r here count tiles: tiles / G and tiles % G, from the host).  rows_r < 0: every
+    // workgroup takes rows_q such tiles and then -rows_r consecutive rows of the rows past them
+    // (workgroup b from row 16 rows_q G + b (-rows_r)), a last tile with fewer than 16 rows: equal
+    // bytes in every workgroup, where whole tiles leave some workgroups with one tile more.
     const int G = ld.grid;
-    const int ntl = ld.rows_q + (bid < ld.rows_r ? 1 : 0);
-    const int nrows = ntl ? (ntl - 1) * 16 + min(16, ld.total - 16 * (bid + (ntl - 1) * G)) : 0;
-    auto grow = [&](int lr) { return 16 * (bid + (lr >> 4) * G) + (lr & 15); };  // global row of local row lr
+    const bool even = ld.rows_r < 0;  // uniform
+    const int ntl = even ? ld.rows_q + 1 : ld.rows_q + (bid < ld.rows_r ? 1 : 0);
+    const int nrows = even  ? 16 * ld.rows_q - ld.rows_r
+                      : ntl ? (ntl - 1) * 16 + min(16, ld.total - 16 * (bid + (ntl - 1) * G))
+                            : 0;
+    const int tail0 = 16 * ld.rows_q * (G - 1) - ld.rows_r * bid;  // global row of local row lr in the last tile: tail0 + lr
+    auto grow = [&](int lr) {  // global row of local row lr
+        return even && lr >= 16 * ld.rows_q ? tail0 + lr : 16 * (bid + (lr >> 4) * G) + (lr & 15);
+    };
 #else
     const int rb = bid * ld.rows_q + min(bid, ld.rows_r);
     const int nrows = ld.rows_q + (bid < ld.rows_r ? 1 : 0);
@@ -1210,6 +1224,15 @@ hipError_t launch(int type, MfmaArgs &a, int k, bool swiglu, bool routed, hipStr
     const int units = QLIN_MFMA_INTERLEAVE ? (a.total + 15) / 16 : a.total;  // tiles or rows per workgroup
     a.rows_q = units / l.p.grid;
     a.rows_r = units % l.p.grid;
+    // Plain launches with at least two whole tiles per workgroup and a remainder that splits evenly
+    // take whole tiles and an equal share of the rest of the rows (the kernel's rows_r < 0): the
+    // Qwen2-7B gate/up pair's 1184 tiles left 160 workgroups with 5 tiles and 96 with 4; now each has
+    // 4 and 10 rows.
+    const int whole = a.total / (16 * l.p.grid), rest = a.total - 16 * whole * l.p.grid;
+    if (QLIN_MFMA_INTERLEAVE && QLIN_MFMA_EVEN && !routed && whole >= 2 && rest > 0 && rest % l.p.grid == 0) {
+        a.rows_q = whole;
+        a.rows_r = -(rest / l.p.grid);
+    }
     a.nsb_magic = magic_of(a.nsb);
     a.grid = l.p.grid;
     const float *lx = a.x;
