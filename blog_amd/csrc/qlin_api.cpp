@@ -956,12 +956,17 @@ int qlin_moe_ffn_decode_grouped_logits(int gu_type, const uint8_t *gate, const u
         const size_t d_rb = d_eb / static_cast<size_t>(hidden);
         const qlin::MoeRouter router{router_logits, routed_scaling, ids, rw};
         qlin::RouteCombine routed{};
+        // the shared SwiGLU rides in the routed gate/up launch when that launch can take it
+        bool shared_done = false;
+        const qlin::SharedUp sh{shared_gate, shared_up, shared_gate_up_rb, sact, shared_ffn, &shared_done};
+        const bool sh_ok = shared_type == QLIN_TYPE_Q4_K && in_dim % 256 == 0 &&
+                           qlin::dense_ok(shared_type, shared_gate, shared_up, shared_gate_up_rb, x, in_dim);
         hipError_t e = qlin::moe_grouped(gu_type, gate, up, g_eb, g_rb, down_type, down, d_eb, d_rb, n_experts, ffn_dim,
                                          in_dim, hidden, x, nullptr, nullptr, workspace, out, tokens, k, stream(),
-                                         &router, &routed);
+                                         &router, &routed, sh_ok ? &sh : nullptr);
         if (e != hipSuccess) return launched(e);
-        if ((rc = qlin_launch_quant_swiglu_rows(shared_type, shared_gate, shared_up, shared_gate_up_rb,
-                                                shared_gate_up_rb, x, sact, shared_ffn, in_dim, tokens)))
+        if (!shared_done && (rc = qlin_launch_quant_swiglu_rows(shared_type, shared_gate, shared_up, shared_gate_up_rb,
+                                                                shared_gate_up_rb, x, sact, shared_ffn, in_dim, tokens)))
             return rc;
         return launched(qlin::dense_matmul(shared_type, shared_down, nullptr, shared_down_rb, sact, out, hidden,
                                            shared_ffn, tokens, 1, stream(), &routed));

@@ -5,14 +5,11 @@
 //   act[r, o] = g / (1 + expf(-g)) * u,  g, u the rows of the gate and up matrices
 //                                               (the gemm, gemm, silu_mul of SharedExperts.cpp:34-40)
 //
-// Q4_K (the shared experts) on v_mfma_f32_16x16x32_bf16 with the tokens as the MFMA rows.  The
-// element value of sub-block j is w = dsc*q - dm (dsc = d*sc_j, dm = dmin*m_j, kernel.cu:913-930), so
-//   sum_k w x = dsc * sum x (128 + q) - (128 dsc + dm) * sum x
-// where the nibble q enters as the exact bf16 128 + q (one v_perm_b32 per two weights) and x as the
-// bf16 pair hi = bf16(x), lo = bf16(x - hi): every product is exact and accumulates in f32.  Per
-// sub-block and 16-token tile one MFMA pair gives sum x (128 + q) for 16 weight rows, and one more
-// pair against an all-ones B gives sum x (in the same D layout); the scales are applied by two fmas
-// per output.  The other formats multiply the canonical f32 element values (decoded as the
+// Q4_K (the shared experts) on v_mfma_f32_16x16x32_bf16 with the tokens as the MFMA rows
+// (q4k_rows_dot, qlin_rows.hpp): the nibble q enters as the exact bf16 128 + q and x as the bf16 pair
+// hi = bf16(x), lo = bf16(x - hi), so every product is exact and accumulates in f32; per sub-block
+// and 16-token tile one MFMA pair gives sum x (128 + q) for 16 weight rows and another pair sum x,
+// and two fmas per output apply the scales.  The other formats multiply the canonical f32 element values (decoded as the
 // reference decodes them) on v_mfma_f32_16x16x4_f32: the contraction the reference runs one warp
 // per (r, o), with the same f32 operands and only the summation order changed.
 //
@@ -24,13 +21,11 @@
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
+#include "qlin_rows.hpp"
 
 namespace qlin {
 namespace {
 
-#ifndef QLIN_DENSE_XFIRST
-#define QLIN_DENSE_XFIRST 1
-#endif
 constexpr int kDWaves = 8, kDThreads = kDWaves * 64;
 constexpr int kDTokens = 64;  // tokens per grid row (4 tiles of 16)
 
@@ -83,24 +78,6 @@ __device__ __forceinline__ void add_out(const DenseArgs &a, float *yo, int t, in
     *yo = y + v;
 }
 
-// The raw bytes a lane needs of one Q4_K super-block: the header (d, dmin, 12 scale bytes) and,
-// for each pair c of sub-blocks, qs bytes 32c + 8g .. 32c + 8g + 7 (low nibbles: sub-block 2c,
-// high nibbles: sub-block 2c + 1).
-struct Q4KRaw {
-    u32x4 h;
-    uint32_t q[8];
-};
-
-__device__ __forceinline__ void load_q4k(Q4KRaw &r, const uint8_t *sb, int g) {
-    r.h = ld16(sb);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(sb + 16 + 32 * c + 8 * g);
-        r.q[2 * c] = v.x;
-        r.q[2 * c + 1] = v.y;
-    }
-}
-
 template <int MODE>
 __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a) {
     constexpr int NW = MODE == kSwiGLU ? 2 : 1;
@@ -115,7 +92,6 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
     const int ntt = min(4, (a.m - t0 + 15) / 16);  // token tiles of this grid row
     const uint8_t *rp[2] = {a.w0 + static_cast<size_t>(row) * a.rb, a.w1 + static_cast<size_t>(row) * a.rb};
 
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0 in every slot
     // one 16-token tile at a time (a tile's weights come again from the cache for the next one)
     for (int tt = 0; tt < ntt; ++tt) {
         // token of this lane's A row (tokens past m read the last one; their D rows are dropped)
@@ -124,77 +100,8 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
         f32x4 D[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) D[w] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        // wave w takes super-blocks w, w + 8, ...; the next one's weights are requested before the
-        // current one's math
-        Q4KRaw cur[NW];
-        int sb = wave;
-        if (sb < nsb) {
-#pragma unroll
-            for (int w = 0; w < NW; ++w) load_q4k(cur[w], rp[w] + static_cast<size_t>(sb) * 144, g);
-        }
-        while (sb < nsb) {  // uniform
-#if QLIN_DENSE_XFIRST
-            // the super-block's x first, then the next weights: a wait for x then never waits for
-            // the weight prefetch (the memory counter completes in issue order), and the 16 loads
-            // share one round trip instead of one per few sub-blocks
-            const float *xr = xrow + sb * 256;
-            float4 xs[16];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                xs[2 * j] = *reinterpret_cast<const float4 *>(xr + 32 * j);
-                xs[2 * j + 1] = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#endif
-            const int sb2 = sb + kDWaves;
-            Q4KRaw nxt[NW];
-            if (sb2 < nsb) {  // uniform
-#pragma unroll
-                for (int w = 0; w < NW; ++w) load_q4k(nxt[w], rp[w] + static_cast<size_t>(sb2) * 144, g);
-            }
-#if QLIN_DENSE_XFIRST
-            __builtin_amdgcn_sched_barrier(0);
-#else
-            const float *xr = xrow + sb * 256;
-#endif
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-#if QLIN_DENSE_XFIRST
-                const float4 x0 = xs[2 * j], x1 = xs[2 * j + 1];
-#else
-                const float4 x0 = *reinterpret_cast<const float4 *>(xr + 32 * j);
-                const float4 x1 = *reinterpret_cast<const float4 *>(xr + 32 * j + 4);
-#endif
-                uint32_t h[4], l[4];
-                split_bf16x2(x0.x, x0.y, h[0], l[0]);
-                split_bf16x2(x0.z, x0.w, h[1], l[1]);
-                split_bf16x2(x1.x, x1.y, h[2], l[2]);
-                split_bf16x2(x1.z, x1.w, h[3], l[3]);
-                const u32x4 ahi = {h[0], h[1], h[2], h[3]}, alo = {l[0], l[1], l[2], l[3]};
-                const f32x4 X = mfma(alo, ones, mfma(ahi, ones, f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
-#pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    // this lane's row: dsc and the coefficient of sum x for sub-block j
-                    int sc, mn;
-                    q4k_scale_min(j, cur[w].h.y, cur[w].h.z, cur[w].h.w, sc, mn);
-                    const float dsc = mul_rn(f16_bits_to_f32(cur[w].h.x & 0xffffu), static_cast<float>(sc));
-                    const float cx =
-                        -(128.0f * dsc + mul_rn(f16_bits_to_f32(cur[w].h.x >> 16), static_cast<float>(mn)));
-                    // elements 8g .. 8g+7 of sub-block j: the low (j even) or high nibbles of the
-                    // lane's bytes of sub-block pair j / 2
-                    const int sh = 4 * (j & 1);
-                    const u32x4 B = weights_operand2((cur[w].q[2 * (j >> 1)] >> sh) & 0x0f0f0f0fu,
-                                                     (cur[w].q[2 * (j >> 1) + 1] >> sh) & 0x0f0f0f0fu);
-                    const f32x4 Dj = mfma(alo, B, mfma(ahi, B, f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) D[w][r] = fmaf(cx, X[r], fmaf(dsc, Dj[r], D[w][r]));
-                }
-            }
-            if (sb2 >= nsb) break;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) cur[w] = nxt[w];
-            sb = sb2;
-        }
+        // wave w takes super-blocks w, w + 8, ...
+        q4k_rows_dot<NW>(rp, xrow, wave, kDWaves, nsb, g, D);
 #pragma unroll
         for (int w = 0; w < NW; ++w) part[wave][w][tt][lane] = D[w];
     }

@@ -195,11 +195,21 @@ bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t ex
 // router non-null: ids and rw are ignored, the routes are router_topk's of the logits (inside the gate/up
 // launch for n_experts <= 64 when its LDS allows, else one router launch first).  defer non-null: out is
 // not touched; the combine is left to the caller, whose launch applies *defer (filled here).
+// The shared experts' SwiGLU over the batch, handed to the batched MoE decode's gate/up launch:
+// act [tokens, rows] = SiLU(wg x) * (wu x) for Q4_K gate and up matrices of row stride rb (K = the
+// routed in_dim), as q4k_dense_kernel computes it.  moe_grouped sets *done when its launch took it.
+struct SharedUp {
+    const uint8_t *wg, *wu;
+    size_t rb;
+    float *act;
+    int rows;
+    bool *done;
+};
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int n_experts, int ffn_dim, int in_dim,
                        int hidden, const float *x, const int *ids, const float *rw, void *workspace, float *out,
                        int tokens, int k, hipStream_t s, const MoeRouter *router = nullptr,
-                       RouteCombine *defer = nullptr);
+                       RouteCombine *defer = nullptr, const SharedUp *shared = nullptr);
 
 // Quantized embedding rows and the MLA latent-absorption products over kv_b (qlin_embed_mla.hip).
 hipError_t quant_embedding(int type, const int *ids, float *out, const uint8_t *table, size_t row_bytes, int hidden,

@@ -20,6 +20,7 @@
 #include "qlin_internal.hpp"
 #include "qlin_mfma.hpp"
 #include "qlin_plan.hpp"
+#include "qlin_rows.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -177,9 +178,21 @@ struct StreamArgs {
     float scaling;
     int *ids_out;
     float *w_out;
+    // SW: the shared experts' SwiGLU in the same launch (sh_rows > 0): workgroup b computes 16-row tile b
+    // of the shared gate and up matrices for the sh_tokens (<= 16) rows of x before its routed share,
+    // into sh_act [sh_tokens, sh_rows], and its routed share is smaller by sh_cost.
+    const uint8_t *sh_wg, *sh_wu;
+    size_t sh_rb;
+    float *sh_act;
+    int sh_rows, sh_tokens, sh_cost;
 };
 // LDS of the in-kernel router, after the staged ids: per wave the 64 exponentials
 constexpr int kRouteWaveFloats = 64;
+// A shared-expert tile in the gate/up launch: its partials (8 super-block slots x 2 matrices x 64
+// lanes of 4 floats) in the dynamic LDS, and its cost in the units of StepFmt<T_Q4_K> (11.6 us of a
+// workgroup's time at 16 tokens in a per-workgroup trace, at 0.04 us per unit)
+constexpr size_t kSharedPartBytes = 8 * 2 * 64 * 16;
+constexpr int kSharedTileCost = 288;
 
 // 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
 // shared by the 16 waves of a CU: both helpers take 32-bit arithmetic when the operands allow
@@ -250,6 +263,36 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     if (tid < 8) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);  // before the barriers below
+
+    // The shared experts' SwiGLU tile of this workgroup, first (it depends on no routing): wave w takes
+    // matrix w & 1 and super-blocks w / 2, w / 2 + 8, ..., the wave and order q4k_dense_kernel's wave
+    // w / 2 gives that matrix, and the 8 waves' sums of a matrix are added in wave order as there: the
+    // same bits as the separate launch.  The partials use the (still unused) staging area.
+    const int n_shared = SW && a.sh_rows > 0 ? (a.sh_rows + 15) / 16 : 0;
+    if constexpr (SW) {
+        if (blockIdx.x < n_shared) {  // uniform
+            const int row0 = blockIdx.x * 16, m = wave & 1, slot = wave >> 1;
+            const uint8_t *rp = (m ? a.sh_wu : a.sh_wg) + static_cast<size_t>(min(row0 + n, a.sh_rows - 1)) * a.sh_rb;
+            const float *xrow = a.x + static_cast<size_t>(min(n, a.sh_tokens - 1)) * a.K + 8 * g;
+            f32x4 D[1] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+            q4k_rows_dot<1>(&rp, xrow, slot, 8, a.K / 256, g, D);
+            f32x4 *part = reinterpret_cast<f32x4 *>(smem);  // [slot][matrix][lane]
+            part[(slot * 2 + m) * 64 + lane] = D[0];
+            __syncthreads();
+            // outputs: token tid / 16, row row0 + tid % 16; D element r of lane l is token 4 (l / 16) + r
+            const int tl = tid >> 4, o = tid & 15;
+            if (tid < 256 && tl < a.sh_tokens && o < min(16, a.sh_rows - row0)) {
+                const int l = (tl >> 2) * 16 + o, r = tl & 3;
+                float v0 = 0.0f, v1 = 0.0f;
+                for (int wv = 0; wv < 8; ++wv) {
+                    v0 += part[(wv * 2) * 64 + l][r];
+                    v1 += part[(wv * 2 + 1) * 64 + l][r];
+                }
+                a.sh_act[static_cast<size_t>(tl) * a.sh_rows + row0 + o] = v0 / (1.0f + expf(-v0)) * v1;
+            }
+            __syncthreads();  // the staging area is free again
+        }
+    }
 
     // GRP: the routes grouped by expert here, as group_kernel does (a stable counting sort, invalid
     // ids left out), into LDS: one launch and two dependent reads (the count, then the records) fewer
@@ -386,7 +429,14 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     }
     const int64_t C = uni(s_pref[nsel]);
     const int bid = blockIdx.x, nwg = gridDim.x;
-    const int64_t c0 = share_bound(C, bid, nwg), c1 = share_bound(C, bid + 1, nwg);
+    // With the shared tiles, workgroup b's range is its equal share of the routed cost plus the shared
+    // tiles' cost, less the cost of the shared tiles it took: ranges then stay ordered and cover [0, C)
+    // as long as an equal share is at least one tile's cost (else the tiles are left out of the split).
+    int64_t us = n_shared ? static_cast<int64_t>(a.sh_cost) : 0;
+    if (us > 0 && (C + us * n_shared) / nwg < us) us = 0;
+    const int64_t Ct = C + us * n_shared;
+    const int64_t c0 = share_bound(Ct, bid, nwg) - us * min(bid, n_shared);
+    const int64_t c1 = share_bound(Ct, bid + 1, nwg) - us * min(bid + 1, n_shared);
     if (c0 >= c1) return;  // uniform
     int s_first = 0;
     for (int hi = nsel - 1; s_first < hi;) {  // first expert whose range ends after c0
@@ -1013,7 +1063,7 @@ bool moe_grouped_up_ok(int type, const uint8_t *wg, const uint8_t *wu, size_t eb
 hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t g_eb, size_t g_rb, int d_type,
                        const uint8_t *wd, size_t d_eb, size_t d_rb, int E, int ffn, int K, int hidden,
                        const float *x, const int *ids, const float *rw, void *ws, float *out, int tokens, int k,
-                       hipStream_t s, const MoeRouter *router, RouteCombine *defer) {
+                       hipStream_t s, const MoeRouter *router, RouteCombine *defer, const SharedUp *shared) {
     (void)gu_type;  // Q4_K (moe_grouped_up_ok)
     const int R = tokens * k;
     if (R == 0 || hidden == 0) return hipSuccess;
@@ -1064,6 +1114,20 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
             ua.scaling = router->scaling;
             ua.ids_out = router->ids;
             ua.w_out = router->w;
+        }
+        // the shared experts' SwiGLU as the first tile of workgroups 0 .. (one 16-token tile, one
+        // shared tile per workgroup at most, its partials in the dynamic LDS)
+        const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+        if (shared && shared->rows > 0 && tokens <= 16 && (shared->rows + 15) / 16 <= up.grid &&
+            shared->rb % 16 == 0 && al16(shared->wg) && al16(shared->wu) && up.lds >= kSharedPartBytes) {
+            ua.sh_wg = shared->wg;
+            ua.sh_wu = shared->wu;
+            ua.sh_rb = shared->rb;
+            ua.sh_act = shared->act;
+            ua.sh_rows = shared->rows;
+            ua.sh_tokens = tokens;
+            ua.sh_cost = kSharedTileCost;
+            if (shared->done) *shared->done = true;
         }
         const hipError_t e = grp ? launch_stream<T_Q4_K, true, true>(up, ua, s) : launch_stream<T_Q4_K, true>(up, ua, s);
         if (e != hipSuccess) return e;
