@@ -763,8 +763,8 @@ def wl_c5(args, torch, qlin, gen):
 
     def step_grouped():
         for wg, wu, wd, sg, su, sd in mats:
-            # the whole FFN in one call: the routing runs in the routed gate/up launch, and the shared
-            # down-add launch also adds the routed sum (no combine launch)
+            # the whole FFN in one call: the routing and the shared SwiGLU run in the routed gate/up launch,
+            # and the shared down-add launch also adds the routed sum (no combine launch)
             qlin.call("qlin_moe_ffn_decode_grouped_logits", Q4_K, wg, wu, gub, Q5_0, wd, db, E, ffn, hid, hid, Q4_K, sg,
                       su, s_rb, sd, sd_rb, sffn, x, logits, 1.0, ids, rw, wsp, nws, out, tokens, k)
 
@@ -801,15 +801,15 @@ def wl_c5(args, torch, qlin, gen):
         "config": {"workload": "c5-moe-grouped", "experts": E, "ffn": ffn, "hidden": hid, "tokens": tokens,
                    "top_k": k, "gate_up": "Q4_K", "down": "Q5_0", "shared_ffn": sffn, "shared": "Q4_K",
                    "distinct_experts": distinct, "algorithmic_bytes_per_step": nbytes,
-                   "launches_per_step": "moe_ffn_decode_grouped_logits: stream gate/up with the routing and "
-                                        "grouping, stream down, shared SwiGLU, shared down-add with the "
-                                        "routed combine (4 launches)",
+                   "launches_per_step": "moe_ffn_decode_grouped_logits: stream gate/up with the routing, the "
+                                        "grouping and the shared SwiGLU tiles, stream down, shared down-add with "
+                                        "the routed combine (3 launches)",
                    "three_calls_us_per_step": round(us_three, 2),
                    "per_token_facade_us_per_step": round(us_tok, 2), "execution": "hip graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(nbytes / us / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "whole step (stream_kernel<Q4_K> gate/up with the router and the grouping, "
-                               "stream_kernel<Q5_0> down, q4k_dense_kernel SwiGLU, q4k_dense_kernel add with "
+                     "kernel": "whole step (stream_kernel<Q4_K> gate/up with the router, the grouping and "
+                               "the shared SwiGLU tiles, stream_kernel<Q5_0> down, q4k_dense_kernel add with "
                                "the routed combine)",
                      "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": nbytes},
     }
