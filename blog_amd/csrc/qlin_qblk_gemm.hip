@@ -28,6 +28,8 @@
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 
+#include <type_traits>
+
 namespace qlin {
 namespace {
 
@@ -35,20 +37,30 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kNT = 2;                    // 16-row weight tiles per wave
-constexpr int kBN = kWaves * kNT * 16;    // weight rows per workgroup (256)
-constexpr int kMT = 4;                    // 16-token tiles per workgroup
-constexpr int kBM = kMT * 16;             // tokens per workgroup (64)
-// One LDS buffer (uint4 units): the qx plane [mt][j][lane] (fp16 integers), then the block scales
-// d8 [mt][j][token] as floats.  Two buffers: 68 KB.
-constexpr int kPlane = kMT * 8 * 64;
-constexpr int kD8 = kMT * 8 * 16 / 4;
-constexpr int kBuf = kPlane + kD8;
-constexpr size_t kLdsBytes = 2 * kBuf * sizeof(uint4);
-constexpr int kSJ = kThreads / kMT / 64;  // staging waves per token tile
-constexpr int kJJ = 8 / kSJ;              // blocks each staging thread converts
+#ifndef QLIN_QBLK_SMALL
+#define QLIN_QBLK_SMALL 1  // the 4-wave, 32-token geometry for launches that would leave half the CUs idle
+#endif
+constexpr int kNT = 2;  // 16-row weight tiles per wave
+// A workgroup's geometry: W waves of 32 rows each, MT 16-token tiles.  The default (8 waves, 64 tokens:
+// 256 rows) covers large grids; a launch that would leave more than half the CUs idle takes 4 waves and
+// 32 tokens (128 rows), four times as many workgroups for the same work per output.
+template <int W, int MT>
+struct Geo {
+    static constexpr int kWaves = W, kThreads = W * 64;
+    static constexpr int kBN = W * kNT * 16;  // weight rows per workgroup
+    static constexpr int kMT = MT, kBM = MT * 16;  // 16-token tiles and tokens per workgroup
+    // One LDS buffer (uint4 units): the qx plane [mt][j][lane] (fp16 integers), then the block scales
+    // d8 [mt][j][token] as floats.  Two buffers (68 KB for the default).
+    static constexpr int kPlane = MT * 8 * 64;
+    static constexpr int kD8 = MT * 8 * 16 / 4;
+    static constexpr int kBuf = kPlane + kD8;
+    static constexpr size_t kLdsBytes = 2 * kBuf * sizeof(uint4);
+    static constexpr int kSJ = kThreads / MT / 64;  // staging waves per token tile
+    static constexpr int kJJ = 8 / kSJ;             // blocks each staging thread converts
+    static_assert(kSJ >= 1 && 8 % kSJ == 0, "whole waves stage whole token tiles");
+};
+using GeoLarge = Geo<8, 4>;
+using GeoSmall = Geo<4, 2>;
 
 template <int FMT> struct QBlk;
 template <> struct QBlk<T_Q8_0> {
@@ -179,7 +191,9 @@ template <int V> using ic = std::integral_constant<int, V>;
 // blocks past the row are zeros.  Thread roles: token tile smt, slot lane sl (token si, k-group sg),
 // blocks kJJ*sjh .. +kJJ-1 of the unit.  Tokens past m repeat the last row (their D rows are never
 // stored).
+template <class G>
 struct ActStage {
+    static constexpr int kSJ = G::kSJ, kJJ = G::kJJ, kBuf = G::kBuf, kPlane = G::kPlane;
     uint4 *lds;
     const uint8_t *xrow;
     int smt, sjh, sl, si, sg, nblk, nunit;
@@ -226,15 +240,17 @@ struct ActStage {
 };
 
 // A fragments of block J: qx of every token tile, and d8 of the lane's 4 tokens
+template <int MT>
 struct Frag {
-    uint4 a[kMT];
-    float4 d8[kMT];
+    uint4 a[MT];
+    float4 d8[MT];
 };
-__device__ __forceinline__ void load_frag(Frag &f, const ActStage &st, int buf, int J, int lane) {
+template <class G>
+__device__ __forceinline__ void load_frag(Frag<G::kMT> &f, const ActStage<G> &st, int buf, int J, int lane) {
     const uint4 *pl = st.plane(buf);
     const float *d8 = st.d8s(buf);
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) {
+    for (int i = 0; i < G::kMT; ++i) {
         f.a[i] = pl[(i * 8 + J) * 64 + lane];
         f.d8[i] = *reinterpret_cast<const float4 *>(d8 + (i * 8 + J) * 16 + 4 * (lane >> 4));
     }
@@ -243,13 +259,19 @@ __device__ __forceinline__ void load_frag(Frag &f, const ActStage &st, int buf, 
 // The block's scaling is pure arithmetic, which instruction selection would otherwise sink below
 // every later block, keeping all of a unit's MFMA results live (spills); consuming the sums pins it
 // before the next block's MFMAs.
-__device__ __forceinline__ void pin(f32x4 (&T)[kMT][kNT]) {
-    static_assert(kMT * kNT == 8, "one operand per sum");
-    asm volatile("" ::"v"(T[0][0]), "v"(T[0][1]), "v"(T[1][0]), "v"(T[1][1]), "v"(T[2][0]), "v"(T[2][1]), "v"(T[3][0]),
-                 "v"(T[3][1]));
+template <int MT>
+__device__ __forceinline__ void pin(f32x4 (&T)[MT][kNT]) {
+    if constexpr (MT == 4) {
+        asm volatile("" ::"v"(T[0][0]), "v"(T[0][1]), "v"(T[1][0]), "v"(T[1][1]), "v"(T[2][0]), "v"(T[2][1]),
+                     "v"(T[3][0]), "v"(T[3][1]));
+    } else {
+        static_assert(MT == 2, "the geometries' token tiles");
+        asm volatile("" ::"v"(T[0][0]), "v"(T[0][1]), "v"(T[1][0]), "v"(T[1][1]));
+    }
 }
 
 // lane (g, n) holds tokens 4g .. 4g+3 of each 16-token tile, weight row n of each 16-row tile
+template <int kMT>
 __device__ __forceinline__ void store_tile(const GemmArgs &a, const f32x4 (&acc)[kMT][kNT], int o0, int m0, int n,
                                            int g) {
 #pragma unroll
@@ -266,8 +288,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs &a, const f32x4 (&acc)
     }
 }
 
-template <int FMT>
-__global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
+template <int FMT, class G>
+__global__ __launch_bounds__(G::kThreads) void qblk_gemm_kernel(const GemmArgs a) {
+    constexpr int kMT = G::kMT, kBN = G::kBN, kBM = G::kBM;
+    using ActStage = qlin::ActStage<G>;
+    using Frag = qlin::Frag<kMT>;
     constexpr int BB = QBlk<FMT>::bytes;
     extern __shared__ uint4 lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -353,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void qblk_gemm_kernel(const GemmArgs a) {
     // block by block; then u + 1's activations (loaded during u) are staged into the other buffer,
     // whose last reads were before the previous barrier, and u + 2's requested.
     WRaw w;
-    ActStage::Raw x;
+    typename ActStage::Raw x;
     fetch_blk(ic<0>{}, w, 0);
     fetch_blk(ic<1>{}, w, 0);
     fetch_blk(ic<2>{}, w, 0);
@@ -404,7 +429,11 @@ __device__ __forceinline__ uint2 piece(const uint32_t (&w)[3], int off) {
     return make_uint2(__builtin_amdgcn_alignbyte(w[1], w[0], off), __builtin_amdgcn_alignbyte(w[2], w[1], off));
 }
 
-__global__ __launch_bounds__(kThreads) void q6k_gemm_kernel(const GemmArgs a) {
+template <class G>
+__global__ __launch_bounds__(G::kThreads) void q6k_gemm_kernel(const GemmArgs a) {
+    constexpr int kMT = G::kMT, kBN = G::kBN, kBM = G::kBM;
+    using ActStage = qlin::ActStage<G>;
+    using Frag = qlin::Frag<kMT>;
     extern __shared__ uint4 lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4, gb = g >> 1;
@@ -525,7 +554,7 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_kernel(const GemmArgs a) {
     };
 
     WRaw w;
-    ActStage::Raw x;
+    typename ActStage::Raw x;
     fetch_sd(w, 0);
     fetch_half(w, 0, 0);
     fetch_half(w, 0, 1);
@@ -566,15 +595,31 @@ hipError_t qblk_gemm_q8_1(int type, const uint8_t *w, size_t rb, const uint8_t *
     a.n = out_dim;
     a.m = m;
     a.nblk = in_dim / 32;
-    const dim3 grid = gemm_grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    switch (type) {
-        case T_Q8_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q8_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
-        case T_Q5_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q5_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
-        case T_Q4_0: hipLaunchKernelGGL(qblk_gemm_kernel<T_Q4_0>, grid, dim3(kThreads), kLdsBytes, s, a); break;
-        case T_Q6_K: hipLaunchKernelGGL(q6k_gemm_kernel, grid, dim3(kThreads), kLdsBytes, s, a); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    auto launch = [&](auto geo) {
+        using G = decltype(geo);
+        const dim3 grid = gemm_grid((out_dim + G::kBN - 1) / G::kBN, (m + G::kBM - 1) / G::kBM);
+        switch (type) {
+            case T_Q8_0: hipLaunchKernelGGL((qblk_gemm_kernel<T_Q8_0, G>), grid, dim3(G::kThreads), G::kLdsBytes, s, a); break;
+            case T_Q5_0: hipLaunchKernelGGL((qblk_gemm_kernel<T_Q5_0, G>), grid, dim3(G::kThreads), G::kLdsBytes, s, a); break;
+            case T_Q4_0: hipLaunchKernelGGL((qblk_gemm_kernel<T_Q4_0, G>), grid, dim3(G::kThreads), G::kLdsBytes, s, a); break;
+            case T_Q6_K:
+                if constexpr (std::is_same_v<G, GeoLarge>) {
+                    hipLaunchKernelGGL((q6k_gemm_kernel<G>), grid, dim3(G::kThreads), G::kLdsBytes, s, a);
+                    break;
+                }
+                return hipErrorInvalidValue;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    };
+    // the default tiles, unless they would leave more than half the CUs idle (the Q6_K kernel keeps
+    // the default: its lm_head shapes fill the chip many times).  DeepSeek-V2-Lite's Q5_0 expert down at
+    // 512 tokens (64 default workgroups): 40.5 -> 23.7 us.  A Q8_0 [4864, 896] at 512 tokens (152 default
+    // workgroups) ran 34.2 us on the default tiles and 45.5 us on the small ones.
+    const int64_t large = static_cast<int64_t>((out_dim + GeoLarge::kBN - 1) / GeoLarge::kBN) *
+                          ((m + GeoLarge::kBM - 1) / GeoLarge::kBM);
+    if (QLIN_QBLK_SMALL && type != T_Q6_K && large * 2 < device_info().cu_count) return launch(GeoSmall{});
+    return launch(GeoLarge{});
 }
 
 }  // namespace qlin

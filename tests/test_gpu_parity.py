@@ -364,7 +364,10 @@ def test_quantize_q8_1_bit_exact(raw):
                                                     # super-block parities, tails; K 768: per-element kernel
                                                     (Q6_K, 1000, 2048, 65), (Q6_K, 513, 512, 17), (Q6_K, 24, 768, 5),
                                                     # K / 32 odd: rows not 4-byte aligned, the per-element kernel
-                                                    (Q8_0, 40, 96, 5), (Q5_0, 24, 160, 3)])
+                                                    (Q8_0, 40, 96, 5), (Q5_0, 24, 160, 3),
+                                                    # grids of at least half the CUs: the 8-wave, 64-token
+                                                    # tiles (the cases above take the 4-wave, 32-token ones)
+                                                    (Q4_0, 8192, 64, 256), (Q8_0, 4096, 128, 512)])
 def test_matmul_q8_1_parity(qtype, out_dim, in_dim, m):
     w, rb, _ = qgen.random_matrix(qtype, out_dim, in_dim, seed=61 + out_dim)
     x = qgen.random_x(m, in_dim, seed=62)
