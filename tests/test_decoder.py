@@ -247,6 +247,8 @@ def test_rms_norm_fused_gemv(qtype, hidden, outs, wtype, one_plus):
     (qgen.Q5_0, 1152, 777, True, "random"),
     (qgen.Q8_0, 896, 5000, False, "nan"),       # every third row's logit NaN (a NaN block scale): never picked
     (qgen.Q8_0, 896, 300, False, "allnan"),     # every logit NaN: nothing beats -inf, index 0
+    (qgen.Q4_K, 1024, 8704, False, "tail_tie"),  # 2 whole tiles and 2 rows per workgroup: the largest logit
+                                                 # in two workgroups' last rows, the lower row wins
 ])
 def test_gemv_argmax(qtype, hidden, vocab, norm, case):
     """The head GEMV with the greedy pick in its epilogue: the logits are the plain launches' bit for bit,
@@ -264,6 +266,19 @@ def test_gemv_argmax(qtype, hidden, vocab, norm, case):
         rows = w.reshape(vocab, rb)
         chosen = rows if case == "allnan" else rows[1::3]
         chosen[:, 0:2] = [0x00, 0x7e]
+    if case == "tail_tie":
+        # the largest logit's row copied into rows 8195 and 8492, past the whole tiles (in the last rows
+        # of workgroups 1 and 150 when every workgroup takes 2 whole tiles and then 2 rows)
+        lg = empty_f32(vocab)
+        qlin.call("qlin_launch_quant_gemv", qtype, dev(w), rb, dev(x), lg, vocab, hidden, 1)
+        top = int(np.argmax(host(lg)))
+        w = w.copy()
+        rows = w.reshape(vocab, rb)
+        src = rows[top].copy()
+        if top not in (8195, 8492):
+            rows[top] = rows[0 if top else 1]  # the maximum now only in the two copies
+        rows[8195] = src
+        rows[8492] = src
     if case == "tie":
         # copy the row of the largest logit into a row below it: two equal logits
         lg = empty_f32(vocab)
@@ -301,6 +316,8 @@ def test_gemv_argmax(qtype, hidden, vocab, norm, case):
         assert got == int(np.argmax(h))
     if case == "tie":
         assert (h == h[got]).sum() >= 2 and got == int(np.flatnonzero(h == h.max())[0])
+    if case == "tail_tie":
+        assert h[8195] == h[8492] == h.max() and got == 8195
 
 
 @pytest.mark.gpu
