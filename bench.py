@@ -683,11 +683,13 @@ def wl_prefill_f32(args, torch, qlin, gen):
     """The prefill entry the engine calls (TensorTool::quant_direct_gemm -> launch_quant_matmul, f32
     activations, TensorTool.cpp:163-168, kernel.cu:1254-1279): Q4_K [14336, 4096] x [512, 4096] (the
     headline) and DeepSeek-V2-Lite's Q6_K lm_head [102400, 2048] x [512, 2048], N(0,1) f32 activations.
-    A step is one qlin_launch_quant_matmul; two weight copies are rotated."""
+    A step is one qlin_launch_quant_matmul; two weight copies are rotated.  Also timed: the Q4_K matrix
+    at a short prompt's 64 tokens (the launch then takes the small workgroup geometry)."""
     M = 512
-    shapes = [("q4k_mlp", Q4_K, 14336, 4096), ("q6k_lm_head", Q6_K, 102400, 2048)]
+    shapes = [("q4k_mlp", Q4_K, 14336, 4096, M), ("q6k_lm_head", Q6_K, 102400, 2048, M),
+              ("q4k_mlp_64_tokens", Q4_K, 14336, 4096, 64)]
     res, head = {}, None
-    for name, qt, N, K in shapes:
+    for name, qt, N, K, M in shapes:
         rb = qlin.row_bytes(qt, K)
         ws = [synth_blocks(torch, qt, N, K, gen) for _ in range(2)]
         x = torch.randn(M, K, device="cuda", generator=gen)
@@ -696,11 +698,11 @@ def wl_prefill_f32(args, torch, qlin, gen):
         us = graph_us(torch, qlin, lambda qt=qt, ws=ws, rb=rb, x=x, y=y, N=N, K=K:
                       [qlin.quant_matmul(qt, w, rb, x, y, N, K, M) for w in ws], reps) / len(ws)
         flops = 2.0 * M * N * K
-        res[name] = {"type": qt, "n": N, "k": K, "us": round(us, 2), "tflops": round(flops / us / 1e6, 1)}
+        res[name] = {"type": qt, "m": M, "n": N, "k": K, "us": round(us, 2), "tflops": round(flops / us / 1e6, 1)}
         log(f"prefill f32 {name}: {us:.2f} us ({flops / us / 1e6:.1f} TFLOP/s)")
         if head is None:
-            head = (qt, ws[0], rb, x, N, K, us, flops, reps)
-    qt, w, rb, x, N, K, us, flops, reps = head
+            head = (qt, ws[0], rb, x, N, K, M, us, flops, reps)
+    qt, w, rb, x, N, K, M, us, flops, reps = head
     result = {
         "metric": "Q4_K x f32 prefill GEMM TFLOP/s (launch_quant_matmul, M=512, K=4096, N=14336)",
         "value": round(flops / us / 1e6, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps * 2, "warmup": 3,

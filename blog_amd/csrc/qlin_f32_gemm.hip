@@ -37,21 +37,31 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kNT = 2;                  // 16-row weight tiles per wave
-constexpr int kBN = kWaves * kNT * 16;  // weight rows per workgroup (256)
-constexpr int kMT = 4;                  // 16-token tiles per workgroup
-constexpr int kBM = kMT * 16;           // tokens per workgroup (64)
-static_assert(kBM == kWaves * 8, "staging: each wave stages 8 tokens, one lane per (token, sub-block)");
-// One LDS buffer (uint4 units): the hi plane [mt][j][lane], the lo plane, the min-term rows hi [mt][lane]
-// and lo (lanes >= 16 stay zero), then the tokens' scale exponents s (ints).  Two buffers: 145 KB.
-constexpr int kPlane = kMT * 8 * 64;
-constexpr int kRows = kMT * 64;
-constexpr int kExp = kBM / 4;
-constexpr int kBuf = 2 * kPlane + 2 * kRows + kExp;
-constexpr size_t kLdsBytes = 2 * kBuf * sizeof(uint4);
-static_assert(kLdsBytes <= 160 * 1024, "fits the CU's LDS");
+#ifndef QLIN_F32_GEMM_SMALL
+#define QLIN_F32_GEMM_SMALL 1  // the 4-wave, 32-token geometry for launches that would leave half the CUs idle
+#endif
+constexpr int kNT = 2;  // 16-row weight tiles per wave
+// A workgroup's geometry: W waves of 32 rows each for MT 16-token tiles.  The default (8 waves, 64
+// tokens: 256 rows) covers large grids; a launch that would leave more than half the CUs idle (short
+// prompts) takes 4 waves and 32 tokens (128 rows), four times as many workgroups.
+template <int W, int MT>
+struct Geo {
+    static constexpr int kWaves = W, kThreads = W * 64;
+    static constexpr int kBN = W * kNT * 16;       // weight rows per workgroup
+    static constexpr int kMT = MT, kBM = MT * 16;  // 16-token tiles and tokens per workgroup
+    static_assert(kBM == W * 8, "staging: each wave stages 8 tokens, one lane per (token, sub-block)");
+    // One LDS buffer (uint4 units): the hi plane [mt][j][lane], the lo plane, the min-term rows hi
+    // [mt][lane] and lo (lanes >= 16 stay zero), then the tokens' scale exponents s (ints).  Two buffers
+    // (145 KB for the default).
+    static constexpr int kPlane = MT * 8 * 64;
+    static constexpr int kRows = MT * 64;
+    static constexpr int kExp = kBM / 4;
+    static constexpr int kBuf = 2 * kPlane + 2 * kRows + kExp;
+    static constexpr size_t kLdsBytes = 2 * kBuf * sizeof(uint4);
+    static_assert(kLdsBytes <= 160 * 1024, "fits the CU's LDS");
+};
+using GeoLarge = Geo<8, 4>;
+using GeoSmall = Geo<4, 2>;
 
 struct F32GemmArgs {
     const uint8_t *w;
@@ -120,8 +130,10 @@ __device__ __forceinline__ uint2 piece(const uint32_t (&w)[3], int off) {
     return make_uint2(__builtin_amdgcn_alignbyte(w[1], w[0], off), __builtin_amdgcn_alignbyte(w[2], w[1], off));
 }
 
-template <int FMT>
-__global__ __launch_bounds__(kThreads) void f32_gemm_kernel(const F32GemmArgs a) {
+template <int FMT, class G>
+__global__ __launch_bounds__(G::kThreads) void f32_gemm_kernel(const F32GemmArgs a) {
+    constexpr int kThreads = G::kThreads, kBN = G::kBN, kMT = G::kMT, kBM = G::kBM;
+    constexpr int kPlane = G::kPlane, kRows = G::kRows, kBuf = G::kBuf;
     constexpr bool Q6 = FMT == T_Q6_K;
     extern __shared__ uint4 lds[];
     auto hi_plane = [&](int buf) { return lds + buf * kBuf; };
@@ -527,9 +539,17 @@ hipError_t f32_gemm(int type, const uint8_t *w, size_t rb, const float *x, float
     a.k = in_dim;
     a.nsb = in_dim / 256;
     a.add = add ? 1 : 0;
-    const dim3 grid = gemm_grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    if (type == T_Q6_K) hipLaunchKernelGGL(f32_gemm_kernel<T_Q6_K>, grid, dim3(kThreads), kLdsBytes, s, a);
-    else hipLaunchKernelGGL(f32_gemm_kernel<T_Q4_K>, grid, dim3(kThreads), kLdsBytes, s, a);
+    auto launch = [&](auto geo) {
+        using G = decltype(geo);
+        const dim3 grid = gemm_grid((out_dim + G::kBN - 1) / G::kBN, (m + G::kBM - 1) / G::kBM);
+        if (type == T_Q6_K) hipLaunchKernelGGL((f32_gemm_kernel<T_Q6_K, G>), grid, dim3(G::kThreads), G::kLdsBytes, s, a);
+        else hipLaunchKernelGGL((f32_gemm_kernel<T_Q4_K, G>), grid, dim3(G::kThreads), G::kLdsBytes, s, a);
+    };
+    // the default tiles, unless they would leave more than half the CUs idle
+    const int64_t large = static_cast<int64_t>((out_dim + GeoLarge::kBN - 1) / GeoLarge::kBN) *
+                          ((m + GeoLarge::kBM - 1) / GeoLarge::kBM);
+    if (QLIN_F32_GEMM_SMALL && large * 2 < device_info().cu_count) launch(GeoSmall{});
+    else launch(GeoLarge{});
     return hipGetLastError();
 }
 

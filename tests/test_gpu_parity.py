@@ -407,14 +407,16 @@ def test_q4k_gemm_c4_shape_every_row():
     assert row_err.max() <= 1e-5, (int(row_err.argmax()), float(row_err.max()))
 
 
-@pytest.mark.parametrize("qtype,N,K", [(Q4_K, 14336, 4096), (Q6_K, 8192, 2048)])
-def test_f32_gemm_prefill_shape_every_row(qtype, N, K):
+@pytest.mark.parametrize("qtype,N,K,M", [(Q4_K, 14336, 4096, 512), (Q6_K, 8192, 2048, 512),
+                                         (Q4_K, 14336, 4096, 64), (Q6_K, 8192, 2048, 80)])
+def test_f32_gemm_prefill_shape_every_row(qtype, N, K, M):
     """The engine's prefill entry (TensorTool::quant_direct_gemm -> launch_quant_matmul with f32
     activations, TensorTool.cpp:163-168, kernel.cu:1254-1279) on the fp16 matrix cores: Q4_K at
     Llama/Qwen-7B MLP shape [14336, 4096] and Q6_K at the DeepSeek-V2-Lite lm_head's K (2048, 8192 of
-    its 102400 rows) x [512, K] N(0,1) f32 activations, every weight row checked against the f64
-    oracle on 64 tokens that include both ends of every 64-token tile."""
-    M = 512
+    its 102400 rows) x [M, K] N(0,1) f32 activations, every weight row checked against the f64
+    oracle on 64 tokens that include both ends of every 64-token tile (every token when M <= 96).  At
+    512 tokens the launch takes 256-row, 64-token workgroups; at 64 and 80 (a short prompt, more than
+    half the CUs idle on those) 128-row, 32-token ones, 80 ending in half a token tile."""
     rng = np.random.default_rng(91 + qtype)
     bb = 144 if qtype == Q4_K else 210
     rb = K // 256 * bb
@@ -427,9 +429,12 @@ def test_f32_gemm_prefill_shape_every_row(qtype, N, K):
     banner(f"f32 prefill gemm type={qtype} {M}x{K}x{N}")
     yd = empty_f32(M, N)
     qlin.quant_matmul(qtype, dev(w.reshape(-1)), rb, dev(x), yd, N, K, M)
-    ends = np.array([[64 * t, 64 * t + 63] for t in range(M // 64)]).reshape(-1)
-    rest = rng.choice(np.setdiff1d(np.arange(M), ends), 64 - ends.size, replace=False)
-    toks = np.sort(np.concatenate([ends, rest]))
+    if M <= 96:
+        toks = np.arange(M)
+    else:
+        ends = np.array([[64 * t, 64 * t + 63] for t in range(M // 64)]).reshape(-1)
+        rest = rng.choice(np.setdiff1d(np.arange(M), ends), 64 - ends.size, replace=False)
+        toks = np.sort(np.concatenate([ends, rest]))
     ref = orc.matmul_f64(qtype, w.reshape(-1), rb, x[toks], N, K)
     got = host(yd)[toks]
     assert normwise_rel_err(got, ref) <= FP32
