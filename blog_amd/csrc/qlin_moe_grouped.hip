@@ -178,21 +178,29 @@ struct StreamArgs {
     float scaling;
     int *ids_out;
     float *w_out;
-    // SW: the shared experts' SwiGLU in the same launch (sh_rows > 0): workgroup b computes 16-row tile b
-    // of the shared gate and up matrices for the sh_tokens (<= 16) rows of x before its routed share,
-    // into sh_act [sh_tokens, sh_rows], and its routed share is smaller by sh_cost.
+    // SW: the shared experts' SwiGLU in the same launch (sh_rows > 0): workgroup b computes 16-row tiles
+    // b * sh_per_wg .. of the shared gate and up matrices for the sh_tokens (<= 16) rows of x before its
+    // routed share, into sh_act [sh_tokens, sh_rows], and its routed share is smaller by sh_cost.
     const uint8_t *sh_wg, *sh_wu;
     size_t sh_rb;
     float *sh_act;
-    int sh_rows, sh_tokens, sh_cost;
+    int sh_rows, sh_tokens, sh_cost, sh_per_wg;
 };
 // LDS of the in-kernel router, after the staged ids: per wave the 64 exponentials
 constexpr int kRouteWaveFloats = 64;
-// A shared-expert tile in the gate/up launch: its partials (8 super-block slots x 2 matrices x 64
-// lanes of 4 floats) in the dynamic LDS, and its cost in the units of StepFmt<T_Q4_K> (11.6 us of a
-// workgroup's time at 16 tokens in a per-workgroup trace, at 0.04 us per unit)
+// Shared-expert tiles in the gate/up launch: up to kSharedMaxTiles per workgroup (one output pass of
+// 256 threads each), the tokens' x and then their partials (per tile 8 super-block slots x 2 matrices
+// x 64 lanes of 4 floats) in the dynamic LDS.  A workgroup's cost for them, in the units of
+// StepFmt<T_Q4_K> (0.04 us of a workgroup's time each): staging x, then each tile (per-workgroup trace
+// at 16 tokens, two tiles per workgroup: x staged 5.2 us after the start, the tiles done 11 us later;
+// at a tile cost of 150 those workgroups ended about 1 us before the others).  Two tiles per workgroup
+// halve the staging (C5 step 89.2 -> 88.2 us against one); more, in this kernel's 128 VGPRs, spill.
+#ifndef QLIN_SHARED_TILES
+#define QLIN_SHARED_TILES 2  // tiles per workgroup
+#endif
+constexpr int kSharedMaxTiles = 2;
 constexpr size_t kSharedPartBytes = 8 * 2 * 64 * 16;
-constexpr int kSharedTileCost = 288;
+constexpr int kSharedStageCost = 125, kSharedTileCost = 135;
 
 // 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
 // shared by the 16 waves of a CU: both helpers take 32-bit arithmetic when the operands allow
@@ -264,31 +272,57 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
     const int n = lane & 15, g = lane >> 4;
     if (tid < 8) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);  // before the barriers below
 
-    // The shared experts' SwiGLU tile of this workgroup, first (it depends on no routing): wave w takes
-    // matrix w & 1 and super-blocks w / 2, w / 2 + 8, ..., the wave and order q4k_dense_kernel's wave
-    // w / 2 gives that matrix, and the 8 waves' sums of a matrix are added in wave order as there: the
-    // same bits as the separate launch.  The partials use the (still unused) staging area.
-    const int n_shared = SW && a.sh_rows > 0 ? (a.sh_rows + 15) / 16 : 0;
+    // The shared experts' SwiGLU tiles of this workgroup, first (they depend on no routing): wave w takes
+    // matrix w & 1 and super-blocks w / 2, w / 2 + 8, ... of each tile, the wave and order
+    // q4k_dense_kernel's wave w / 2 gives that matrix, and the 8 waves' sums of a matrix are added in
+    // wave order as there: the same bits as the separate launch.  The tokens' x is staged in LDS once
+    // per workgroup (read from L2 by every wave, the x lines' L2 channels were the bound), after each
+    // wave has requested its first weights, and serves the workgroup's sh_per_wg tiles; x and then the
+    // partials use the (still unused) staging area.
+    const int n_tiles = SW && a.sh_rows > 0 ? (a.sh_rows + 15) / 16 : 0;
+    const int n_shared = n_tiles ? (n_tiles + a.sh_per_wg - 1) / a.sh_per_wg : 0;  // workgroups with tiles
     if constexpr (SW) {
         if (blockIdx.x < n_shared) {  // uniform
-            const int row0 = blockIdx.x * 16, m = wave & 1, slot = wave >> 1;
-            const uint8_t *rp = (m ? a.sh_wu : a.sh_wg) + static_cast<size_t>(min(row0 + n, a.sh_rows - 1)) * a.sh_rb;
-            const float *xrow = a.x + static_cast<size_t>(min(n, a.sh_tokens - 1)) * a.K + 8 * g;
-            f32x4 D[1] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
-            q4k_rows_dot<1>(&rp, xrow, slot, 8, a.K / 256, g, D);
-            f32x4 *part = reinterpret_cast<f32x4 *>(smem);  // [slot][matrix][lane]
-            part[(slot * 2 + m) * 64 + lane] = D[0];
+            const int m = wave & 1, slot = wave >> 1, nsb = a.K / 256;
+            const int t0 = blockIdx.x * a.sh_per_wg, nt = min(a.sh_per_wg, n_tiles - t0);
+            const uint8_t *wm = m ? a.sh_wu : a.sh_wg;
+            const uint8_t *rp[kSharedMaxTiles];
+#pragma unroll
+            for (int t = 0; t < kSharedMaxTiles; ++t)
+                rp[t] = wm + static_cast<size_t>(min((t0 + min(t, nt - 1)) * 16 + n, a.sh_rows - 1)) * a.sh_rb;
+            Q4KRaw cur[1];
+            if (slot < nsb) load_q4k(cur[0], rp[0] + static_cast<size_t>(slot) * 144, g);
+            float *sx = reinterpret_cast<float *>(smem);  // [sh_tokens][K]
+            const int nx4 = a.sh_tokens * a.K / 4;
+            for (int i = tid; i < nx4; i += kSThreads)
+                reinterpret_cast<float4 *>(sx)[i] = reinterpret_cast<const float4 *>(a.x)[i];
             __syncthreads();
-            // outputs: token tid / 16, row row0 + tid % 16; D element r of lane l is token 4 (l / 16) + r
-            const int tl = tid >> 4, o = tid & 15;
-            if (tid < 256 && tl < a.sh_tokens && o < min(16, a.sh_rows - row0)) {
-                const int l = (tl >> 2) * 16 + o, r = tl & 3;
-                float v0 = 0.0f, v1 = 0.0f;
-                for (int wv = 0; wv < 8; ++wv) {
-                    v0 += part[(wv * 2) * 64 + l][r];
-                    v1 += part[(wv * 2 + 1) * 64 + l][r];
+            const float *xrow = sx + min(n, a.sh_tokens - 1) * a.K + 8 * g;
+            f32x4 D[kSharedMaxTiles];
+#pragma unroll
+            for (int t = 0; t < kSharedMaxTiles; ++t) D[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            q4k_tiles_dot<kSharedMaxTiles>(cur, rp, nt, xrow, slot, 8, nsb, g, D);
+            __syncthreads();  // x is read: the partials take its place
+            f32x4 *part = reinterpret_cast<f32x4 *>(smem);  // [tile][slot][matrix][lane]
+#pragma unroll
+            for (int t = 0; t < kSharedMaxTiles; ++t)
+                if (t < nt) part[((t * 8 + slot) * 2 + m) * 64 + lane] = D[t];
+            __syncthreads();
+            // outputs: 256 threads per tile; token tl, row row0 + o; D element r of lane l is token
+            // 4 (l / 16) + r
+            const int ti = tid >> 8, tl = (tid >> 4) & 15, o = tid & 15;
+            if (ti < nt) {
+                const int row0 = (t0 + ti) * 16;
+                if (tl < a.sh_tokens && o < min(16, a.sh_rows - row0)) {
+                    const int l = (tl >> 2) * 16 + o, r = tl & 3;
+                    const f32x4 *pt = part + ti * 8 * 2 * 64;
+                    float v0 = 0.0f, v1 = 0.0f;
+                    for (int wv = 0; wv < 8; ++wv) {
+                        v0 += pt[(wv * 2) * 64 + l][r];
+                        v1 += pt[(wv * 2 + 1) * 64 + l][r];
+                    }
+                    a.sh_act[static_cast<size_t>(tl) * a.sh_rows + row0 + o] = v0 / (1.0f + expf(-v0)) * v1;
                 }
-                a.sh_act[static_cast<size_t>(tl) * a.sh_rows + row0 + o] = v0 / (1.0f + expf(-v0)) * v1;
             }
             __syncthreads();  // the staging area is free again
         }
@@ -1118,15 +1152,19 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
         // the shared experts' SwiGLU as the first tile of workgroups 0 .. (one 16-token tile, one
         // shared tile per workgroup at most, its partials in the dynamic LDS)
         const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-        if (shared && shared->rows > 0 && tokens <= 16 && (shared->rows + 15) / 16 <= up.grid &&
-            shared->rb % 16 == 0 && al16(shared->wg) && al16(shared->wu) && up.lds >= kSharedPartBytes) {
+        const int sh_tiles = shared ? (shared->rows + 15) / 16 : 0;
+        const int per_wg = std::max(1, std::min(QLIN_SHARED_TILES, kSharedMaxTiles));
+        if (shared && shared->rows > 0 && tokens <= 16 && (sh_tiles + per_wg - 1) / per_wg <= up.grid &&
+            shared->rb % 16 == 0 && al16(shared->wg) && al16(shared->wu) &&
+            up.lds >= std::max(per_wg * kSharedPartBytes, static_cast<size_t>(tokens) * K * sizeof(float))) {
             ua.sh_wg = shared->wg;
             ua.sh_wu = shared->wu;
             ua.sh_rb = shared->rb;
             ua.sh_act = shared->act;
             ua.sh_rows = shared->rows;
             ua.sh_tokens = tokens;
-            ua.sh_cost = kSharedTileCost;
+            ua.sh_cost = kSharedStageCost + per_wg * kSharedTileCost;
+            ua.sh_per_wg = per_wg;
             if (shared->done) *shared->done = true;
         }
         const hipError_t e = grp ? launch_stream<T_Q4_K, true, true>(up, ua, s) : launch_stream<T_Q4_K, true>(up, ua, s);
