@@ -242,7 +242,7 @@ def read_traffic():
     return None
 
 
-# ---- the other configurations (2 and 4, and DeepSeek's Q6_K lm_head) -----
+# ---- the other configurations (C1, C2 and C4, and DeepSeek's Q6_K lm_head) -------------------------
 # Each is one JSON line like the headline one: a step is one pass of the configuration's launches
 # over synthetic inputs resident in HBM, timed as HIP-graph replays on the launch stream, with the
 # distinct weight copies rotated so that the 256 MB Infinity Cache cannot hold them.

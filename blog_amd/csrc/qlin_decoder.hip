@@ -1,8 +1,9 @@
 // qlin_decoder.hip -- the glue of a Qwen2-architecture decoder layer around the quantized linears,
 // gfx950: RMSNorm, rotary embedding with the KV-cache store, and causal grouped-query attention.
 //
-// These are not on the quantized-linear path; they exist so that a whole decoder (BASELINE config
-// 3: Qwen2.5-0.5B architecture, all linears Q8_0) can run its greedy decode on the path's kernels.
+// These are not on the quantized-linear path; they exist so that a whole decoder (benchmark
+// configuration C3: Qwen2.5-0.5B architecture, all linears Q8_0) can run its greedy decode on the
+// path's kernels.
 // Semantics, restated from the reference engine (AI/codes/local-llm/src/backend/cuda/ops/kernel.cu):
 //   rms_norm      112-150   y = x * rsqrt(mean(x^2) + eps) * w, w from bf16 / f16 (1 + w if one_plus)
 //   rope          186-226   pairs (i, i + d/2), inv_freq = 1 / theta^(2i / d), angle = pos * inv_freq

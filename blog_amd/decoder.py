@@ -1,4 +1,4 @@
-"""A Qwen2-architecture decoder over the quantized-linear path: the harness of BASELINE config 3.
+"""A Qwen2-architecture decoder over the quantized-linear path: the harness of benchmark configuration C3.
 
 Qwen2.5-0.5B architecture (24 layers, hidden 896, 14 query / 2 KV heads of 64, SwiGLU FFN 4864,
 vocabulary 151936, RMSNorm eps 1e-6, rotary theta 1e6), every linear in Q8_0, random-init weights

@@ -2,8 +2,8 @@
  * qlin_decoder.h -- the glue around the quantized linears of a Qwen2-architecture decoder layer:
  * RMSNorm, rotary embedding with the KV-cache store, and causal grouped-query attention.
  *
- * These are not part of the quantized-linear path.  They let a whole decoder (
- * Qwen2.5-0.5B architecture with every linear in Q8_0) run its greedy decode on the path's kernels;
+ * These are not part of the quantized-linear path.  They let a whole decoder (benchmark configuration
+ * C3, Qwen2.5-0.5B architecture with every linear in Q8_0) run its greedy decode on the path's kernels;
  * the linears, the embedding lookup and the argmax are the entry points of qlin.h.  Conventions as
  * in qlin.h: caller-owned device pointers, asynchronous on qlin_set_stream's stream, nothing
  * allocated, a qlin_status returned.

@@ -1,4 +1,4 @@
-"""a Qwen2.5-0.5B-architecture decoder with every linear in Q8_0, greedy decoding.
+"""Benchmark configuration C3: a Qwen2.5-0.5B-architecture decoder with every linear in Q8_0, greedy decoding.
 
 CPU: the oracle's decoder twin (orc_qwen2_logits) pinned by an independent numpy restatement of the
 layer on a small model (every index: GQA head mapping, rotary pairs, causal window, tied head), and
