@@ -138,21 +138,24 @@ using plan::kXPad;
 //   Per block: sum x*w = d * (D - corr * X), X = sum of x (hi + lo) over the block, because the
 //   operand is bf16(128 + u) with u = q + 16 (Q5_0), or l / h (Q8_0: 128*17 + 128).
 template <int FMT> struct StepFmt;
-// The workgroups split the selected experts' work by a cost: w0 per 16-row tile and pass, w1 per tile
-// and route, and ws per expert and pass (the workgroup that takes part of an expert stages its routes'
-// x and starts a new stream of steps).  Fitted to per-workgroup times within one launch of the C5
-// shape (16 tokens, top-6 of 64): a gate/up tile 1.27 us, a route on it 0.04 us, an expert 4.4 us; a
-// down tile 0.57 us, a route on it 0.07 us, an expert 3.8 us.  (Weights fitted earlier to whole-launch
-// times, (4, 1, 0) for gate/up, left the workgroups with one-route experts 40% longer than the rest.)
+// The workgroups split the selected experts' work by a cost: a 16-row tile costs the larger of w0 per
+// pass (the weights' stream) and wc per route (the block-diagonal operand's MFMA and VALU work), plus
+// w1 per route, and an expert ws per pass (the workgroup that takes part of an expert stages its
+// routes' x and starts a new stream of steps).  Fitted to per-workgroup times within one launch of the
+// C5 shape (16 tokens, top-6 of 64): a gate/up tile takes 1.49 us with 1, 2 or 3 routes and 1.80 us
+// with 4 (workgroups that take one expert, by its route count), an expert about 4.4 us more; over all
+// workgroups a down tile 0.52 us, a route on it 0.07 us, an expert 3.2 us (residual 1.0 us, no trend
+// left by route count).  (A gate/up cost linear in the routes, 32 + routes, left the workgroups with
+// a 4-route expert 7 us behind the median.)
 template <> struct StepFmt<T_Q4_K> {
-    static constexpr int ce = 256, bb = 144, cb = 144, tpb = 0, w0 = 32, w1 = 1, ws = 112;
+    static constexpr int ce = 256, bb = 144, cb = 144, tpb = 0, w0 = 32, wc = 10, w1 = 0, ws = 94;
 };
 template <> struct StepFmt<T_Q5_0> {
-    static constexpr int ce = 128, bb = 22, cb = 88, nd = 5, tpb = 4, w0 = 8, w1 = 1, ws = 54;
+    static constexpr int ce = 128, bb = 22, cb = 88, nd = 5, tpb = 4, w0 = 8, wc = 0, w1 = 1, ws = 54;
     static constexpr float corr = 144.0f;
 };
 template <> struct StepFmt<T_Q8_0> {
-    static constexpr int ce = 128, bb = 34, cb = 136, nd = 8, tpb = 8, w0 = 8, w1 = 1, ws = 54;
+    static constexpr int ce = 128, bb = 34, cb = 136, nd = 8, tpb = 8, w0 = 8, wc = 0, w1 = 1, ws = 54;
     static constexpr float corr = 2304.0f;
 };
 
@@ -191,10 +194,11 @@ constexpr int kRouteWaveFloats = 64;
 // Shared-expert tiles in the gate/up launch: up to kSharedMaxTiles per workgroup (one output pass of
 // 256 threads each), the tokens' x and then their partials (per tile 8 super-block slots x 2 matrices
 // x 64 lanes of 4 floats) in the dynamic LDS.  A workgroup's cost for them, in the units of
-// StepFmt<T_Q4_K> (0.04 us of a workgroup's time each): staging x, then each tile (per-workgroup trace
-// at 16 tokens, two tiles per workgroup: x staged 5.2 us after the start, the tiles done 11 us later;
-// at a tile cost of 150 those workgroups ended about 1 us before the others).  Two tiles per workgroup
-// halve the staging (C5 step 89.2 -> 88.2 us against one); more, in this kernel's 128 VGPRs, spill.
+// StepFmt<T_Q4_K> (about 0.047 us of a workgroup's time each): staging x, then each tile
+// (per-workgroup trace at 16 tokens, two tiles per workgroup: x staged 5.2 us after the start, the
+// tiles done 11 us later; at a tile cost of 150 those workgroups ended about 1 us before the others).
+// Two tiles per workgroup halve the staging (C5 step 89.2 -> 88.2 us against one); more, in this
+// kernel's 128 VGPRs, spill.
 #ifndef QLIN_SHARED_TILES
 #define QLIN_SHARED_TILES 2  // tiles per workgroup
 #endif
@@ -230,7 +234,9 @@ __device__ __forceinline__ int64_t uni(int64_t v) {
 // expert's set-up per pass, which comes first in the expert's cost range.
 template <int FMT, int NQ>
 __device__ __forceinline__ int64_t tile_cost(int cnt) {
-    return static_cast<int64_t>((cnt + NQ - 1) / NQ) * StepFmt<FMT>::w0 + static_cast<int64_t>(cnt) * StepFmt<FMT>::w1;
+    using F = StepFmt<FMT>;
+    const int64_t stream = static_cast<int64_t>((cnt + NQ - 1) / NQ) * F::w0, math = static_cast<int64_t>(cnt) * F::wc;
+    return (stream > math ? stream : math) + static_cast<int64_t>(cnt) * F::w1;
 }
 template <int FMT, int NQ>
 __device__ __forceinline__ int64_t setup_cost(int cnt) {
