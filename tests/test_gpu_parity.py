@@ -864,15 +864,16 @@ def test_moe_grouped_unaligned_output():
     (Q4_K, 16, 4, 3, 256, 512, 0, Q4_K),        # no shared experts: the routed call alone
     (Q4_K, 8, 6, 2, 256, 2304, 512, Q4_K),      # 9 super-blocks: the shared tile's wave 0 takes two
     (Q4_K, 8, 20, 2, 256, 512, 512, Q4_K),      # over 16 tokens: the shared SwiGLU as its own launch
-    (Q4_K, 8, 6, 2, 256, 512, 4352, Q4_K),      # 272 shared tiles, more than the workgroups: its own launch
+    (Q4_K, 8, 6, 2, 256, 512, 4352, Q4_K),      # 272 shared tiles on 136 workgroups, two each
+    (Q4_K, 8, 6, 2, 256, 512, 8448, Q4_K),      # 528 shared tiles, more than two per workgroup: its own launch
 ])
 def test_moe_ffn_matches_three_calls(gu, E, tokens, k, ffn, hid, sffn, stype):
     """The MoE FFN call (routed from the logits, then the shared experts) gives, bit for bit, what the
     routed call from logits followed by qlin_launch_quant_swiglu_rows and qlin_launch_quant_matmul_add
     give on the same inputs, and the per-token reference's routed sum plus the shared experts to 1e-4.
     Up to 16 tokens with Q4_K shared weights, the shared SwiGLU runs inside the routed gate/up launch
-    (one 16-row tile per workgroup, the separate kernel's sums in its order); the last cases take the
-    separate launch."""
+    (two 16-row tiles per workgroup from x staged in LDS, the separate kernel's sums in its order); the
+    cases over 16 tokens and over two tiles per workgroup take the separate launch."""
     wg, wu, grb, geb, wdn, drb, deb, x, _, _ = _moe_batch(gu, Q5_0, E, ffn, hid, tokens, k, 401 + E + tokens)
     rng = np.random.default_rng(411 + tokens)
     logits = rng.standard_normal((tokens, E)).astype(np.float32)
