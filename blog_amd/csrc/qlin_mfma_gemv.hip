@@ -1054,7 +1054,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     int best_i = 0;
     auto write_row = [&](int r, const float (&tot)[NW]) {
         const int gr = grow(r);
-        if constexpr (ROUTED) {
+        if constexpr (ROUTED && SWIGLU) {  // (the routed down adds its routes above and never gets here)
             // a route without an expert gives 0 (kernel.cu:1340-1385)
             const bool none = s_ids[route_of(gr, a.route_rows, a.route_magic)] < 0;
             mats.y[0][gr] = none ? 0.0f : tot[0] / (1.0f + expf(-tot[0])) * tot[1];

@@ -66,7 +66,8 @@ using GeoSmall = Geo<4, 2>;
 
 template <int FMT> struct QBlk;
 template <> struct QBlk<T_Q8_0> {
-    static constexpr int bytes = 34, offset = 0;
+    static constexpr int bytes = 34;
+    [[maybe_unused]] static constexpr int offset = 0;  // (the int8 path subtracts 1152 instead)
 };
 template <> struct QBlk<T_Q5_0> {
     static constexpr int bytes = 22, offset = 16;
