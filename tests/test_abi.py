@@ -16,8 +16,13 @@ HEADERS = [os.path.join(ROOT, "include", h) for h in ("qlin.h", "qlin_gguf.h", "
 OK, UNSUP, SHAPE, NULL, ROWB, LIMIT, LAUNCH, ALIGN = range(8)
 
 
+def _read(path):
+    with open(path) as f:
+        return f.read()
+
+
 def declared_symbols():
-    text = "".join(open(h).read() for h in HEADERS)
+    text = "".join(_read(h) for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(qlin_\w+)\s*\(", text)))
 

@@ -62,7 +62,8 @@ def test_header_tensors_and_placement(written):
     with gguf.GgufFile(path) as f:
         assert f.version == 3 and f.alignment == 32
         assert f.tensor_view_names() == [t[0] for t in tensors]
-        raw = open(path, "rb").read()
+        with open(path, "rb") as fh:
+            raw = fh.read()
         for name, gtype, shape, data in tensors:
             v = f.get_tensor_view(name)
             assert v.dtype == gtype and list(v.shape) == shape          # file dims reversed: [out, in]

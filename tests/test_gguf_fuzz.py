@@ -50,7 +50,8 @@ def _write_cases(out):
                  + b"\0" * 16)
     with open(p("hugecount"), "wb") as fh:
         fh.write(b"GGUF" + struct.pack("<IQQ", 3, 2 ** 40, 0) + b"\0" * 64)
-    base = bytes(open(p("valid"), "rb").read())
+    with open(p("valid"), "rb") as fh:
+        base = fh.read()
     for cut in range(0, len(base), max(1, len(base) // 400)):
         with open(p(f"cut{cut:06d}"), "wb") as fh:
             fh.write(base[:cut])
