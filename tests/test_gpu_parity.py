@@ -407,6 +407,34 @@ def test_q4k_gemm_c4_shape_every_row():
     assert row_err.max() <= 1e-5, (int(row_err.argmax()), float(row_err.max()))
 
 
+def test_q6k_gemm_lm_head_shape_every_row():
+    """DeepSeek-V2-Lite's lm_head in prefill: Q6_K [102400, 2048] x Q8_1 activations [512, 2048] -> [512,
+    102400] (q6k_gemm_kernel, d applied once per super-block into output sums kept in LDS), every weight
+    row checked against the oracle on 32 tokens: both ends of each of the 8 64-token tiles plus random
+    ones, so every workgroup of the 3200 covers some checked outputs.  Random ql / qh / scale bytes, d =
+    f16(|N(0,1)| * 0.01)."""
+    N, K, M = 102400, 2048, 512
+    rng = np.random.default_rng(83)
+    rb = K // 256 * 210
+    w = rng.integers(0, 256, size=(N, K // 256, 210), dtype=np.uint8)
+    w[:, :, 208:210] = f16_bits(np.abs(rng.standard_normal((N, K // 256))) * 0.01).view(np.uint8).reshape(N, K // 256, 2)
+    x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+    xq = orc.quantize_q8_1(x, K)
+    banner("q6k gemm lm_head shape 512x2048x102400")
+    yd = empty_f32(M, N)
+    qlin.quant_matmul_q8_1(Q6_K, dev(w.reshape(-1)), rb, dev(xq), yd, N, K, M)
+    ends = np.array([[64 * t, 64 * t + 63] for t in range(M // 64)]).reshape(-1)
+    rest = rng.choice(np.setdiff1d(np.arange(M), ends), 32 - ends.size, replace=False)
+    toks = np.sort(np.concatenate([ends, rest]))
+    rbx = orc.q8_1_row_bytes(K)
+    xq_t = np.ascontiguousarray(xq.reshape(M, rbx)[toks]).reshape(-1)
+    ref = orc.matmul_q8_1(Q6_K, w.reshape(-1), rb, xq_t, N, K, toks.size, threads=0)
+    got = host(yd)[toks]
+    assert normwise_rel_err(got, ref) <= FP32
+    row_err = np.linalg.norm(got - ref, axis=0) / np.maximum(np.linalg.norm(ref, axis=0), 1e-30)
+    assert row_err.max() <= 1e-5, (int(row_err.argmax()), float(row_err.max()))
+
+
 @pytest.mark.parametrize("qtype,N,K,M", [(Q4_K, 14336, 4096, 512), (Q6_K, 8192, 2048, 512),
                                          (Q4_K, 14336, 4096, 64), (Q6_K, 8192, 2048, 80)])
 def test_f32_gemm_prefill_shape_every_row(qtype, N, K, M):
