@@ -72,6 +72,7 @@
 // step's 16 row sums in LDS; they are added in super-block order at the end (deterministic) and
 // only then is y written.
 #include <cstddef>
+#include <type_traits>
 
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
@@ -465,7 +466,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             // (wide rows: the 48 bytes from the 16-byte unit holding the first byte, w[0..11] and
             // w[12..23], with the offset into that unit, 0..14)
             const int h = g >> 1;
-            const int sh = static_cast<int>(reinterpret_cast<uintptr_t>(q) & (WIDE ? 15u : 3u));
+            // Wide rows start 16-aligned, so super-block sb starts 210 sb = 2 sb (mod 16) into a unit:
+            // an offset from the step, not from the pointer's bits, which keeps q a global pointer
+            // (masking its bits makes the loads flat ones, whose count a wait for LDS results shares)
+            const int sh = WIDE ? (2 * p.sb) & 15 : static_cast<int>(reinterpret_cast<uintptr_t>(q) & 3u);
             if constexpr (WIDE) {
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
@@ -666,10 +670,23 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
 
     // Q6_K: dword t of this lane's ql and qh bytes (elements 4t..4t+3 of its low- and high-nibble
     // groups): from the 36 bytes at or 2 before them, or (wide rows) from the 48-byte window, first
-    // shifting by whole dwords (offset bits 3 and 2, uniform per step), then by bytes
-    auto q6_words = [&](const Raw &cur, uint32_t (&ql)[8], uint32_t (&qh)[8]) {
+    // shifting by whole dwords (offset bits 3 and 2, uniform per step), then by bytes.  offc: the
+    // wide row's offset as a compile-time constant (std::integral_constant), or -1 to read it from the
+    // step
+    auto q6_words = [&](const Raw &cur, uint32_t (&ql)[8], uint32_t (&qh)[8], auto offc) {
+        constexpr int OFF = decltype(offc)::value;
         const uint32_t off = cur.w[26] >> 16;
-        if constexpr (WIDE) {
+        if constexpr (WIDE && OFF >= 0) {
+            // constant shifts: the dword shift selects registers, the byte shift (0 or 2) costs one
+            // v_alignbyte per dword or nothing
+            constexpr int D = OFF >> 2;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                ql[t] = (OFF & 3) ? __builtin_amdgcn_alignbyte(cur.w[t + D + 1], cur.w[t + D], OFF & 3) : cur.w[t + D];
+                qh[t] = (OFF & 3) ? __builtin_amdgcn_alignbyte(cur.w[12 + t + D + 1], cur.w[12 + t + D], OFF & 3)
+                                  : cur.w[12 + t + D];
+            }
+        } else if constexpr (WIDE) {
             // (the dword shifts as bit-field merges under an all-ones or all-zero mask the compiler
             // cannot see through: as selects between neighbouring elements they would become an
             // element chosen by a computed index, which keeps the arrays in scratch)
@@ -703,10 +720,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     // Q6_K: this lane's four 16-element scales (sc[8h + 2(g & 1)], +1, +4, +5) and d.  Wide rows: the
     // 8-byte pieces of the 32-byte window hold the scale pairs at window offsets o = off + 8h + 2(g & 1)
     // and o + 4, d at off + 16; dword j of the window is in lane group j >> 1 (element j & 1)
-    auto q6_scales = [&](const Raw &cur, float &s0, float &s1, float &s2, float &s3, float &dd) {
+    auto q6_scales = [&](const Raw &cur, float &s0, float &s1, float &s2, float &s3, float &dd, auto offc) {
+        constexpr int OFF = decltype(offc)::value;
         uint32_t sa, sb, dw;
         if constexpr (WIDE) {
-            const int off = static_cast<int>(cur.w[26] >> 16);
+            const int off = OFF >= 0 ? OFF : static_cast<int>(cur.w[26] >> 16);
             const int o = off + 8 * (g >> 1) + 2 * (g & 1), j = o >> 2;
             const int la = 16 * (j >> 1) + n, lb = 16 * ((j + 1) >> 1) + n;
             const uint32_t ax = __shfl(cur.w[24], la), ay = __shfl(cur.w[25], la);
@@ -760,16 +778,18 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             auto digits = [](const i32x4 &d) { return digits_value(d); };
             float r;
             if constexpr (FMT == T_Q6_K) {
-                // 6-bit values u of the low-nibble group (elements 4t..4t+3 from ql/qh dword t) and of the
-                // high-nibble group; MFMA u carries one 16-element scale group: the low group's
-                // elements 0..15, 16..31, then the high group's
+              // 6-bit values u of the low-nibble group (elements 4t..4t+3 from ql/qh dword t) and of the
+              // high-nibble group; MFMA u carries one 16-element scale group: the low group's elements
+              // 0..15, 16..31, then the high group's
+              auto q6_dot = [&](auto offc) {
                 const int hs = 2 * (g & 1);
                 uint32_t lo[8], hi[8], wl[8], wh[8];
-                q6_words(cur, wl, wh);
+                q6_words(cur, wl, wh, offc);
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    lo[t] = (wl[t] & 0x0f0f0f0fu) | (((wh[t] >> hs) & 0x03030303u) << 4);
-                    hi[t] = ((wl[t] >> 4) & 0x0f0f0f0fu) | (((wh[t] >> (hs + 4)) & 0x03030303u) << 4);
+                    const uint32_t whs = wh[t] >> hs;  // the low group's 2 bits at 0, 1, the high group's at 4, 5
+                    lo[t] = (wl[t] & 0x0f0f0f0fu) | ((whs << 4) & 0x30303030u);
+                    hi[t] = ((wl[t] >> 4) & 0x0f0f0f0fu) | (whs & 0x30303030u);
                 }
                 auto vec = [](const uint32_t *v) {
                     return i32x4{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]),
@@ -788,13 +808,31 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
                 const float scl = sxp[blo], sch = sxp[bhi];
                 const float *x16 = sxp + K / 32;
                 float s0, s1, s2, s3, dd;
-                q6_scales(cur, s0, s1, s2, s3, dd);
+                q6_scales(cur, s0, s1, s2, s3, dd, offc);
                 // u - 32: the offset leaves with the 16-element x sums
-                r = s0 * (scl * digits(d0) - 32.0f * x16[2 * blo]);
-                r = fmaf(s1, scl * digits(d1) - 32.0f * x16[2 * blo + 1], r);
-                r = fmaf(s2, sch * digits(d2) - 32.0f * x16[2 * bhi], r);
-                r = fmaf(s3, sch * digits(d3) - 32.0f * x16[2 * bhi + 1], r);
-                r *= dd;
+                float v = s0 * (scl * digits(d0) - 32.0f * x16[2 * blo]);
+                v = fmaf(s1, scl * digits(d1) - 32.0f * x16[2 * blo + 1], v);
+                v = fmaf(s2, sch * digits(d2) - 32.0f * x16[2 * bhi], v);
+                v = fmaf(s3, sch * digits(d3) - 32.0f * x16[2 * bhi + 1], v);
+                return v * dd;
+              };
+              if constexpr (WIDE) {
+                // the super-block's offset into its 16-byte unit is 2 sb mod 16, uniform per step: one
+                // scalar branch to a copy of the step with constant shifts
+                using std::integral_constant;
+                switch ((2 * p.sb) & 15) {
+                    case 0: r = q6_dot(integral_constant<int, 0>{}); break;
+                    case 2: r = q6_dot(integral_constant<int, 2>{}); break;
+                    case 4: r = q6_dot(integral_constant<int, 4>{}); break;
+                    case 6: r = q6_dot(integral_constant<int, 6>{}); break;
+                    case 8: r = q6_dot(integral_constant<int, 8>{}); break;
+                    case 10: r = q6_dot(integral_constant<int, 10>{}); break;
+                    case 12: r = q6_dot(integral_constant<int, 12>{}); break;
+                    default: r = q6_dot(integral_constant<int, 14>{}); break;
+                }
+              } else {
+                r = q6_dot(std::integral_constant<int, -1>{});
+              }
             } else if constexpr (FMT == T_Q8_0) {
                 const i32x4 b0 = {static_cast<int>(src[0]), static_cast<int>(src[1]), static_cast<int>(src[2]),
                                   static_cast<int>(src[3])};
@@ -914,7 +952,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
         if constexpr (FMT == T_Q6_K) {
             const int hs = 2 * (g & 1);  // qh bit pair of the low-nibble group; +4 for the high one
             uint32_t wl[8], wh[8];
-            q6_words(cur, wl, wh);
+            q6_words(cur, wl, wh, std::integral_constant<int, -1>{});
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const uint32_t ql = wl[t], qh = wh[t];
@@ -949,7 +987,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             const int gl = 8 * (g >> 1) + 2 * (g & 1), gh = gl + 4;  // 16-element unit index in the chunk
             const float *xs = xsum + p.sb * 16;
             float s0, s1, s2, s3, dd;
-            q6_scales(cur, s0, s1, s2, s3, dd);
+            q6_scales(cur, s0, s1, s2, s3, dd, std::integral_constant<int, -1>{});
             r = s0 * ((d[0] + d[1]) - 160.0f * xs[gl]);
             r = fmaf(s1, (d2[0] + d2[1]) - 160.0f * xs[gl + 1], r);
             r = fmaf(s2, (d[2] + d[3]) - 160.0f * xs[gh], r);
