@@ -91,6 +91,35 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
     const int t0 = blockIdx.y * kDTokens;
     const int ntt = min(4, (a.m - t0 + 15) / 16);  // token tiles of this grid row
     const uint8_t *rp[2] = {a.w0 + static_cast<size_t>(row) * a.rb, a.w1 + static_cast<size_t>(row) * a.rb};
+    const int rows = min(16, a.n - row0);
+
+    // kAdd over at most two token tiles (thread i writes output i alone): what is added before the
+    // product -- the output's current value and a batched MoE decode's routed results with their
+    // ids and weights -- depends on nothing this launch computes, so it is requested here, ahead of
+    // the weights, and the same adds in the same order run at the end (one round trip fewer after the
+    // sums)
+    constexpr int kPreRoutes = MODE == kAdd ? 8 : 1;
+    const bool pre = MODE == kAdd && ntt <= 2 && a.c.k <= kPreRoutes;  // uniform
+    const int ptl = tid >> 4, po = tid & 15, pt = t0 + ptl;
+    const bool pown = pre && tid < ntt * 256 && po < rows && pt < a.m;
+    float pre_y = 0.0f, pre_v[kPreRoutes], pre_w[kPreRoutes];
+    int pre_e[kPreRoutes];
+    if constexpr (MODE == kAdd) {
+        if (pown) {
+            pre_y = a.y[static_cast<size_t>(pt) * a.n + row0 + po];
+            if (a.c.yr) {  // uniform
+#pragma unroll
+                for (int r = 0; r < kPreRoutes; ++r) {
+                    if (r < a.c.k) {
+                        const int route = pt * a.c.k + r;
+                        pre_e[r] = a.c.ids[route];
+                        pre_w[r] = a.c.rw[route];
+                        pre_v[r] = a.c.yr[static_cast<size_t>(route) * a.n + row0 + po];
+                    }
+                }
+            }
+        }
+    }
 
     // one 16-token tile at a time (a tile's weights come again from the cache for the next one)
     for (int tt = 0; tt < ntt; ++tt) {
@@ -108,7 +137,6 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
     __syncthreads();
 
     // outputs: row o = row0 + (i % 16), token t0 + i / 16; D element r of lane l is token 4(l/16) + r
-    const int rows = min(16, a.n - row0);
     for (int i = tid; i < ntt * 256; i += kDThreads) {
         const int tl = i >> 4, o = i & 15;  // token within the grid row, row within the tile
         const int t = t0 + tl;
@@ -120,9 +148,25 @@ __global__ __launch_bounds__(kDThreads) void q4k_dense_kernel(const DenseArgs a)
             if constexpr (NW == 2) v1 += part[wv][NW - 1][tt][l][r];
         }
         float *yo = a.y + static_cast<size_t>(t) * a.n + row0 + o;
-        if constexpr (MODE == kSwiGLU) *yo = v0 / (1.0f + expf(-v0)) * v1;
-        else if constexpr (MODE == kAdd) add_out(a, yo, t, row0 + o, v0);
-        else *yo = v0;
+        if constexpr (MODE == kSwiGLU) {
+            *yo = v0 / (1.0f + expf(-v0)) * v1;
+        } else if constexpr (MODE == kAdd) {
+            if (pre) {  // (then i == tid)
+                float y = pre_y;
+                if (a.c.yr) {
+                    float total = 0.0f;  // routed_total's sum from the preloaded values
+#pragma unroll
+                    for (int r = 0; r < kPreRoutes; ++r)
+                        if (r < a.c.k && pre_e[r] >= 0 && pre_e[r] < a.c.n_experts) total = fmaf(pre_v[r], pre_w[r], total);
+                    y += total;
+                }
+                *yo = y + v0;
+            } else {
+                add_out(a, yo, t, row0 + o, v0);
+            }
+        } else {
+            *yo = v0;
+        }
     }
 }
 
