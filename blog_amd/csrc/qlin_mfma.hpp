@@ -53,6 +53,28 @@ struct ScaleDecoder {
 
 __device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
+// Loads from dword-aligned addresses of 16, 12 and 8 bytes, one instruction each (the HSA runtime runs
+// gfx950 with unaligned access enabled).  A 16-byte load on a dword boundary runs at the rate of an
+// aligned one; off a dword boundary the same load is much slower, so pieces that are only 2-byte
+// aligned are read from the dword before them and realigned in registers.
+__device__ __forceinline__ u32x4 ld16_a4(const uint8_t *p) {
+    u32x4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 4), 16);
+    return v;
+}
+typedef uint32_t u32x3_a4 __attribute__((ext_vector_type(3), aligned(4)));
+__device__ __forceinline__ void ld12_a4(const uint8_t *p, uint32_t (&v)[3]) {
+    const u32x3_a4 t = *reinterpret_cast<const u32x3_a4 *>(__builtin_assume_aligned(p, 4));
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+}
+__device__ __forceinline__ uint2 ld8_a4(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 4), 8);
+    return v;
+}
+
 // bits 0..3 of b to bit 0 of bytes 0..3 (the four shifted copies of b do not overlap): the fifth
 // bits of four Q5_0 elements, ready to join their nibbles
 __device__ __forceinline__ uint32_t spread4(uint32_t b) { return __umul24(b & 0xfu, 0x204081u) & 0x01010101u; }

@@ -50,7 +50,11 @@
 //     hold the low nibbles of 32-element group (g/2, g%2) and the high nibbles of group
 //     (g/2, g%2+2), whose top 2 bits come from the matching qh bytes; u = 6-bit value is carried
 //     as bf16(128 + u).  Scales change every 16 elements, so MFMAs 0-3 and 4-7 accumulate
-//     separately and the x sums are kept per 16; y += d sum sc (D - 160 X16).
+//     separately and the x sums are kept per 16; y += d sum sc (D - 160 X16).  On the int8 matrix
+//     cores lane group g = 2h + s instead takes positions 16s..16s+15 of all four 32-element
+//     column groups c of half h (ql bytes 64h + 16s and + 32, qh bytes 128 + 32h + 16s, so no
+//     byte is read by two lane groups), MFMA c carries column group c with u itself as B, and
+//     y += d sum_c sc (s_x D_c - 32 X16).
 //   Q5_0 (chunk = 4 blocks of 22 B, kernel.cu:1159-1175; int8 matrix cores only): lane group g
 //     decodes block g, q = nibble | (bit e of qh) << 4 as the int8 B operand; y += d (D - 16 X).
 //   Their blocks are only 2-byte aligned, so each lane loads aligned dwords and realigns them
@@ -369,10 +373,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     // Q4_K sub-blocks 2g (MFMAs 0, 1) and 2g + 1 (2, 3), Q4_0 blocks 2g and 2g + 1 likewise (their 4
     // x 16 bytes are 64 consecutive plane bytes), Q8_0 block g (MFMAs 0, 1: 32 bytes)
     const bool i8_on = (n >> 2) == g && (n & 3) < 3;
-    // (Q6_K: lane group g's low-nibble group starts (g >> 1) * 128 + (g & 1) * 32 into the chunk, its
-    // high-nibble group 64 further)
+    // (Q6_K: lane group g's elements of column group c start 128 (g >> 1) + 32 c + 16 (g & 1) into the
+    // chunk)
     const int8_t *a8 = planes + (n & 3) * KP +
-                       (K32 ? 32 * g : FMT == T_Q6_K ? (g >> 1) * 128 + (g & 1) * 32 : 64 * g);  // when i8_on
+                       (K32 ? 32 * g : FMT == T_Q6_K ? (g >> 1) * 128 + (g & 1) * 16 : 64 * g);  // when i8_on
     __shared__ u32x4 s_zero[4];
     const uint8_t *a_lo, *a_hi;
     int a_lo_st, a_hi_st;
@@ -459,6 +463,28 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             st.w[0] = h.x; st.w[1] = h.y; st.w[2] = h.z; st.w[3] = h.w;
             st.w[4] = qa.x; st.w[5] = qa.y; st.w[6] = qa.z; st.w[7] = qa.w;
             st.w[8] = qb.x; st.w[9] = qb.y; st.w[10] = qb.z; st.w[11] = qb.w;
+        } else if constexpr (FMT == T_Q6_K && I8) {
+            // Lane group g = 2h + s takes positions 16s .. 16s + 15 of all four 32-element column groups c
+            // of half h: ql bytes o = 64h + 16s (c = 0, 2: low and high nibbles) and o + 32 (c = 1, 3), qh
+            // bytes c0 = 128 + 32h + 16s (bits 2c, 2c + 1), and the half's scales sc[8h + 2c + s]; no byte
+            // is read by two lane groups.  Rows are whole dwords (an even number of super-blocks), so even
+            // super-blocks start on a dword and odd ones 2 bytes past one.  Every load is dword-aligned:
+            // the three pieces and 12 bytes at 192 + 8h, all from 2 bytes before them in an odd
+            // super-block.  The 12 bytes hold the half's 8 scales and, for h = 1, d; at their end an even
+            // super-block's h = 1 lanes read the next super-block's first 2 bytes, which exist (a row's last
+            // super-block is odd).  An odd super-block's pieces then lack their last 2 bytes: the first
+            // dword that another lane group of the row loaded (process).
+            const int h = g >> 1, o = 64 * h + 16 * (g & 1), c0 = 128 + 32 * h + 16 * (g & 1);
+            const uint8_t *qa = q - ((__builtin_amdgcn_readfirstlane(p.sb) & 1) ? 2 : 0);
+            const u32x4 la = ld16_a4(qa + o), lb = ld16_a4(qa + o + 32), qh = ld16_a4(qa + c0);
+            st.w[0] = la.x; st.w[1] = la.y; st.w[2] = la.z; st.w[3] = la.w;
+            st.w[5] = lb.x; st.w[6] = lb.y; st.w[7] = lb.z; st.w[8] = lb.w;
+            st.w[10] = qh.x; st.w[11] = qh.y; st.w[12] = qh.z; st.w[13] = qh.w;
+            uint32_t sv[3];
+            ld12_a4(qa + 192 + 8 * h, sv);
+            st.w[15] = sv[0];
+            st.w[16] = sv[1];
+            st.w[17] = sv[2];
         } else if constexpr (FMT == T_Q6_K) {
             // ql bytes [32g, 32g+32) and qh bytes [128+32h, +32) from the dwords at or 2 bytes before
             // them (rows are a multiple of 4 bytes, so odd super-blocks start 2 bytes in), then the
@@ -670,23 +696,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
 
     // Q6_K: dword t of this lane's ql and qh bytes (elements 4t..4t+3 of its low- and high-nibble
     // groups): from the 36 bytes at or 2 before them, or (wide rows) from the 48-byte window, first
-    // shifting by whole dwords (offset bits 3 and 2, uniform per step), then by bytes.  offc: the
-    // wide row's offset as a compile-time constant (std::integral_constant), or -1 to read it from the
-    // step
-    auto q6_words = [&](const Raw &cur, uint32_t (&ql)[8], uint32_t (&qh)[8], auto offc) {
-        constexpr int OFF = decltype(offc)::value;
+    // shifting by whole dwords (offset bits 3 and 2, uniform per step), then by bytes
+    auto q6_words = [&](const Raw &cur, uint32_t (&ql)[8], uint32_t (&qh)[8]) {
         const uint32_t off = cur.w[26] >> 16;
-        if constexpr (WIDE && OFF >= 0) {
-            // constant shifts: the dword shift selects registers, the byte shift (0 or 2) costs one
-            // v_alignbyte per dword or nothing
-            constexpr int D = OFF >> 2;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                ql[t] = (OFF & 3) ? __builtin_amdgcn_alignbyte(cur.w[t + D + 1], cur.w[t + D], OFF & 3) : cur.w[t + D];
-                qh[t] = (OFF & 3) ? __builtin_amdgcn_alignbyte(cur.w[12 + t + D + 1], cur.w[12 + t + D], OFF & 3)
-                                  : cur.w[12 + t + D];
-            }
-        } else if constexpr (WIDE) {
+        if constexpr (WIDE) {
             // (the dword shifts as bit-field merges under an all-ones or all-zero mask the compiler
             // cannot see through: as selects between neighbouring elements they would become an
             // element chosen by a computed index, which keeps the arrays in scratch)
@@ -720,11 +733,10 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     // Q6_K: this lane's four 16-element scales (sc[8h + 2(g & 1)], +1, +4, +5) and d.  Wide rows: the
     // 8-byte pieces of the 32-byte window hold the scale pairs at window offsets o = off + 8h + 2(g & 1)
     // and o + 4, d at off + 16; dword j of the window is in lane group j >> 1 (element j & 1)
-    auto q6_scales = [&](const Raw &cur, float &s0, float &s1, float &s2, float &s3, float &dd, auto offc) {
-        constexpr int OFF = decltype(offc)::value;
+    auto q6_scales = [&](const Raw &cur, float &s0, float &s1, float &s2, float &s3, float &dd) {
         uint32_t sa, sb, dw;
         if constexpr (WIDE) {
-            const int off = OFF >= 0 ? OFF : static_cast<int>(cur.w[26] >> 16);
+            const int off = static_cast<int>(cur.w[26] >> 16);
             const int o = off + 8 * (g >> 1) + 2 * (g & 1), j = o >> 2;
             const int la = 16 * (j >> 1) + n, lb = 16 * ((j + 1) >> 1) + n;
             const uint32_t ax = __shfl(cur.w[24], la), ay = __shfl(cur.w[25], la);
@@ -778,61 +790,96 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             auto digits = [](const i32x4 &d) { return digits_value(d); };
             float r;
             if constexpr (FMT == T_Q6_K) {
-              // 6-bit values u of the low-nibble group (elements 4t..4t+3 from ql/qh dword t) and of the
-              // high-nibble group; MFMA u carries one 16-element scale group: the low group's elements
-              // 0..15, 16..31, then the high group's
-              auto q6_dot = [&](auto offc) {
-                const int hs = 2 * (g & 1);
-                uint32_t lo[8], hi[8], wl[8], wh[8];
-                q6_words(cur, wl, wh, offc);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const uint32_t whs = wh[t] >> hs;  // the low group's 2 bits at 0, 1, the high group's at 4, 5
-                    lo[t] = (wl[t] & 0x0f0f0f0fu) | ((whs << 4) & 0x30303030u);
-                    hi[t] = ((wl[t] >> 4) & 0x0f0f0f0fu) | (whs & 0x30303030u);
-                }
-                auto vec = [](const uint32_t *v) {
-                    return i32x4{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]),
-                                 static_cast<int>(v[3])};
+                // MFMA c: the 6-bit values u of column group c at the lane group's 16 positions (elements
+                // 4t..4t+3 from dword t of the ql and qh pieces), one 16-element scale group.  ODD: the
+                // pieces and scales were read from 2 bytes before them (the load's layout).
+                // The value of x at lane group g ^ 1 / g ^ 2 of the same row (the swap's first result holds
+                // the partner's value in the odd / upper lane groups, its second in the others).  Every
+                // lane must run them, so their results are selected after the call, never by a
+                // conditional around it: a swap in a branch reads its partners with their lanes off.
+                auto from16 = [&](uint32_t x) {
+                    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+                    return static_cast<uint32_t>((g & 1) ? r[0] : r[1]);
                 };
-                const i32x4 *pq = reinterpret_cast<const i32x4 *>(
-                    i8_on ? a8 + p.sb * CE : reinterpret_cast<const int8_t *>(s_zero));
-                // A: the low group at +0, +16 bytes, the high group at +64, +80 (zero area: 64 bytes,
-                // so its lanes read it at +0, +16 twice)
-                const int hoff = i8_on ? 4 : 0;
-                const i32x4 d0 = mfma_i8(pq[0], vec(lo), i32x4{0, 0, 0, 0});
-                const i32x4 d1 = mfma_i8(pq[1], vec(lo + 4), i32x4{0, 0, 0, 0});
-                const i32x4 d2 = mfma_i8(pq[hoff], vec(hi), i32x4{0, 0, 0, 0});
-                const i32x4 d3 = mfma_i8(pq[hoff + 1], vec(hi + 4), i32x4{0, 0, 0, 0});
-                const int blo = p.sb * 8 + (g >> 1) * 4 + (g & 1), bhi = blo + 2;  // 32-element blocks
-                const float scl = sxp[blo], sch = sxp[bhi];
-                const float *x16 = sxp + K / 32;
-                float s0, s1, s2, s3, dd;
-                q6_scales(cur, s0, s1, s2, s3, dd, offc);
-                // u - 32: the offset leaves with the 16-element x sums
-                float v = s0 * (scl * digits(d0) - 32.0f * x16[2 * blo]);
-                v = fmaf(s1, scl * digits(d1) - 32.0f * x16[2 * blo + 1], v);
-                v = fmaf(s2, sch * digits(d2) - 32.0f * x16[2 * bhi], v);
-                v = fmaf(s3, sch * digits(d3) - 32.0f * x16[2 * bhi + 1], v);
-                return v * dd;
-              };
-              if constexpr (WIDE) {
-                // the super-block's offset into its 16-byte unit is 2 sb mod 16, uniform per step: one
-                // scalar branch to a copy of the step with constant shifts
-                using std::integral_constant;
-                switch ((2 * p.sb) & 15) {
-                    case 0: r = q6_dot(integral_constant<int, 0>{}); break;
-                    case 2: r = q6_dot(integral_constant<int, 2>{}); break;
-                    case 4: r = q6_dot(integral_constant<int, 4>{}); break;
-                    case 6: r = q6_dot(integral_constant<int, 6>{}); break;
-                    case 8: r = q6_dot(integral_constant<int, 8>{}); break;
-                    case 10: r = q6_dot(integral_constant<int, 10>{}); break;
-                    case 12: r = q6_dot(integral_constant<int, 12>{}); break;
-                    default: r = q6_dot(integral_constant<int, 14>{}); break;
-                }
-              } else {
-                r = q6_dot(std::integral_constant<int, -1>{});
-              }
+                auto from32 = [&](uint32_t x) {
+                    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+                    return static_cast<uint32_t>((g >> 1) ? r[0] : r[1]);
+                };
+                auto q6_dot = [&](auto oddc) {
+                    constexpr bool ODD = decltype(oddc)::value;
+                    const int s = g & 1;
+                    uint32_t tail[3] = {0u, 0u, 0u};
+                    if constexpr (ODD) {
+                        // the dword after each piece's window starts the window of the piece 16 bytes on
+                        // (the scales' window after the last qh piece): A of g + 1 or B of g - 1 for the A
+                        // pieces (lane group g ^ 1); for B and C the next lane group (g ^ 1 from an even
+                        // group, g ^ 3 from an odd one), which gives B or A / C, or C / the h = 0 scales
+                        const uint32_t a0 = cur.w[0], b0 = cur.w[5], c0 = cur.w[10], s0w = cur.w[15];
+                        tail[0] = from16(s ? a0 : b0);
+                        const uint32_t db = s ? b0 : ((g >> 1) ? a0 : c0), dc = g == 0 ? s0w : c0;
+                        const uint32_t b1 = from16(db), c1 = from16(dc);
+                        const uint32_t b3 = from32(b1), c3 = from32(c1);
+                        tail[1] = s ? b3 : b1;
+                        tail[2] = s ? c3 : c1;
+                    }
+                    uint32_t bq[4][4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        uint32_t la = cur.w[t], lb = cur.w[5 + t], qh = cur.w[10 + t];
+                        if constexpr (ODD) {
+                            la = __builtin_amdgcn_alignbyte(t < 3 ? cur.w[t + 1] : tail[0], cur.w[t], 2);
+                            lb = __builtin_amdgcn_alignbyte(t < 3 ? cur.w[6 + t] : tail[1], cur.w[5 + t], 2);
+                            qh = __builtin_amdgcn_alignbyte(t < 3 ? cur.w[11 + t] : tail[2], cur.w[10 + t], 2);
+                        }
+                        bq[0][t] = (la & M) | ((qh << 4) & 0x30303030u);
+                        bq[1][t] = (lb & M) | ((qh << 2) & 0x30303030u);
+                        bq[2][t] = ((la >> 4) & M) | (qh & 0x30303030u);
+                        bq[3][t] = ((lb >> 4) & M) | ((qh >> 2) & 0x30303030u);
+                    }
+                    auto vec = [](const uint32_t *v) {
+                        return i32x4{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]),
+                                     static_cast<int>(v[3])};
+                    };
+                    // A: column group c at +32c bytes (the zero area's lanes read its first 16 bytes)
+                    const i32x4 *pq = reinterpret_cast<const i32x4 *>(
+                        i8_on ? a8 + p.sb * CE : reinterpret_cast<const int8_t *>(s_zero));
+                    const int ast = i8_on ? 2 : 0;
+                    const i32x4 d0 = mfma_i8(pq[0], vec(bq[0]), i32x4{0, 0, 0, 0});
+                    const i32x4 d1 = mfma_i8(pq[ast], vec(bq[1]), i32x4{0, 0, 0, 0});
+                    const i32x4 d2 = mfma_i8(pq[2 * ast], vec(bq[2]), i32x4{0, 0, 0, 0});
+                    const i32x4 d3 = mfma_i8(pq[3 * ast], vec(bq[3]), i32x4{0, 0, 0, 0});
+                    // the half's scales sc[8h .. 8h + 7] and d: the h = 1 lanes hold d in the last of their
+                    // 12 bytes (low half, or high half after the odd super-block's 2-byte shift), the h = 0
+                    // lanes take it from the lane group 2 above
+                    uint32_t sw0 = cur.w[15], sw1 = cur.w[16];
+                    if constexpr (ODD) {
+                        sw0 = __builtin_amdgcn_alignbyte(cur.w[16], cur.w[15], 2);
+                        sw1 = __builtin_amdgcn_alignbyte(cur.w[17], cur.w[16], 2);
+                    }
+                    const uint32_t dh = from32(cur.w[17]);
+                    const uint32_t dw = (g >> 1) ? cur.w[17] : dh;
+                    const uint32_t db = (ODD ? dw >> 16 : dw) & 0xffffu;
+                    // x digit scales of the 32-element blocks 8 sb + 4h + c, x sums of the 16-element
+                    // groups 16 sb + 8h + 2c + s, weight scales sc[8h + 2c + s]
+                    const float4 sx = *reinterpret_cast<const float4 *>(sxp + p.sb * 8 + 4 * (g >> 1));
+                    const float *x16 = sxp + K / 32 + p.sb * 16 + 8 * (g >> 1) + s;
+                    const uint32_t sa = sw0 >> (8 * s), sb = sw1 >> (8 * s);
+                    const float s0 = static_cast<float>(static_cast<int8_t>(sa & 0xffu));
+                    const float s1 = static_cast<float>(static_cast<int8_t>((sa >> 16) & 0xffu));
+                    const float s2 = static_cast<float>(static_cast<int8_t>(sb & 0xffu));
+                    const float s3 = static_cast<float>(static_cast<int8_t>((sb >> 16) & 0xffu));
+                    const float dd = f16_bits_to_f32(db);
+                    // u - 32: the offset leaves with the 16-element x sums
+                    float v = s0 * (sx.x * digits(d0) - 32.0f * x16[0]);
+                    v = fmaf(s1, sx.y * digits(d1) - 32.0f * x16[2], v);
+                    v = fmaf(s2, sx.z * digits(d2) - 32.0f * x16[4], v);
+                    v = fmaf(s3, sx.w * digits(d3) - 32.0f * x16[6], v);
+                    return v * dd;
+                };
+                if (__builtin_amdgcn_readfirstlane(p.sb) & 1)  // a scalar branch: the swaps see every lane
+                    r = q6_dot(std::true_type{});
+                else
+                    r = q6_dot(std::false_type{});
             } else if constexpr (FMT == T_Q8_0) {
                 const i32x4 b0 = {static_cast<int>(src[0]), static_cast<int>(src[1]), static_cast<int>(src[2]),
                                   static_cast<int>(src[3])};
@@ -952,7 +999,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
         if constexpr (FMT == T_Q6_K) {
             const int hs = 2 * (g & 1);  // qh bit pair of the low-nibble group; +4 for the high one
             uint32_t wl[8], wh[8];
-            q6_words(cur, wl, wh, std::integral_constant<int, -1>{});
+            q6_words(cur, wl, wh);
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const uint32_t ql = wl[t], qh = wh[t];
@@ -987,7 +1034,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             const int gl = 8 * (g >> 1) + 2 * (g & 1), gh = gl + 4;  // 16-element unit index in the chunk
             const float *xs = xsum + p.sb * 16;
             float s0, s1, s2, s3, dd;
-            q6_scales(cur, s0, s1, s2, s3, dd, std::integral_constant<int, -1>{});
+            q6_scales(cur, s0, s1, s2, s3, dd);
             r = s0 * ((d[0] + d[1]) - 160.0f * xs[gl]);
             r = fmaf(s1, (d2[0] + d2[1]) - 160.0f * xs[gl + 1], r);
             r = fmaf(s2, (d[2] + d[3]) - 160.0f * xs[gh], r);
