@@ -74,6 +74,32 @@ __device__ __forceinline__ uint2 ld8_a4(const uint8_t *p) {
     __builtin_memcpy(&v, __builtin_assume_aligned(p, 4), 8);
     return v;
 }
+// N consecutive dwords from a dword-aligned address: 16-byte loads, then one of 12, 8 or 4 bytes
+template <int N>
+__device__ __forceinline__ void ld_dwords_a4(const uint8_t *p, uint32_t *w) {
+#pragma unroll
+    for (int i = 0; i + 4 <= N; i += 4) {
+        const u32x4 v = ld16_a4(p + 4 * i);
+        w[i] = v.x;
+        w[i + 1] = v.y;
+        w[i + 2] = v.z;
+        w[i + 3] = v.w;
+    }
+    constexpr int B = N - N % 4;
+    if constexpr (N % 4 == 3) {
+        uint32_t t[3];
+        ld12_a4(p + 4 * B, t);
+        w[B] = t[0];
+        w[B + 1] = t[1];
+        w[B + 2] = t[2];
+    } else if constexpr (N % 4 == 2) {
+        const uint2 t = ld8_a4(p + 4 * B);
+        w[B] = t.x;
+        w[B + 1] = t.y;
+    } else if constexpr (N % 4 == 1) {
+        w[B] = *reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p + 4 * B, 4));
+    }
+}
 
 // bits 0..3 of b to bit 0 of bytes 0..3 (the four shifted copies of b do not overlap): the fifth
 // bits of four Q5_0 elements, ready to join their nibbles

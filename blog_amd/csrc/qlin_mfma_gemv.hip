@@ -57,8 +57,9 @@
 //     y += d sum_c sc (s_x D_c - 32 X16).
 //   Q5_0 (chunk = 4 blocks of 22 B, kernel.cu:1159-1175; int8 matrix cores only): lane group g
 //     decodes block g, q = nibble | (bit e of qh) << 4 as the int8 B operand; y += d (D - 16 X).
-//   Their blocks are only 2-byte aligned, so each lane loads aligned dwords and realigns them
-//     with v_alignbyte_b32.
+//   Their blocks are only 2-byte aligned, so each lane loads the dword-aligned window around its
+//     bytes (16-byte loads on dword boundaries, which run at the rate of aligned ones; off a dword
+//     boundary they are much slower) and realigns it in registers.
 //
 // Routed experts (the per-token MoE, TensorTool.cpp:271-336 with kernel.cu:1340-1385, 2253-2287):
 // route r's weights are expert ids[r]'s.  The gate/up SwiGLU of k routes is the SwiGLU over k * ffn
@@ -504,10 +505,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
                     st.w[12 + 4 * k] = m.x; st.w[13 + 4 * k] = m.y; st.w[14 + 4 * k] = m.z; st.w[15 + 4 * k] = m.w;
                 }
             } else {
-#pragma unroll
-                for (int k = 0; k < 9; ++k) st.w[k] = ld4(q - sh + 32 * g + 4 * k);
-#pragma unroll
-                for (int k = 0; k < 9; ++k) st.w[9 + k] = ld4(q - sh + 128 + 32 * h + 4 * k);
+                ld_dwords_a4<9>(q - sh + 32 * g, st.w);
+                ld_dwords_a4<9>(q - sh + 128 + 32 * h, st.w + 9);
             }
             if constexpr (WIDE) {
                 // the 32 bytes from the 16-byte unit holding scale byte 0 (inside the row, as rows
@@ -525,14 +524,12 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             // block g = bytes [22g, 22g+22), from the dword at or 2 bytes before it (6 dwords, inside
             // the chunk for every g)
             const uint8_t *b = q + 22 * g - 2 * (g & 1);
-#pragma unroll
-            for (int k = 0; k < 6; ++k) st.w[k] = ld4(b + 4 * k);
+            ld_dwords_a4<6>(b, st.w);
         } else {
             // Q4_0: blocks 2g, 2g+1 = bytes [36g, 36g+36).  Q8_0: block g = bytes [34g, 34g+34), read
             // from the dword at or 2 bytes before it.
             const uint8_t *b = FMT == T_Q4_0 ? q + 36 * g : q + 34 * g - 2 * (g & 1);
-#pragma unroll
-            for (int k = 0; k < 9; ++k) st.w[k] = ld4(b + 4 * k);
+            ld_dwords_a4<9>(b, st.w);
         }
     };
 
@@ -779,9 +776,11 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
 #pragma unroll
                 for (int k = 0; k < 4; ++k) src[4 + k] = cur.w[5 + k];
             } else {
-                const bool odd = g & 1;  // odd blocks start 2 bytes into the first dword
+                // odd blocks' bytes start at the second dword, even ones' 2 bytes into the first: one
+                // byte permute per dword with a per-lane selector
+                const uint32_t sel = (g & 1) ? 0x07060504u : 0x05040302u;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) src[k] = odd ? cur.w[k + 1] : __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2);
+                for (int k = 0; k < 8; ++k) src[k] = __builtin_amdgcn_perm(cur.w[k + 1], cur.w[k], sel);
             }
             auto nib = [&](int k0, int sh) {
                 return i32x4{static_cast<int>((src[k0] >> sh) & M), static_cast<int>((src[k0 + 1] >> sh) & M),

@@ -565,8 +565,7 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 st.w[8] = qb.x; st.w[9] = qb.y; st.w[10] = qb.z; st.w[11] = qb.w;
             } else {
                 // nd + 1 dwords from the one holding d (d_dw + nd is at most the chunk's last dword)
-#pragma unroll
-                for (int k = 0; k <= F::nd; ++k) st.w[1 + k] = *reinterpret_cast<const uint32_t *>(q + 4 * (d_dw + k));
+                ld_dwords_a4<F::nd + 1>(q + 4 * d_dw, st.w + 1);
             }
         };
 
