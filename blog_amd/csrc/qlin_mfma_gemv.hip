@@ -286,16 +286,18 @@ struct Mats {
 
 
 // A lane's raw bytes of one step: Q4_K the 16-byte header and 32 bytes of nibbles; the 32-weight
-// formats 9 aligned dwords covering the lane's blocks.
+// formats the 9 (Q5_0: 6) dwords from the one at or 2 bytes before the lane's blocks; Q6_K on the
+// int8 matrix cores three 16-byte pieces and 12 scale bytes, on the bf16 ones 48-byte windows.
 struct Raw {
     uint32_t w[27];
 };
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
 
-// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  WIDE (Q6_K): every super-block lies in
-// whole 16-byte units of its row (16-aligned rows of 8k super-blocks), so its ql and qh are read as
-// three aligned 16-byte pieces each.  ROUTED: the routed-expert forms (a.ids).
+// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  WIDE (Q6_K on the bf16 matrix cores):
+// every super-block lies in whole 16-byte units of its row (16-aligned rows of 8k super-blocks), so
+// its ql and qh are read as three aligned 16-byte pieces each.  ROUTED: the routed-expert forms
+// (a.ids).
 template <int FMT, bool SWIGLU, int XR, bool WIDE = false, bool ROUTED = false>
 __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const float *lx, const uint8_t *lw0, size_t lrb,
                                                                        int lnsb, int ltotal, int lrows_q, int lrows_r,
@@ -1274,7 +1276,8 @@ int sum_elems(int type) { return type == T_Q6_K ? kSumElems<T_Q6_K> : kSumElems<
 bool mfma_type(int type) {
     return type == T_Q4_K || type == T_Q4_0 || type == T_Q8_0 || type == T_Q6_K || type == T_Q5_0;
 }
-// Q4_K loads 16-byte pieces; the 32-weight formats and Q6_K aligned dwords
+// Q4_K loads 16-byte pieces at 16-byte boundaries; the 32-weight formats and Q6_K load at dword
+// boundaries (16-byte loads among them)
 size_t weight_align(int type) { return type == T_Q4_K ? 16 : 4; }
 uint32_t magic_of(int d) { return d > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + d - 1) / d) : 0u; }
 

@@ -1041,7 +1041,7 @@ hipError_t launch_stream(const StreamPlan &p, const StreamArgs &a, hipStream_t s
     return p.nq == 4 ? launch_stream_nq<FMT, 4, SW, GRP>(p, a, s) : launch_stream_nq<FMT, 2, SW, GRP>(p, a, s);
 }
 
-// The streaming down kernel reads Q5_0 / Q8_0 4-block chunks as aligned dwords (88 and 136 bytes,
+// The streaming down kernel reads Q5_0 / Q8_0 4-block chunks at dword boundaries (88 and 136 bytes,
 // multiples of 4, so every chunk starts 4-aligned once the weights do), and Q4_K super-blocks as
 // 16-byte pieces (144 bytes = 9 x 16).
 bool down_stream_ok(int type, const uint8_t *w, size_t eb, size_t rb, int ffn) {
