@@ -955,7 +955,7 @@ def wl_moe_token(args, torch, qlin, gen):
                                 "gate/up, [2048, 2816] down): 3 launches; separate calls: 4"},
         "roofline": {"bound": "hbm", "achieved": round(sw_bytes / us_sw / 1e3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_bytes / us_sw / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "mfma_gemv_kernel<12, true, 1, false, true> (routed gate/up SwiGLU, 6 x 2 x [1408, 2048])",
+                     "kernel": "mfma_gemv_kernel<12, true, 1, true> (routed gate/up SwiGLU, 6 x 2 x [1408, 2048])",
                      "avg_launch_us": round(us_sw, 3), "algorithmic_bytes_per_launch": sw_bytes},
     }
     if not args.no_cpu:

@@ -46,15 +46,11 @@
 //   Q8_0 (chunk = 4 blocks of 34 B, kernel.cu:1178-1185): q + 128 = 16 h + l splits each int8
 //     weight into two nibbles, so block g becomes the nibble pair of a Q4_K sub-block pair with the
 //     same x slice in both; y += d (D_l + 16 D_h - 2304 X).
-//   Q6_K (chunk = one 210 B super-block, kernel.cu:1122-1156): the 32 ql bytes of lane group g
-//     hold the low nibbles of 32-element group (g/2, g%2) and the high nibbles of group
-//     (g/2, g%2+2), whose top 2 bits come from the matching qh bytes; u = 6-bit value is carried
-//     as bf16(128 + u).  Scales change every 16 elements, so MFMAs 0-3 and 4-7 accumulate
-//     separately and the x sums are kept per 16; y += d sum sc (D - 160 X16).  On the int8 matrix
-//     cores lane group g = 2h + s instead takes positions 16s..16s+15 of all four 32-element
-//     column groups c of half h (ql bytes 64h + 16s and + 32, qh bytes 128 + 32h + 16s, so no
-//     byte is read by two lane groups), MFMA c carries column group c with u itself as B, and
-//     y += d sum_c sc (s_x D_c - 32 X16).
+//   Q6_K (chunk = one 210 B super-block, kernel.cu:1122-1156; int8 matrix cores only): lane group
+//     g = 2h + s takes positions 16s..16s+15 of all four 32-element column groups c of half h (ql
+//     bytes 64h + 16s and + 32, qh bytes 128 + 32h + 16s, so no byte is read by two lane groups);
+//     MFMA c carries column group c, one 16-element scale group, with the 6-bit u itself as B;
+//     the x sums are kept per 16; y += d sum_c sc (s_x D_c - 32 X16).
 //   Q5_0 (chunk = 4 blocks of 22 B, kernel.cu:1159-1175; int8 matrix cores only): lane group g
 //     decodes block g, q = nibble | (bit e of qh) << 4 as the int8 B operand; y += d (D - 16 X).
 //   Their blocks are only 2-byte aligned, so each lane loads the dword-aligned window around its
@@ -126,9 +122,6 @@ constexpr int threads_for(bool swiglu) { return 64 * waves_for(swiglu); }
 // bf16 one, which the long x of a down projection (K = 18944) does not repay.
 #ifndef QLIN_MFMA_I8
 #define QLIN_MFMA_I8 3
-#endif
-#ifndef QLIN_MFMA_I8_Q6K
-#define QLIN_MFMA_I8_Q6K 1
 #endif
 #ifndef QLIN_MFMA_FINAL_UNROLL
 #define QLIN_MFMA_FINAL_UNROLL 4  // batches the final per-row sum's LDS reads (same order of adds)
@@ -294,11 +287,8 @@ struct Raw {
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
 
-// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  WIDE (Q6_K on the bf16 matrix cores):
-// every super-block lies in whole 16-byte units of its row (16-aligned rows of 8k super-blocks), so
-// its ql and qh are read as three aligned 16-byte pieces each.  ROUTED: the routed-expert forms
-// (a.ids).
-template <int FMT, bool SWIGLU, int XR, bool WIDE = false, bool ROUTED = false>
+// XR: float4 loads of x per thread (K/4 <= XR * kThreads).  ROUTED: the routed-expert forms (a.ids).
+template <int FMT, bool SWIGLU, int XR, bool ROUTED = false>
 __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const float *lx, const uint8_t *lw0, size_t lrb,
                                                                        int lnsb, int ltotal, int lrows_q, int lrows_r,
                                                                        uint32_t lmagic, int lgrid, int lnmat,
@@ -313,8 +303,8 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     // I8 (Q4_K): x as three base-128 int8 digits per element in planes [3][K] and (scale, sum of x)
     // per 32 elements, in no more LDS than the bf16 layout takes (3 KP + K/4 against 4 KX + K/8 bytes).
     // Q5_0 has only this form.
-    constexpr bool I8 = FMT == T_Q5_0 ||
-                        ((FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0 || (FMT == T_Q6_K && QLIN_MFMA_I8_Q6K)) &&
+    constexpr bool I8 = FMT == T_Q5_0 || FMT == T_Q6_K ||
+                        ((FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q8_0) &&
                          (QLIN_MFMA_I8 == 2 || (QLIN_MFMA_I8 == 1 && SWIGLU) || (QLIN_MFMA_I8 == 3 && XR <= 2)));
     constexpr bool K32 = FMT == T_Q8_0 || FMT == T_Q5_0;  // 128-weight chunks: lane group g, block g
     // The parts (digit planes) are kXPad bytes longer than K values: an A operand read gathers
@@ -357,12 +347,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     const ScaleDecoder dec(g);
     const Mats mats(a, ld);
 
-    // A-operand role of this lane: row i = n holds part (i & 1) of sub-block i >> 1, which is
-    // carried by the slots of lane-group g only when (i >> 2) == g.
-    const bool a_active = (n >> 2) == g;
-    const bool a_high = (n >> 1) & 1;        // sub-block 2g+1: slots 4..7
-    const int a_part = n & 1;
-    // Q4_K, Q4_0 and Q8_0 take another slot order: every MFMA gives lane group g's 8 slots to 8
+    // bf16 A operand (Q4_K, Q4_0, Q8_0): every MFMA gives lane group g's 8 slots to 8
     // consecutive weights of one 32-weight unit ("sub-block" j of the D rows).  MFMAs 0..3 carry
     // unit 2g, 4..7 unit 2g+1:
     //   Q4_K: the low / high nibbles of the pair's bytes 8t..8t+7 (sub-blocks 2g, 2g+1);
@@ -371,7 +356,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     // Row n of A (part n & 1 of unit n >> 1) then holds x in all 8 slots of MFMAs 0..3 when
     // n >> 1 == 2g, of MFMAs 4..7 when n >> 1 == 2g + 1, and zeros otherwise, so each A operand is
     // 16 bytes read from the staged x or from a zero area (stride 0), with no selects.
-    constexpr bool kDirectA = FMT != T_Q6_K;
+    const int a_part = n & 1;
     // I8 A operand: row n is digit n & 3 (3: none) of the 32-element units of lane group g = n >> 2:
     // Q4_K sub-blocks 2g (MFMAs 0, 1) and 2g + 1 (2, 3), Q4_0 blocks 2g and 2g + 1 likewise (their 4
     // x 16 bytes are 64 consecutive plane bytes), Q8_0 block g (MFMAs 0, 1: 32 bytes)
@@ -488,40 +473,6 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             st.w[15] = sv[0];
             st.w[16] = sv[1];
             st.w[17] = sv[2];
-        } else if constexpr (FMT == T_Q6_K) {
-            // ql bytes [32g, 32g+32) and qh bytes [128+32h, +32) from the dwords at or 2 bytes before
-            // them (rows are a multiple of 4 bytes, so odd super-blocks start 2 bytes in), then the
-            // lane's 4 scales and d as 16-bit loads
-            // (wide rows: the 48 bytes from the 16-byte unit holding the first byte, w[0..11] and
-            // w[12..23], with the offset into that unit, 0..14)
-            const int h = g >> 1;
-            // Wide rows start 16-aligned, so super-block sb starts 210 sb = 2 sb (mod 16) into a unit:
-            // an offset from the step, not from the pointer's bits, which keeps q a global pointer
-            // (masking its bits makes the loads flat ones, whose count a wait for LDS results shares)
-            const int sh = WIDE ? (2 * p.sb) & 15 : static_cast<int>(reinterpret_cast<uintptr_t>(q) & 3u);
-            if constexpr (WIDE) {
-#pragma unroll
-                for (int k = 0; k < 3; ++k) {
-                    const u32x4 l = ld16(q - sh + 32 * g + 16 * k), m = ld16(q - sh + 128 + 32 * h + 16 * k);
-                    st.w[4 * k] = l.x; st.w[4 * k + 1] = l.y; st.w[4 * k + 2] = l.z; st.w[4 * k + 3] = l.w;
-                    st.w[12 + 4 * k] = m.x; st.w[13 + 4 * k] = m.y; st.w[14 + 4 * k] = m.z; st.w[15 + 4 * k] = m.w;
-                }
-            } else {
-                ld_dwords_a4<9>(q - sh + 32 * g, st.w);
-                ld_dwords_a4<9>(q - sh + 128 + 32 * h, st.w + 9);
-            }
-            if constexpr (WIDE) {
-                // the 32 bytes from the 16-byte unit holding scale byte 0 (inside the row, as rows
-                // end on a unit boundary), 8 per lane group; the lanes gather theirs in process
-                const uint2 sv = *reinterpret_cast<const uint2 *>(q - sh + 192 + 8 * g);
-                st.w[24] = sv.x;
-                st.w[25] = sv.y;
-                st.w[26] = static_cast<uint32_t>(sh) << 16;
-            } else {
-                st.w[24] = *reinterpret_cast<const uint16_t *>(q + 192 + 8 * h + 2 * (g & 1));
-                st.w[25] = *reinterpret_cast<const uint16_t *>(q + 196 + 8 * h + 2 * (g & 1));
-                st.w[26] = *reinterpret_cast<const uint16_t *>(q + 208) | (static_cast<uint32_t>(sh) << 16);
-            }
         } else if constexpr (FMT == T_Q5_0) {
             // block g = bytes [22g, 22g+22), from the dword at or 2 bytes before it (6 dwords, inside
             // the chunk for every g)
@@ -692,69 +643,6 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
     __syncthreads();
 
     u32x4 aop[8];
-
-    // Q6_K: dword t of this lane's ql and qh bytes (elements 4t..4t+3 of its low- and high-nibble
-    // groups): from the 36 bytes at or 2 before them, or (wide rows) from the 48-byte window, first
-    // shifting by whole dwords (offset bits 3 and 2, uniform per step), then by bytes
-    auto q6_words = [&](const Raw &cur, uint32_t (&ql)[8], uint32_t (&qh)[8]) {
-        const uint32_t off = cur.w[26] >> 16;
-        if constexpr (WIDE) {
-            // (the dword shifts as bit-field merges under an all-ones or all-zero mask the compiler
-            // cannot see through: as selects between neighbouring elements they would become an
-            // element chosen by a computed index, which keeps the arrays in scratch)
-            uint32_t m8 = 0u - ((off >> 3) & 1u), m4 = 0u - ((off >> 2) & 1u);
-            asm("" : "+v"(m8));
-            asm("" : "+v"(m4));
-            uint32_t c[10], e[10];
-#pragma unroll
-            for (int j = 0; j < 10; ++j) {
-                c[j] = (cur.w[j + 2] & m8) | (cur.w[j] & ~m8);
-                e[j] = (cur.w[14 + j] & m8) | (cur.w[12 + j] & ~m8);
-            }
-#pragma unroll
-            for (int j = 0; j < 9; ++j) {
-                c[j] = (c[j + 1] & m4) | (c[j] & ~m4);
-                e[j] = (e[j + 1] & m4) | (e[j] & ~m4);
-            }
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                ql[t] = __builtin_amdgcn_alignbyte(c[t + 1], c[t], off & 3u);
-                qh[t] = __builtin_amdgcn_alignbyte(e[t + 1], e[t], off & 3u);
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                ql[t] = __builtin_amdgcn_alignbyte(cur.w[t + 1], cur.w[t], off);
-                qh[t] = __builtin_amdgcn_alignbyte(cur.w[10 + t], cur.w[9 + t], off);
-            }
-        }
-    };
-    // Q6_K: this lane's four 16-element scales (sc[8h + 2(g & 1)], +1, +4, +5) and d.  Wide rows: the
-    // 8-byte pieces of the 32-byte window hold the scale pairs at window offsets o = off + 8h + 2(g & 1)
-    // and o + 4, d at off + 16; dword j of the window is in lane group j >> 1 (element j & 1)
-    auto q6_scales = [&](const Raw &cur, float &s0, float &s1, float &s2, float &s3, float &dd) {
-        uint32_t sa, sb, dw;
-        if constexpr (WIDE) {
-            const int off = static_cast<int>(cur.w[26] >> 16);
-            const int o = off + 8 * (g >> 1) + 2 * (g & 1), j = o >> 2;
-            const int la = 16 * (j >> 1) + n, lb = 16 * ((j + 1) >> 1) + n;
-            const uint32_t ax = __shfl(cur.w[24], la), ay = __shfl(cur.w[25], la);
-            const uint32_t bx = __shfl(cur.w[24], lb), by = __shfl(cur.w[25], lb);
-            sa = ((j & 1) ? ay : ax) >> (8 * (o & 3));
-            sb = ((j & 1) ? bx : by) >> (8 * (o & 3));
-            const int jd = (off + 16) >> 2;
-            dw = __shfl((jd & 1) ? cur.w[25] : cur.w[24], 16 * (jd >> 1) + n) >> (8 * (off & 3));
-        } else {
-            sa = cur.w[24];
-            sb = cur.w[25];
-            dw = cur.w[26];
-        }
-        s0 = static_cast<float>(static_cast<int8_t>(sa & 0xffu));
-        s1 = static_cast<float>(static_cast<int8_t>((sa >> 8) & 0xffu));
-        s2 = static_cast<float>(static_cast<int8_t>(sb & 0xffu));
-        s3 = static_cast<float>(static_cast<int8_t>((sb >> 8) & 0xffu));
-        dd = f16_bits_to_f32(dw & 0xffffu);
-    };
 
     // One step: the 16 rows' dots with super-block sb, parked in LDS (each (row, matrix, sb) slot is
     // written by exactly one step; a global store here would share vmcnt with the weight stream).
@@ -950,36 +838,13 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
         }
         // A operands of this chunk (x only): the lane's 32 values of its part / sub-block (Q8_0: the
         // block both nibble sub-blocks of the pair come from).
-        if constexpr (kDirectA) {
+        {
             const u32x4 *pl = reinterpret_cast<const u32x4 *>(a_lo + p.sb * a_lo_st);
             const u32x4 *ph = reinterpret_cast<const u32x4 *>(a_hi + p.sb * a_hi_st);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 aop[t] = pl[t];
                 aop[4 + t] = ph[t];
-            }
-        } else {
-            uint32_t dw[16];
-            if (a_active) {
-                // Q6_K sub-block j = n >> 1 is (half j/4, group (j/2)%2 + 2 (j%2)) of 32 elements
-                const int j = n >> 1;
-                const int xo = p.sb * CE + (j >> 2) * 128 + (((j >> 1) & 1) + 2 * (j & 1)) * 32;
-                const uint4 *src = reinterpret_cast<const uint4 *>(xpart + a_part * KX + xo);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint4 v = src[q];
-                    dw[4 * q] = v.x; dw[4 * q + 1] = v.y; dw[4 * q + 2] = v.z; dw[4 * q + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) dw[q] = 0u;
-            }
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                aop[t].x = a_high ? 0u : dw[2 * t];
-                aop[t].y = a_high ? 0u : dw[2 * t + 1];
-                aop[t].z = a_high ? dw[2 * t] : 0u;
-                aop[t].w = a_high ? dw[2 * t + 1] : 0u;
             }
         }
         // the 8 dwords of nibbles this lane feeds to the MFMAs
@@ -996,20 +861,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
                 qv[k] = (odd ? cur.w[k + 1] : __builtin_amdgcn_alignbyte(cur.w[k + 1], cur.w[k], 2)) ^ 0x80808080u;
         }
         f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4 d2 = {0.0f, 0.0f, 0.0f, 0.0f};  // Q6_K: elements 16..31 of each group
-        if constexpr (FMT == T_Q6_K) {
-            const int hs = 2 * (g & 1);  // qh bit pair of the low-nibble group; +4 for the high one
-            uint32_t wl[8], wh[8];
-            q6_words(cur, wl, wh);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const uint32_t ql = wl[t], qh = wh[t];
-                const uint32_t lo = (ql & 0x0f0f0f0fu) | (((qh >> hs) & 0x03030303u) << 4);
-                const uint32_t hi = ((ql >> 4) & 0x0f0f0f0fu) | (((qh >> (hs + 4)) & 0x03030303u) << 4);
-                if (t < 4) d = mfma(aop[t], weights_operand2(lo, hi), d);
-                else d2 = mfma(aop[t], weights_operand2(lo, hi), d2);
-            }
-        } else if constexpr (FMT == T_Q4_0) {
+        if constexpr (FMT == T_Q4_0) {
             // block 2g + (t >> 2): low nibbles of bytes 0..7, 8..15 (elements 0..15), then high nibbles
             constexpr uint32_t M = 0x0f0f0f0fu;
 #pragma unroll
@@ -1030,18 +882,7 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             }
         }
         float r;
-        if constexpr (FMT == T_Q6_K) {
-            // groups of this lane: low nibbles (half h, group p), high nibbles (h, p + 2); x sums per 16
-            const int gl = 8 * (g >> 1) + 2 * (g & 1), gh = gl + 4;  // 16-element unit index in the chunk
-            const float *xs = xsum + p.sb * 16;
-            float s0, s1, s2, s3, dd;
-            q6_scales(cur, s0, s1, s2, s3, dd);
-            r = s0 * ((d[0] + d[1]) - 160.0f * xs[gl]);
-            r = fmaf(s1, (d2[0] + d2[1]) - 160.0f * xs[gl + 1], r);
-            r = fmaf(s2, (d[2] + d[3]) - 160.0f * xs[gh], r);
-            r = fmaf(s3, (d2[2] + d2[3]) - 160.0f * xs[gh + 1], r);
-            r *= dd;
-        } else if constexpr (FMT == T_Q4_K) {
+        if constexpr (FMT == T_Q4_K) {
             const float2 xs = *reinterpret_cast<const float2 *>(xsum + p.sb * 8 + 2 * g);
             uint32_t scp, mp;
             dec(cur.w[1], cur.w[2], cur.w[3], scp, mp);
@@ -1228,9 +1069,9 @@ struct Kern {
     size_t static_lds = kMaxLds;
     unsigned threads = 0;
 };
-template <int FMT, bool SW, int XR, bool WIDE, bool R>
+template <int FMT, bool SW, int XR, bool R>
 Kern kern() {
-    const void *fn = reinterpret_cast<const void *>(&mfma_gemv_kernel<FMT, SW, XR, WIDE, R>);
+    const void *fn = reinterpret_cast<const void *>(&mfma_gemv_kernel<FMT, SW, XR, R>);
     static const size_t lds = [fn] {
         hipFuncAttributes fa{};
         return hipFuncGetAttributes(&fa, fn) == hipSuccess ? fa.sharedSizeBytes : kMaxLds;
@@ -1238,37 +1079,33 @@ Kern kern() {
     return Kern{fn, lds, static_cast<unsigned>(threads_for(SW))};
 }
 // x loads per thread from K; routed launches have at most 4 (K <= 16 * threads)
-template <int FMT, bool SW, bool WIDE, bool R>
+template <int FMT, bool SW, bool R>
 Kern kern_xr(int k) {
     constexpr int kThreads = threads_for(SW);
     const int need = (k / 4 + kThreads - 1) / kThreads;
-    if (need <= 1) return kern<FMT, SW, 1, WIDE, R>();
-    if (need <= 2) return kern<FMT, SW, 2, WIDE, R>();
-    if (need <= 4) return kern<FMT, SW, 4, WIDE, R>();
+    if (need <= 1) return kern<FMT, SW, 1, R>();
+    if (need <= 2) return kern<FMT, SW, 2, R>();
+    if (need <= 4) return kern<FMT, SW, 4, R>();
     if constexpr (!R) {
-        if (need <= 6) return kern<FMT, SW, 6, WIDE, R>();
-        if (need <= kMaxXr) return kern<FMT, SW, kMaxXr, WIDE, R>();
+        if (need <= 6) return kern<FMT, SW, 6, R>();
+        if (need <= kMaxXr) return kern<FMT, SW, kMaxXr, R>();
     }
     return Kern{};
 }
 template <bool SW, bool R>
-Kern kern_for(int type, bool wide, int k) {
+Kern kern_for(int type, int k) {
     switch (type) {
-        case T_Q4_K: return kern_xr<T_Q4_K, SW, false, R>(k);
-        case T_Q4_0: return kern_xr<T_Q4_0, SW, false, R>(k);
-        case T_Q8_0: return kern_xr<T_Q8_0, SW, false, R>(k);
-        case T_Q5_0: return kern_xr<T_Q5_0, SW, false, R>(k);
-        case T_Q6_K:
-            if constexpr (!R) {
-                if (wide) return kern_xr<T_Q6_K, SW, true, R>(k);
-            }
-            return kern_xr<T_Q6_K, SW, false, R>(k);
+        case T_Q4_K: return kern_xr<T_Q4_K, SW, R>(k);
+        case T_Q4_0: return kern_xr<T_Q4_0, SW, R>(k);
+        case T_Q8_0: return kern_xr<T_Q8_0, SW, R>(k);
+        case T_Q5_0: return kern_xr<T_Q5_0, SW, R>(k);
+        case T_Q6_K: return kern_xr<T_Q6_K, SW, R>(k);
         default: return Kern{};
     }
 }
-Kern kernel_for(int type, bool swiglu, bool routed, bool wide, int k) {
-    if (routed) return swiglu ? kern_for<true, true>(type, false, k) : kern_for<false, true>(type, false, k);
-    return swiglu ? kern_for<true, false>(type, wide, k) : kern_for<false, false>(type, wide, k);
+Kern kernel_for(int type, bool swiglu, bool routed, int k) {
+    if (routed) return swiglu ? kern_for<true, true>(type, k) : kern_for<false, true>(type, k);
+    return swiglu ? kern_for<true, false>(type, k) : kern_for<false, false>(type, k);
 }
 
 int chunk_elems(int type) { return type == T_Q8_0 || type == T_Q5_0 ? 128 : 256; }
@@ -1281,13 +1118,6 @@ bool mfma_type(int type) {
 size_t weight_align(int type) { return type == T_Q4_K ? 16 : 4; }
 uint32_t magic_of(int d) { return d > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + d - 1) / d) : 0u; }
 
-// Q6_K rows of whole 16-byte units from 16-aligned bases take the 16-byte-piece form
-bool q6_wide(int type, const MfmaArgs &a, int nw) {
-    bool wide = type == T_Q6_K && a.row_bytes % 16 == 0;
-    for (int i = 0; i < nw; ++i) wide = wide && aligned16(a.w[i]);
-    return wide;
-}
-
 // The launch's kernel and plan, or no kernel when the shape does not fit (callers then take the
 // per-element kernels).
 struct Launch {
@@ -1297,7 +1127,7 @@ struct Launch {
 };
 Launch prepare(int type, const MfmaArgs &a, int k, bool swiglu, bool routed) {
     Launch l;
-    l.k = kernel_for(type, swiglu, routed, !routed && q6_wide(type, a, swiglu ? 2 : a.nmat), k);
+    l.k = kernel_for(type, swiglu, routed, k);
     if (!l.k.fn) return l;
     l.p = make_plan(a.total, k, a.nsb, swiglu, sum_elems(type));
     l.ok = plan::gemv_fits(l.p, l.k.static_lds);
