@@ -195,8 +195,9 @@ constexpr int kRouteWaveFloats = 64;
 // 256 threads each), the tokens' x and then their partials (per tile 8 super-block slots x 2 matrices
 // x 64 lanes of 4 floats) in the dynamic LDS.  A workgroup's cost for them, in the units of
 // StepFmt<T_Q4_K> (about 0.047 us of a workgroup's time each): staging x, then each tile
-// (per-workgroup trace at 16 tokens, two tiles per workgroup: x staged 5.2 us after the start, the
-// tiles done 11 us later; at a tile cost of 150 those workgroups ended about 1 us before the others).
+// (per-workgroup trace at 16 tokens, two tiles per workgroup: x staged 6.0 us after the start, the
+// tiles done 10 us later; with x rows unpadded, staging took 5.3 us and the tiles 11.7 more, their
+// 16 lanes reading one bank, and the costs were 125 and 135).
 // Two tiles per workgroup halve the staging (C5 step 89.2 -> 88.2 us against one); more, in this
 // kernel's 128 VGPRs, spill.
 #ifndef QLIN_SHARED_TILES
@@ -204,7 +205,7 @@ constexpr int kRouteWaveFloats = 64;
 #endif
 constexpr int kSharedMaxTiles = 2;
 constexpr size_t kSharedPartBytes = 8 * 2 * 64 * 16;
-constexpr int kSharedStageCost = 125, kSharedTileCost = 135;
+constexpr int kSharedStageCost = 140, kSharedTileCost = 115;
 
 // 64-bit integer division is a sequence of a few hundred scalar instructions, run by every wave and
 // shared by the 16 waves of a CU: both helpers take 32-bit arithmetic when the operands allow
@@ -298,12 +299,22 @@ __global__ __launch_bounds__(kSThreads) void stream_kernel(const StreamArgs a) {
                 rp[t] = wm + static_cast<size_t>(min((t0 + min(t, nt - 1)) * 16 + n, a.sh_rows - 1)) * a.sh_rb;
             Q4KRaw cur[1];
             if (slot < nsb) load_q4k(cur[0], rp[0] + static_cast<size_t>(slot) * 144, g);
-            float *sx = reinterpret_cast<float *>(smem);  // [sh_tokens][K]
-            const int nx4 = a.sh_tokens * a.K / 4;
-            for (int i = tid; i < nx4; i += kSThreads)
-                reinterpret_cast<float4 *>(sx)[i] = reinterpret_cast<const float4 *>(a.x)[i];
+            // [sh_tokens][K + 4]: the rows padded by 16 bytes, so that the 16 lanes of a lane group, one
+            // token each, read the same offsets of 16 rows from different banks.  The flat copy advances
+            // its (token, column) pair with the index instead of dividing it.
+            float *sx = reinterpret_cast<float *>(smem);
+            const int k4 = a.K / 4, nx4 = a.sh_tokens * k4;
+            int xt = tid / k4, xj = tid - xt * k4;
+            for (int i = tid; i < nx4; i += kSThreads) {
+                reinterpret_cast<float4 *>(sx)[xt * (k4 + 1) + xj] = reinterpret_cast<const float4 *>(a.x)[i];
+                xj += kSThreads;
+                while (xj >= k4) {
+                    xj -= k4;
+                    ++xt;
+                }
+            }
             __syncthreads();
-            const float *xrow = sx + min(n, a.sh_tokens - 1) * a.K + 8 * g;
+            const float *xrow = sx + min(n, a.sh_tokens - 1) * (a.K + 4) + 8 * g;
             f32x4 D[kSharedMaxTiles];
 #pragma unroll
             for (int t = 0; t < kSharedMaxTiles; ++t) D[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1161,7 +1172,7 @@ hipError_t moe_grouped(int gu_type, const uint8_t *wg, const uint8_t *wu, size_t
         const int per_wg = std::max(1, std::min(QLIN_SHARED_TILES, kSharedMaxTiles));
         if (shared && shared->rows > 0 && tokens <= 16 && (sh_tiles + per_wg - 1) / per_wg <= up.grid &&
             shared->rb % 16 == 0 && al16(shared->wg) && al16(shared->wu) &&
-            up.lds >= std::max(per_wg * kSharedPartBytes, static_cast<size_t>(tokens) * K * sizeof(float))) {
+            up.lds >= std::max(per_wg * kSharedPartBytes, static_cast<size_t>(tokens) * (K + 4) * sizeof(float))) {
             ua.sh_wg = shared->wg;
             ua.sh_wu = shared->wu;
             ua.sh_rb = shared->rb;
