@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 import subprocess
+import threading
 
 import numpy as np
 
@@ -22,6 +23,7 @@ BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (
 NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 
 _lib = None
+_lib_lock = threading.Lock()
 
 
 def build() -> None:
@@ -29,12 +31,18 @@ def build() -> None:
 
 
 def lib() -> C.CDLL:
+    """The loaded library, its signatures declared.  Safe from several threads at once: the library is
+    published only after every signature is set (a call through an undeclared function would pass its
+    pointer arguments as 32-bit ints)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            build()
-        _lib = C.CDLL(LIB_PATH)
-        _declare(_lib)
+        with _lib_lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    build()
+                L = C.CDLL(LIB_PATH)
+                _declare(L)
+                _lib = L
     return _lib
 
 

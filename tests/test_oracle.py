@@ -358,3 +358,35 @@ def test_argmax_lowest_index_on_ties(orc):
     v = np.array([1, 5, np.nan, 5, -np.inf, 2], np.float32)
     assert orc.argmax(v) == 1
     assert orc.argmax(np.full(5, -np.inf, np.float32)) == 0
+
+
+def test_first_use_from_threads():
+    """The first calls into the oracle's library may come from a thread pool (the CPU baseline legs
+    do this); each must see the declared signatures: a call through a function whose argument types
+    are not yet set passes its pointers as 32-bit ints and crashes.  Fresh interpreters (the library
+    not yet loaded; a crash shows as a status, not as the test runner's end), 16 threads released
+    together, and a tiny thread switch interval so a switch lands inside the loader."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    code = (
+        "import sys; sys.path[:0] = [%r, %r]\n"
+        "sys.setswitchinterval(1e-6)\n"
+        "import threading, numpy as np, oracle\n"
+        "from concurrent.futures import ThreadPoolExecutor\n"
+        "h = np.arange(4096, dtype=np.uint16)\n"
+        "ref = h.view(np.float16).astype(np.float32)\n"
+        "gate = threading.Barrier(16)\n"
+        "def one(_):\n"
+        "    gate.wait()\n"
+        "    got = oracle.f16_to_f32(h)\n"
+        "    return bool(np.array_equal(got[:1024], ref[:1024]))\n"
+        "with ThreadPoolExecutor(16) as ex:\n"
+        "    ok = list(ex.map(one, range(16)))\n"
+        "assert all(ok)\n"
+    ) % (os.path.join(root, "oracle"), root)
+    for _ in range(6):
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, (r.returncode, r.stderr[-2000:])
