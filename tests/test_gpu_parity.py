@@ -106,7 +106,7 @@ GEMV_CASES = [
     (Q4_0, 18944, 3584), (Q4_0, 3584, 18944), (Q4_0, 5, 64), (Q4_0, 17, 256), (Q4_0, 300, 4608),
     (Q5_0, 2048, 1408), (Q5_0, 5, 64), (Q5_0, 300, 4096), (Q5_0, 33, 128), (Q5_0, 100, 18944),
     (Q6_K, 64, 512), (Q6_K, 257, 2048), (Q6_K, 16384, 2048), (Q6_K, 33, 768), (Q6_K, 100, 7168),
-    # K > 8192: the bf16 (not int8) operands, rows of dwords (18944) and of 16-byte units (14336)
+    # long K on the int8 form, whose row stride is then a multiple of 4 bytes (18944) or of 16 (14336)
     (Q6_K, 100, 18944), (Q6_K, 64, 14336),
 ]
 
