@@ -455,13 +455,14 @@ __global__ __launch_bounds__(threads_for(SWIGLU)) void mfma_gemv_kernel(const fl
             // Lane group g = 2h + s takes positions 16s .. 16s + 15 of all four 32-element column groups c
             // of half h: ql bytes o = 64h + 16s (c = 0, 2: low and high nibbles) and o + 32 (c = 1, 3), qh
             // bytes c0 = 128 + 32h + 16s (bits 2c, 2c + 1), and the half's scales sc[8h + 2c + s]; no byte
-            // is read by two lane groups.  Rows are whole dwords (an even number of super-blocks), so even
+            // is read by two lane groups.  Rows start on dwords (row_bytes a multiple of 4), so even
             // super-blocks start on a dword and odd ones 2 bytes past one.  Every load is dword-aligned:
             // the three pieces and 12 bytes at 192 + 8h, all from 2 bytes before them in an odd
             // super-block.  The 12 bytes hold the half's 8 scales and, for h = 1, d; at their end an even
-            // super-block's h = 1 lanes read the next super-block's first 2 bytes, which exist (a row's last
-            // super-block is odd).  An odd super-block's pieces then lack their last 2 bytes: the first
-            // dword that another lane group of the row loaded (process).
+            // super-block's h = 1 lanes read the 2 bytes after it, which exist: the next super-block's, or
+            // the row's padding (a packed row has an even count, so its last super-block is odd; with an
+            // odd count row_bytes is at least 2 past the packed size).  An odd super-block's pieces then
+            // lack their last 2 bytes: the first dword that another lane group of the row loaded (process).
             const int h = g >> 1, o = 64 * h + 16 * (g & 1), c0 = 128 + 32 * h + 16 * (g & 1);
             const uint8_t *qa = q - ((__builtin_amdgcn_readfirstlane(p.sb) & 1) ? 2 : 0);
             const u32x4 la = ld16_a4(qa + o), lb = ld16_a4(qa + o + 32), qh = ld16_a4(qa + c0);
@@ -1331,6 +1332,10 @@ bool mfma_routed_ok(int type, bool swiglu, const uint8_t *w0, const uint8_t *w1,
     }
     // the down projection: rows = hidden, k = ffn per route; route_of(chunk) for every chunk
     const int cpr = k / chunk_elems(type);
+    // Q6_K's load takes a super-block's dword offset (0 or 2) from its step index, which in the routed
+    // down counts the routes' chunks end to end: that is the super-block's parity in its row only when a
+    // route has an even number of them (an odd one needs a padded row_bytes to pass the checks above)
+    if (type == T_Q6_K && cpr % 2) return false;
     if (static_cast<uint64_t>(routes) * cpr * cpr >= lim) return false;
     a = down_routed_args(type, w0, eb, rb, x, nullptr, nullptr, nullptr, routes, rows, k);
     return prepare(type, a, routes * k, false, true).ok;

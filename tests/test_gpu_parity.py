@@ -1108,3 +1108,42 @@ def test_gemv_multi_generic_types():
     qlin.quant_gemv_multi(Q8_0, [dev(w) for w, _, _ in mats], mats[0][1], dev(x), ys, [33, 64], 512)
     for (w, rb, _), y, n in zip(mats, ys, (33, 64)):
         assert normwise_rel_err(host(y), orc.matmul_f64(Q8_0, w, rb, x, n, 512)[0]) <= FP32
+
+
+def _pad_rows(w, rows, rb, prb):
+    """w's rows (rb bytes each) at a stride of prb bytes, the gap filled with 0xA5."""
+    out = np.full((rows, prb), 0xA5, np.uint8)
+    out[:, :rb] = w.reshape(rows, rb)
+    return out.reshape(-1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ffn,extra", [(768, 2), (1024, 4), (1280, 6)])
+def test_q6k_padded_rows(ffn, extra):
+    """Q6_K rows at a stride past their packed size, a multiple of 4 bytes (so the matrix-core checks
+    pass), with an odd or even number of super-blocks per row: the GEMV and the routed down in route
+    order (launch_quant_down_f32_indexed_accum_ordered, kernel.cu:1363-1385), every route of every
+    parity, against the oracle at the same stride."""
+    E, hid = 8, 96
+    w, rb, vals = qgen.random_matrix(Q6_K, E * hid, ffn, seed=ffn + 7)
+    prb = rb + extra
+    assert prb % 4 == 0
+    wp = _pad_rows(w, E * hid, rb, prb)
+    banner(f"q6k padded rows ffn={ffn} rb={rb} stride={prb}")
+    x = qgen.random_x(1, ffn, seed=ffn)
+    y = gpu_gemv(Q6_K, wp, prb, x, E * hid, ffn)
+    ref = orc.matmul_f64(Q6_K, wp, prb, x, E * hid, ffn)
+    assert normwise_rel_err(y, ref) <= GATE
+    assert cond_err(y, ref, vals, x) <= COND
+    ids = np.array([3, 0, 7, 5, 1, -1, 6], np.int32)
+    k = ids.size
+    rw = np.linspace(0.3, 0.05, k).astype(np.float32)
+    act = np.random.default_rng(ffn).standard_normal((k, ffn)).astype(np.float32)
+    out0 = np.random.default_rng(ffn + 1).standard_normal(hid).astype(np.float32)
+    out_d = dev(out0)
+    qlin.call("qlin_launch_quant_down_f32_indexed_accum_ordered", Q6_K, dev(wp), hid * prb, prb, dev(act), dev(ids),
+              dev(rw), out_d, k, hid, ffn)
+    ref = orc.down_indexed_ordered(Q6_K, wp, hid * prb, prb, act, ids, rw, out0, hid, ffn)
+    got = host(out_d)
+    assert normwise_rel_err(got - out0, ref - out0) <= 1e-4
+    assert normwise_rel_err(got, ref) <= FP32
